@@ -1,0 +1,257 @@
+"""Benchmark of the Chunked Greedy hot path on one MI355X.
+
+Metric: reorder time (ms) + reordered vs original SpMM GB/s,
+N=32..256, 1 GPU.  Workload: configuration C2 (planted blocks, n = 2^20,
+16 nnz/row, 16,777,216 nnz), synthetic and seeded, generated on the host and
+resident in HBM before timing starts.
+
+One step = csg reorder (sporder.chunk_similarity_greedy) + symmetric
+permutation apply with values (sporder.reorder) + CSR SpMM at N=128 on the
+reordered matrix.  W untimed steps, then K timed steps between
+torch.cuda.synchronize() calls -> ms_per_step.
+
+Reported beside it (same run):
+  - reorder wall_ms, median of 5 timed calls after a 1 GiB cache flush each
+    (the reference harness protocol, bench/reorder/reorder_bench/methods/
+    sporder_csg.py:41-57), with the stage spans;
+  - SpMM kernel time per launch (warmup 30, 100 iterations, HIP events on the
+    library stream; bench/spmm/spmm_bench/batch_bench.py:229-231) for the
+    original and the reordered matrix at N = 32 and 128, as algorithmic GB/s
+    with B_spmm(N) = 4(n+1) + 8 nnz + 8 n N bytes;
+  - value = reordered SpMM GB/s at N = 128;
+  - roofline of the dominant kernel (largest share of the step) against
+    8 TB/s, and cpu_baseline: the oracle (C++/OpenMP restatement of csg and a
+    CSR SpMM in the same fmaf order) on the host cores.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+import numpy as np
+
+HBM_PEAK_GBS = 8000.0
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def spmm_bytes(n, nnz, N):
+    return 4 * (n + 1) + 8 * nnz + 8 * n * N
+
+
+def reorder_bytes(n, nnz, k, symmetric):
+    b = 2 * (4 * (n + 1) + 4 * nnz) + 8 * n * k   # sketch: CSR + CSC reads, table write
+    b += 8 * n * k + 4 * n                         # greedy: table read, order write
+    if not symmetric:
+        b += 2 * (4 * (n + 1) + 4 * nnz)           # transpose
+    return b
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--seed", type=int, default=2)
+    ap.add_argument("--rows", type=int, default=1 << 20, help="C2 row count (default 2^20)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--spmm-iters", type=int, default=100)
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: the Chunked Greedy path has no multi-GPU "
+              "execution in this build (chunks shard by row range; see DESIGN.md)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from chunkedgreedy_amd import sporder, synth
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    n_rows = args.rows
+    blocks = n_rows // 64
+    t0 = time.time()
+    ptr_h, ind_h, val_h = synth.config2(seed=args.seed, n=n_rows, blocks=blocks)
+    n = ptr_h.shape[0] - 1
+    nnz = int(ind_h.shape[0])
+    is_sym = synth.is_pattern_symmetric(ptr_h, ind_h)
+    log(f"generated C2 n={n} nnz={nnz} symmetric={is_sym} in {time.time() - t0:.1f}s")
+
+    ptr = torch.from_numpy(ptr_h).to(dev)
+    ind = torch.from_numpy(ind_h).to(dev)
+    val = torch.from_numpy(val_h).to(dev)
+    gen = torch.Generator(device=dev).manual_seed(42)
+    B128 = torch.randn((n, 128), generator=gen, dtype=torch.float32, device=dev)
+    gen = torch.Generator(device=dev).manual_seed(42)
+    B32 = torch.randn((n, 32), generator=gen, dtype=torch.float32, device=dev)
+    ctx = sporder.Context()
+    out128 = torch.empty((n, 128), dtype=torch.float32, device=dev)
+
+    def step():
+        order = sporder.chunk_similarity_greedy(ptr, ind, is_symmetric=is_sym, ctx=ctx)
+        p2, i2, v2 = sporder.reorder(ptr, ind, order, val=val, symmetric=True, ctx=ctx)
+        sporder.spmm_csr(p2, i2, v2, B128, out=out128, ctx=ctx)
+        return order, (p2, i2, v2)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        order, reordered = step()
+    torch.cuda.synchronize()
+    ms_per_step = (time.perf_counter() - t0) * 1e3 / max(args.steps, 1)
+    log(f"step {ms_per_step:.3f} ms")
+
+    # Reorder protocol: flush, timed call with timing; median of 5.
+    flush = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    walls, spans = [], []
+    for _ in range(5):
+        flush.zero_()
+        torch.cuda.synchronize()
+        _, timing = sporder.chunk_similarity_greedy(ptr, ind, is_symmetric=is_sym,
+                                                    with_timing=True, ctx=ctx)
+        walls.append(timing["wall_ms"])
+        spans.append(timing)
+    del flush
+    med = statistics.median(walls)
+    span = spans[walls.index(med)] if med in walls else spans[0]
+    _, stats = sporder.chunk_similarity_greedy(ptr, ind, is_symmetric=is_sym, with_stats=True,
+                                               ctx=ctx)
+    log(f"reorder wall median {med:.3f} ms spans {span}")
+
+    # Permutation apply timing (events around the call).
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    perm_ms = []
+    for _ in range(5):
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        sporder.reorder(ptr, ind, order, val=val, symmetric=True, ctx=ctx)
+        perm_ms.append((time.perf_counter() - t1) * 1e3)
+    perm_med = statistics.median(perm_ms)
+
+    # SpMM per-launch kernel time, original vs reordered.
+    p2, i2, v2 = reordered
+
+    def spmm_ms(p, i, v, B):
+        out = torch.empty((n, B.shape[1]), dtype=torch.float32, device=dev)
+        for _ in range(30):
+            sporder.spmm_csr(p, i, v, B, out=out, ctx=ctx)
+        tot = 0.0
+        for _ in range(args.spmm_iters):
+            _, ms = sporder.spmm_csr(p, i, v, B, out=out, ctx=ctx)
+            tot += ms
+        return tot / args.spmm_iters
+
+    spmm = {}
+    for N, B in ((32, B32), (128, B128)):
+        t_orig = spmm_ms(ptr, ind, val, B)
+        t_re = spmm_ms(p2, i2, v2, B)
+        bts = spmm_bytes(n, nnz, N)
+        spmm[str(N)] = {
+            "orig_ms": round(t_orig, 4), "reordered_ms": round(t_re, 4),
+            "orig_gbs": round(bts / t_orig / 1e6, 1),
+            "reordered_gbs": round(bts / t_re / 1e6, 1),
+            "bytes": bts,
+        }
+        log(f"spmm N={N}: orig {t_orig:.3f} ms, reordered {t_re:.3f} ms")
+
+    k_used = stats["k_used"]
+    # Dominant kernel of the step: compare the stage spans with the SpMM.
+    stage = {
+        "csg_sketch": span["similarity_ms"],
+        "csg_greedy": span["chunk_greedy_ms"],
+        "csr2csc": span["csr2csc_ms"],
+        "spmm_rowsplit_n128": spmm["128"]["reordered_ms"],
+    }
+    dom = max(stage, key=stage.get)
+    algo_bytes = {
+        "csg_sketch": 2 * (4 * (n + 1) + 4 * nnz) + 8 * n * k_used,
+        "csg_greedy": 8 * n * k_used + 4 * n,
+        "csr2csc": 2 * (4 * (n + 1) + 4 * nnz),
+        "spmm_rowsplit_n128": spmm_bytes(n, nnz, 128),
+    }
+    achieved = algo_bytes[dom] / (stage[dom] * 1e-3) / 1e9
+    roofline = {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 1),
+                "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "algorithmic_bytes": algo_bytes[dom], "avg_ms": round(stage[dom], 4)}
+    spmm_ach = spmm["128"]["reordered_gbs"]
+    roofline_spmm = {"kernel": "spmm_rowsplit_n128", "bound": "hbm", "achieved": spmm_ach,
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(spmm_ach / HBM_PEAK_GBS, 4)}
+    reorder_gbs = reorder_bytes(n, nnz, k_used, is_sym) / (med * 1e-3) / 1e9
+
+    cpu = None
+    if not args.no_cpu:
+        import oracle
+
+        threads = min(os.cpu_count() or 1, 16)
+        oracle.set_num_threads(threads)
+        log(f"cpu baseline on {threads} threads")
+        cpu_reorder = []
+        for _ in range(3):
+            t1 = time.perf_counter()
+            o_order, _ = oracle.chunk_similarity_greedy(ptr_h, ind_h, is_symmetric=is_sym)
+            cpu_reorder.append((time.perf_counter() - t1) * 1e3)
+        parity = bool(np.array_equal(o_order, order.cpu().numpy()))
+        B_h = B128.cpu().numpy()
+        p2h, i2h, v2h = (x.cpu().numpy() for x in reordered)
+        cpu_spmm = []
+        for _ in range(3):
+            t1 = time.perf_counter()
+            oracle.spmm_csr(p2h, i2h, v2h, B_h)
+            cpu_spmm.append((time.perf_counter() - t1) * 1e3)
+        cs = statistics.median(cpu_spmm)
+        cpu = {"value": round(spmm_bytes(n, nnz, 128) / (cs * 1e-3) / 1e9, 2), "unit": "GB/s",
+               "cores": threads, "kind": "port",
+               "sample": "full C2: oracle CSR SpMM N=128 on the reordered matrix (median of 3)"
+                         "; csg reorder by the oracle on full C2 (median of 3)",
+               "reorder_ms": round(statistics.median(cpu_reorder), 2),
+               "spmm_ms": round(cs, 2), "permutation_bit_exact_vs_gpu": parity}
+
+    out = {
+        "metric": "reorder time (ms) + reordered vs original SpMM GB/s, N=32..256, 1 GPU",
+        "value": spmm["128"]["reordered_gbs"],
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic",
+        "config": {"workload": "C2 planted blocks", "n": n, "nnz": nnz, "blocks": blocks,
+                   "nnz_per_row": 16, "spmm_N": [32, 128], "k": k_used,
+                   "m": stats["m_used"], "chunk_size": stats["chunk_size_used"],
+                   "seed": args.seed, "is_symmetric": is_sym},
+        "reorder_ms": round(med, 4),
+        "reorder_spans_ms": {k: round(v, 4) for k, v in span.items() if k != "wall_ms"},
+        "reorder_gbs": round(reorder_gbs, 1),
+        "permute_ms": round(perm_med, 4),
+        "spmm": spmm,
+        "csg_stats": stats,
+        "roofline": roofline,
+        "roofline_spmm": roofline_spmm,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

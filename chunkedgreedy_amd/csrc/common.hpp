@@ -1,0 +1,219 @@
+// common.hpp -- runtime pieces shared by every kernel file of
+// libsporder_hip.so: error handling (abort with a diagnostic, as the
+// reference's ensure/expect do, sporder/src/common/error_checking.h:12-61),
+// the context (private stream + device facts + grow-only workspace; the
+// reference's counterpart is sporder/src/common/context.h:67-197), event
+// timers (sporder/src/common/timer.h:12-51) and wave64 helpers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+
+#include "sporder.h"
+
+namespace sporder_hip {
+
+[[noreturn]] void fail_hip(hipError_t err, const char *expr, const char *file,
+                           int line);
+[[noreturn]] void fail_expect(const char *msg, const char *file, int line);
+
+#define SP_HIP(expr)                                                           \
+  do {                                                                         \
+    hipError_t sp_err_ = (expr);                                               \
+    if (sp_err_ != hipSuccess) {                                               \
+      ::sporder_hip::fail_hip(sp_err_, #expr, __FILE__, __LINE__);             \
+    }                                                                          \
+  } while (0)
+
+#define SP_EXPECT(cond, msg)                                                   \
+  do {                                                                         \
+    if (!(cond)) {                                                             \
+      ::sporder_hip::fail_expect(msg, __FILE__, __LINE__);                     \
+    }                                                                          \
+  } while (0)
+
+#define SP_LAUNCH_CHECK() SP_HIP(hipGetLastError())
+
+constexpr int kWave = 64;
+
+inline int64_t ceil_div64(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Bump allocator over a grow-only device buffer owned by the context.
+// reserve() must be called with the call's total before any take().
+struct Workspace {
+  void *base = nullptr;
+  size_t capacity = 0;
+  size_t offset = 0;
+
+  static size_t align(size_t bytes) { return (bytes + 255u) & ~size_t(255u); }
+};
+
+struct Context {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  int num_cus = 0;
+  int max_threads_per_cu = 0;
+  size_t lds_per_block = 0;
+  Workspace ws;
+  hipEvent_t ev[8] = {};
+
+  void init();
+  void destroy();
+  void sync() { SP_HIP(hipStreamSynchronize(stream)); }
+
+  // Grow the workspace to hold `bytes` (rounded), then reset the cursor.
+  void reserve(size_t bytes);
+  template <typename T> T *take(size_t count) {
+    size_t bytes = Workspace::align(count * sizeof(T) + (count == 0 ? 1 : 0));
+    SP_EXPECT(ws.offset + bytes <= ws.capacity,
+              "workspace overflow (internal sizing error)");
+    T *p = reinterpret_cast<T *>(static_cast<char *>(ws.base) + ws.offset);
+    ws.offset += bytes;
+    return p;
+  }
+  // Blocks for a grid-stride kernel: at least `min_blocks`, at most what
+  // `waves` full passes of the device at `block` threads per block holds.
+  int grid_for(int64_t work_blocks, int block, int waves = 4) const {
+    int64_t cap = static_cast<int64_t>(num_cus) * max_threads_per_cu * waves /
+                  block;
+    if (cap < 1) cap = 1;
+    int64_t g = work_blocks < cap ? work_blocks : cap;
+    return static_cast<int>(g < 1 ? 1 : g);
+  }
+};
+
+// Bytes a workspace request of `count` T's occupies (for reserve sums).
+template <typename T> inline size_t ws_bytes(size_t count) {
+  return Workspace::align(count * sizeof(T) + (count == 0 ? 1 : 0));
+}
+
+// One timed span on the library stream (begin/end are stream-ordered).
+struct EventSpan {
+  hipEvent_t a = nullptr, b = nullptr;
+  bool on = false;
+  void create(bool enable) {
+    on = enable;
+    if (on) {
+      SP_HIP(hipEventCreate(&a));
+      SP_HIP(hipEventCreate(&b));
+    }
+  }
+  void begin(hipStream_t s) {
+    if (on) SP_HIP(hipEventRecord(a, s));
+  }
+  void end(hipStream_t s) {
+    if (on) SP_HIP(hipEventRecord(b, s));
+  }
+  float ms() const {
+    float t = 0.0f;
+    if (on) SP_HIP(hipEventElapsedTime(&t, a, b));
+    return t;
+  }
+  void destroy() {
+    if (on) {
+      SP_HIP(hipEventDestroy(a));
+      SP_HIP(hipEventDestroy(b));
+      on = false;
+    }
+  }
+};
+
+// ---- host-side stages shared between files -------------------------------
+
+// In-place exclusive (inclusive=false) or inclusive scan of `count` int32
+// values; `tmp` must hold scan_tmp_elems(count) int32.
+size_t scan_tmp_elems(int64_t count);
+void scan_i32(Context &ctx, const int32_t *in, int32_t *out, int64_t count,
+              bool inclusive, int32_t *tmp);
+
+// Stable LSD radix sort of (key, value) pairs on the low `key_bits` bits.
+// Input in keys_in/vals_in (preserved), result in keys_out/vals_out; the
+// alt buffers are ping-pong space of `count` elements each; `tmp` must hold
+// radix_tmp_elems(count) int32.
+size_t radix_tmp_elems(int64_t count);
+void radix_sort_pairs(Context &ctx, const uint32_t *keys_in,
+                      const uint32_t *vals_in, uint32_t *keys_out,
+                      uint32_t *vals_out, uint32_t *keys_alt,
+                      uint32_t *vals_alt, int64_t count, int key_bits,
+                      int32_t *tmp);
+
+// Stable CSR -> CSC transpose (rows ascending within each column).
+// Workspace needed: csr2csc_ws_bytes(n, nnz).
+size_t csr2csc_ws_bytes(int32_t n, int32_t nnz);
+void csr2csc(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
+             const int32_t *d_ind, int32_t *d_col_ptr, int32_t *d_row_ind);
+
+// Chunk-restricted sketch + top-k table (u64 weighted_index, n*k).
+void chunk_sketch_top_k(Context &ctx, int32_t n, int32_t k, int32_t chunk_size,
+                        int32_t m_capacity, const int32_t *d_ptr,
+                        const int32_t *d_ind, const int32_t *d_col_ptr,
+                        const int32_t *d_row_ind, uint64_t *d_table);
+
+// Degree / weight totals of a top-k table (reference
+// sporder/src/common/similarity_top_k.cu:120-172).
+struct TopKTotals {
+  unsigned long long total_degree;
+  double total_weight;
+  int32_t zero_degree_rows;
+  int32_t pad;
+};
+void top_k_stats(Context &ctx, int32_t n, int32_t k, const uint64_t *d_table,
+                 TopKTotals *d_totals);
+
+int bits_for(int64_t max_value);
+
+// Set `count` u32 words to `value` with a kernel on the library stream
+// (a kernel rather than a memset node, so a captured call stays correct).
+void fill_u32(Context &ctx, void *p, int64_t count, uint32_t value);
+
+// ---- device helpers --------------------------------------------------------
+
+__device__ __forceinline__ int lane_id() { return __lane_id(); }
+
+__device__ __forceinline__ uint64_t ballot(bool p) { return __ballot(p); }
+
+__device__ __forceinline__ int32_t readlane(int32_t v, int lane) {
+  return __builtin_amdgcn_readlane(v, lane);
+}
+__device__ __forceinline__ float readlane_f(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// Inclusive prefix sum across the 64 lanes of a wave.
+__device__ __forceinline__ int32_t wave_incl_scan(int32_t v) {
+  int l = lane_id();
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    int32_t o = __shfl_up(v, off, kWave);
+    if (l >= off) v += o;
+  }
+  return v;
+}
+
+__device__ __forceinline__ int32_t wave_sum(int32_t v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+// weighted_index packing (reference sporder/src/common/weighted_index.h:15-27).
+__device__ __forceinline__ uint64_t pack_wi(int32_t index, float weight) {
+  return (static_cast<uint64_t>(__float_as_uint(weight)) << 32) |
+         static_cast<uint32_t>(index + 1);
+}
+__device__ __forceinline__ int32_t wi_index(uint64_t v) {
+  return static_cast<int32_t>(static_cast<uint32_t>(v)) - 1;
+}
+__device__ __forceinline__ float wi_weight(uint64_t v) {
+  return __uint_as_float(static_cast<uint32_t>(v >> 32));
+}
+
+} // namespace sporder_hip
+
+struct sporder_context_struct {
+  sporder_hip::Context impl;
+};

@@ -1,0 +1,109 @@
+// context.hip -- context lifecycle, error reporting and the workspace.
+// Reference counterparts: sporder/src/common/context.h:67-197 (stream,
+// device facts, stream-ordered allocation) and error_checking.h:21-61
+// (abort with a file:line diagnostic).  Instead of per-call stream-ordered
+// allocations this library keeps one grow-only workspace per context, so a
+// steady-state call (same or smaller problem) performs no allocation.
+#include "common.hpp"
+
+namespace sporder_hip {
+
+void fail_hip(hipError_t err, const char *expr, const char *file, int line) {
+  std::fprintf(stderr, "%s:%d: HIP error in %s: %s\n", file, line, expr,
+               hipGetErrorString(err));
+  std::fflush(stderr);
+  std::abort();
+}
+
+void fail_expect(const char *msg, const char *file, int line) {
+  std::fprintf(stderr, "%s:%d: expect failed - %s\n", file, line, msg);
+  std::fflush(stderr);
+  std::abort();
+}
+
+void Context::init() {
+  SP_HIP(hipGetDevice(&device));
+  SP_HIP(hipStreamCreate(&stream));
+  SP_HIP(hipDeviceGetAttribute(&num_cus, hipDeviceAttributeMultiprocessorCount,
+                               device));
+  SP_HIP(hipDeviceGetAttribute(&max_threads_per_cu,
+                               hipDeviceAttributeMaxThreadsPerMultiProcessor,
+                               device));
+  int lds = 0;
+  SP_HIP(hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock,
+                               device));
+  lds_per_block = static_cast<size_t>(lds);
+}
+
+void Context::destroy() {
+  int cur = 0;
+  SP_HIP(hipGetDevice(&cur));
+  SP_HIP(hipSetDevice(device));
+  SP_HIP(hipStreamSynchronize(stream));
+  if (ws.base) {
+    SP_HIP(hipFree(ws.base));
+    ws.base = nullptr;
+  }
+  SP_HIP(hipStreamDestroy(stream));
+  SP_HIP(hipSetDevice(cur));
+}
+
+void Context::reserve(size_t bytes) {
+  bytes = Workspace::align(bytes + 256);
+  if (bytes > ws.capacity) {
+    // Pending work may still read the old buffer.
+    SP_HIP(hipStreamSynchronize(stream));
+    if (ws.base) {
+      SP_HIP(hipFree(ws.base));
+      ws.base = nullptr;
+    }
+    // Grow geometrically so that a sequence of slightly larger calls does not
+    // reallocate each time.
+    size_t grown = ws.capacity + ws.capacity / 2;
+    size_t cap = bytes > grown ? bytes : grown;
+    SP_HIP(hipMalloc(&ws.base, cap));
+    ws.capacity = cap;
+  }
+  ws.offset = 0;
+}
+
+namespace {
+__global__ void fill_u32_kernel(uint32_t *p, int64_t count, uint32_t value) {
+  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+       i < count; i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    p[i] = value;
+  }
+}
+} // namespace
+
+void fill_u32(Context &ctx, void *p, int64_t count, uint32_t value) {
+  if (count <= 0) return;
+  int g = ctx.grid_for(ceil_div64(count, 256), 256, 2);
+  fill_u32_kernel<<<g, 256, 0, ctx.stream>>>(static_cast<uint32_t *>(p), count,
+                                             value);
+  SP_LAUNCH_CHECK();
+}
+
+int bits_for(int64_t max_value) {
+  int b = 0;
+  while (b < 63 && (int64_t(1) << b) <= max_value) ++b;
+  return b;
+}
+
+} // namespace sporder_hip
+
+extern "C" {
+
+sporder_context_t sporder_context_create(void) {
+  auto *h = new sporder_context_struct;
+  h->impl.init();
+  return h;
+}
+
+void sporder_context_destroy(sporder_context_t h) {
+  if (!h) return;
+  h->impl.destroy();
+  delete h;
+}
+
+} // extern "C"

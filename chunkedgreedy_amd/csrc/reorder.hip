@@ -1,0 +1,281 @@
+// reorder.hip -- permutation apply (sporder_reorder).
+//
+// Reference: sporder/src/reorder.cu:72-149 and bridge sporder/src/sporder.cpp:49-60.
+//   ROWS:      ptr_new = scan of gathered row lengths; row p = old row
+//              new_order[p] copied verbatim (values alongside).
+//   SYMMETRIC: additionally old2new = inverse(new_order), columns mapped
+//              through it, and every row re-sorted by column with its values.
+//
+// The reference sorts rows with cub::DeviceSegmentedSort.  Here rows are
+// sorted by size class: up to 64 entries in one wave (register bitonic network
+// over lanes), up to kBlockSortCap entries in one workgroup (LDS bitonic), and
+// longer rows with the library's stable radix sort, one row at a time.  Column
+// keys of a valid permutation are distinct within a row, so every method gives
+// the same (unique) sorted result.
+#include "common.hpp"
+
+#include <algorithm>
+#include <vector>
+
+namespace sporder_hip {
+
+namespace {
+
+constexpr int kBlockSortCap = 4096;
+constexpr int kBlockSortThreads = 256;
+
+__global__ void gather_row_lengths(int32_t n, const int32_t *__restrict__ ptr_old,
+                                   const int32_t *__restrict__ new2old,
+                                   int32_t *__restrict__ ptr_new) {
+  for (int64_t p = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+       p < n; p += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    int32_t o = new2old[p];
+    ptr_new[p + 1] = ptr_old[o + 1] - ptr_old[o];
+    if (p == 0) ptr_new[0] = 0;
+  }
+}
+
+__global__ void invert_perm(int32_t n, const int32_t *__restrict__ src,
+                            int32_t *__restrict__ dst) {
+  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+       i < n; i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    dst[src[i]] = static_cast<int32_t>(i);
+  }
+}
+
+// One wave per new row: copy the source row's columns (optionally mapped by
+// col_map) and values.  With val_new set and val_old NULL the values written
+// are 0.0f, as in the reference's gather_rows (reorder.cu:37-45).
+__global__ void gather_rows(int32_t n, const int32_t *__restrict__ ptr_old,
+                            const int32_t *__restrict__ ind_old,
+                            const float *__restrict__ val_old,
+                            const int32_t *__restrict__ new2old,
+                            const int32_t *__restrict__ col_map,
+                            const int32_t *__restrict__ ptr_new,
+                            int32_t *__restrict__ ind_new,
+                            float *__restrict__ val_new) {
+  const int lane = lane_id();
+  const int64_t wave0 = (blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x) / kWave;
+  const int64_t nwaves = static_cast<int64_t>(gridDim.x) * blockDim.x / kWave;
+  for (int64_t p = wave0; p < n; p += nwaves) {
+    int32_t o = new2old[p];
+    int32_t src = ptr_old[o], src_end = ptr_old[o + 1];
+    int32_t dst = ptr_new[p];
+    for (int32_t q = src + lane; q < src_end; q += kWave) {
+      int32_t c = ind_old[q];
+      int32_t off = dst + (q - src);
+      ind_new[off] = col_map ? col_map[c] : c;
+      if (val_new) val_new[off] = val_old ? val_old[q] : 0.0f;
+    }
+  }
+}
+
+// Rows of up to 64 entries: bitonic network across the lanes of one wave.
+// Longer rows are appended to `long_rows` for the next stages.
+__global__ void sort_rows_wave(int32_t n, const int32_t *__restrict__ ptr,
+                               const int32_t *__restrict__ key_in,
+                               const float *__restrict__ val_in,
+                               int32_t *__restrict__ key_out,
+                               float *__restrict__ val_out,
+                               int32_t *__restrict__ long_rows,
+                               int32_t *__restrict__ long_count) {
+  const int lane = lane_id();
+  const int64_t wave0 = (blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x) / kWave;
+  const int64_t nwaves = static_cast<int64_t>(gridDim.x) * blockDim.x / kWave;
+  for (int64_t r = wave0; r < n; r += nwaves) {
+    int32_t s = ptr[r], e = ptr[r + 1], len = e - s;
+    if (len > kWave) {
+      if (lane == 0) long_rows[atomicAdd(long_count, 1)] = static_cast<int32_t>(r);
+      continue;
+    }
+    if (len == 0) continue;
+    bool in = lane < len;
+    int32_t key = in ? key_in[s + lane] : 0x7fffffff;
+    float val = (in && val_in) ? val_in[s + lane] : 0.0f;
+#pragma unroll
+    for (int kk = 2; kk <= kWave; kk <<= 1) {
+#pragma unroll
+      for (int j = kk >> 1; j > 0; j >>= 1) {
+        int32_t ok = __shfl_xor(key, j, kWave);
+        float ov = __shfl_xor(val, j, kWave);
+        bool ascending = (lane & kk) == 0;
+        bool lower = (lane & j) == 0;
+        bool take = (ascending == lower) ? (ok < key) : (ok > key);
+        if (take) {
+          key = ok;
+          val = ov;
+        }
+      }
+    }
+    if (in) {
+      key_out[s + lane] = key;
+      if (val_out) val_out[s + lane] = val;
+    }
+  }
+}
+
+// Rows of 65..kBlockSortCap entries: LDS bitonic sort, one workgroup per row.
+// Rows beyond the cap are appended to `huge_rows`.
+__global__ void __launch_bounds__(kBlockSortThreads)
+    sort_rows_block(const int32_t *__restrict__ ptr,
+                    const int32_t *__restrict__ long_rows,
+                    const int32_t *__restrict__ long_count,
+                    const int32_t *__restrict__ key_in,
+                    const float *__restrict__ val_in, int32_t *__restrict__ key_out,
+                    float *__restrict__ val_out, int32_t *__restrict__ huge_rows,
+                    int32_t *__restrict__ huge_count) {
+  __shared__ int32_t sk[kBlockSortCap];
+  __shared__ float sv[kBlockSortCap];
+  const int32_t count = *long_count;
+  for (int32_t t = blockIdx.x; t < count; t += gridDim.x) {
+    int32_t r = long_rows[t];
+    int32_t s = ptr[r], e = ptr[r + 1], len = e - s;
+    if (len > kBlockSortCap) {
+      if (threadIdx.x == 0) huge_rows[atomicAdd(huge_count, 1)] = r;
+      continue;
+    }
+    int32_t pow2 = 1;
+    while (pow2 < len) pow2 <<= 1;
+    for (int32_t i = threadIdx.x; i < pow2; i += blockDim.x) {
+      bool in = i < len;
+      sk[i] = in ? key_in[s + i] : 0x7fffffff;
+      sv[i] = (in && val_in) ? val_in[s + i] : 0.0f;
+    }
+    __syncthreads();
+    for (int32_t kk = 2; kk <= pow2; kk <<= 1) {
+      for (int32_t j = kk >> 1; j > 0; j >>= 1) {
+        for (int32_t i = threadIdx.x; i < pow2; i += blockDim.x) {
+          int32_t partner = i ^ j;
+          if (partner > i) {
+            bool ascending = (i & kk) == 0;
+            int32_t a = sk[i], b = sk[partner];
+            if ((a > b) == ascending) {
+              sk[i] = b;
+              sk[partner] = a;
+              float fa = sv[i];
+              sv[i] = sv[partner];
+              sv[partner] = fa;
+            }
+          }
+        }
+        __syncthreads();
+      }
+    }
+    for (int32_t i = threadIdx.x; i < len; i += blockDim.x) {
+      key_out[s + i] = sk[i];
+      if (val_out) val_out[s + i] = sv[i];
+    }
+    __syncthreads();
+  }
+}
+
+} // namespace
+
+} // namespace sporder_hip
+
+using namespace sporder_hip;
+
+extern "C" void sporder_reorder(sporder_context_t h, int32_t n, int32_t nnz,
+                                const int32_t *d_ptr_old, const int32_t *d_ind_old,
+                                const float *d_val_old, const int32_t *d_new_order,
+                                sporder_reorder_mode_t mode, int32_t *d_ptr_new,
+                                int32_t *d_ind_new, float *d_val_new) {
+  SP_EXPECT(h != nullptr, "null context");
+  SP_EXPECT(mode == SPORDER_REORDER_ROWS || mode == SPORDER_REORDER_SYMMETRIC,
+            "invalid reorder mode");
+  SP_EXPECT(n >= 1 && nnz >= 0, "expect n >= 1 and nnz >= 0");
+  Context &ctx = h->impl;
+  const bool symmetric = mode == SPORDER_REORDER_SYMMETRIC;
+  const bool with_vals = d_val_old != nullptr && d_val_new != nullptr;
+
+  size_t need = ws_bytes<int32_t>(scan_tmp_elems(static_cast<int64_t>(n) + 1));
+  if (symmetric) {
+    need += ws_bytes<int32_t>(n) + ws_bytes<int32_t>(nnz) + ws_bytes<float>(nnz) +
+            2 * ws_bytes<int32_t>(static_cast<size_t>(n) + 2) + ws_bytes<int32_t>(2);
+  }
+  ctx.reserve(need);
+  int32_t *scan_tmp = ctx.take<int32_t>(scan_tmp_elems(static_cast<int64_t>(n) + 1));
+
+  const int row_grid = ctx.grid_for(ceil_div64(n, 256), 256, 4);
+  const int wave_grid = ctx.grid_for(ceil_div64(n, 4), 256, 4);
+
+  gather_row_lengths<<<row_grid, 256, 0, ctx.stream>>>(n, d_ptr_old, d_new_order,
+                                                       d_ptr_new);
+  SP_LAUNCH_CHECK();
+  scan_i32(ctx, d_ptr_new, d_ptr_new, static_cast<int64_t>(n) + 1, true, scan_tmp);
+
+  if (!symmetric) {
+    gather_rows<<<wave_grid, 256, 0, ctx.stream>>>(n, d_ptr_old, d_ind_old, d_val_old,
+                                                   d_new_order, nullptr, d_ptr_new,
+                                                   d_ind_new, d_val_new);
+    SP_LAUNCH_CHECK();
+    ctx.sync();
+    return;
+  }
+
+  int32_t *old2new = ctx.take<int32_t>(n);
+  int32_t *unsorted = ctx.take<int32_t>(nnz);
+  float *val_unsorted = ctx.take<float>(nnz);
+  int32_t *long_rows = ctx.take<int32_t>(static_cast<size_t>(n) + 2);
+  int32_t *huge_rows = ctx.take<int32_t>(static_cast<size_t>(n) + 2);
+  int32_t *counts = ctx.take<int32_t>(2);
+
+  invert_perm<<<row_grid, 256, 0, ctx.stream>>>(n, d_new_order, old2new);
+  SP_LAUNCH_CHECK();
+  gather_rows<<<wave_grid, 256, 0, ctx.stream>>>(
+      n, d_ptr_old, d_ind_old, d_val_old, d_new_order, old2new, d_ptr_new, unsorted,
+      with_vals ? val_unsorted : nullptr);
+  SP_LAUNCH_CHECK();
+  fill_u32(ctx, counts, 2, 0u);
+  sort_rows_wave<<<wave_grid, 256, 0, ctx.stream>>>(
+      n, d_ptr_new, unsorted, with_vals ? val_unsorted : nullptr, d_ind_new,
+      with_vals ? d_val_new : nullptr, long_rows, counts);
+  SP_LAUNCH_CHECK();
+  sort_rows_block<<<ctx.num_cus * 4, kBlockSortThreads, 0, ctx.stream>>>(
+      d_ptr_new, long_rows, counts, unsorted, with_vals ? val_unsorted : nullptr,
+      d_ind_new, with_vals ? d_val_new : nullptr, huge_rows, counts + 1);
+  SP_LAUNCH_CHECK();
+
+  int32_t hcount = 0;
+  SP_HIP(hipMemcpyAsync(&hcount, counts + 1, sizeof(int32_t), hipMemcpyDeviceToHost,
+                        ctx.stream));
+  ctx.sync();
+  if (hcount > 0) {
+    // Rows longer than one workgroup's LDS: stable radix sort per row.
+    std::vector<int32_t> rows(hcount), bounds;
+    SP_HIP(hipMemcpy(rows.data(), huge_rows, sizeof(int32_t) * hcount,
+                     hipMemcpyDeviceToHost));
+    bounds.resize(2 * static_cast<size_t>(hcount));
+    int64_t max_len = 0;
+    for (int32_t i = 0; i < hcount; ++i) {
+      SP_HIP(hipMemcpy(&bounds[2 * i], d_ptr_new + rows[i], 2 * sizeof(int32_t),
+                       hipMemcpyDeviceToHost));
+      max_len = std::max<int64_t>(max_len, bounds[2 * i + 1] - bounds[2 * i]);
+    }
+    uint32_t *kalt = nullptr, *valt = nullptr, *zvals = nullptr;
+    int32_t *tmp = nullptr;
+    SP_HIP(hipMalloc(&kalt, max_len * 4));
+    SP_HIP(hipMalloc(&valt, max_len * 4));
+    SP_HIP(hipMalloc(&zvals, max_len * 4));
+    SP_HIP(hipMalloc(&tmp, radix_tmp_elems(max_len) * 4));
+    fill_u32(ctx, zvals, max_len, 0u);
+    uint32_t *vout = nullptr;
+    if (!with_vals) SP_HIP(hipMalloc(&vout, max_len * 4));
+    const int bits = bits_for(n - 1);
+    for (int32_t i = 0; i < hcount; ++i) {
+      int32_t s = bounds[2 * i], len = bounds[2 * i + 1] - s;
+      const uint32_t *vin = with_vals ? reinterpret_cast<const uint32_t *>(val_unsorted + s)
+                                      : zvals;
+      uint32_t *vo = with_vals ? reinterpret_cast<uint32_t *>(d_val_new + s) : vout;
+      radix_sort_pairs(ctx, reinterpret_cast<const uint32_t *>(unsorted + s), vin,
+                       reinterpret_cast<uint32_t *>(d_ind_new + s), vo, kalt, valt, len,
+                       bits, tmp);
+    }
+    ctx.sync();
+    SP_HIP(hipFree(kalt));
+    SP_HIP(hipFree(valt));
+    SP_HIP(hipFree(zvals));
+    SP_HIP(hipFree(tmp));
+    if (vout) SP_HIP(hipFree(vout));
+  }
+}

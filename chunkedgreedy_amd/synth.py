@@ -1,0 +1,250 @@
+"""Seeded synthetic CSR generators for the benchmark configurations.
+
+The reference ships no generators for these inputs (its experiments read
+SuiteSparse files), so the shapes follow the configuration text:
+
+  C1 planted(n=20_000, blocks=256, nnz/row=10)          CPU plumbing case
+  C2 planted(n=1_048_576, blocks=16_384, nnz/row=16)    headline workload
+  C3 rmat(scale=22, edge_factor=16, a,b,c,d=.57,.19,.19,.05), symmetrized,
+     deduplicated, no self loops, values 1/deg(row)
+  C4 stencil7(160), diagonal 6 / off-diagonal -1, random symmetric permutation
+  C5 chung_lu(n=2_449_029, exponent=2.1, avg degree 25), symmetric, with self
+     loops, values of D^-1/2 (A+I) D^-1/2
+
+Every generator returns (ptr int32[n+1], ind int32[nnz], val float32[nnz]) with
+column indices sorted and distinct within each row, from numpy's PCG64 seeded
+by `seed`.  The same seed gives the same matrix on every host.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+Csr = tuple[np.ndarray, np.ndarray, np.ndarray]
+
+
+def _rng(seed: int) -> np.random.Generator:
+    return np.random.Generator(np.random.PCG64(seed))
+
+
+def _coo_to_csr(n: int, rows: np.ndarray, cols: np.ndarray, vals: np.ndarray) -> Csr:
+    order = np.lexsort((cols, rows))
+    rows, cols, vals = rows[order], cols[order], vals[order]
+    counts = np.bincount(rows, minlength=n)
+    ptr = np.zeros(n + 1, np.int64)
+    np.cumsum(counts, out=ptr[1:])
+    return ptr.astype(np.int32), cols.astype(np.int32), vals.astype(np.float32)
+
+
+def _sort_rows(ptr: np.ndarray, ind: np.ndarray, val: np.ndarray) -> Csr:
+    n = ptr.shape[0] - 1
+    rows = np.repeat(np.arange(n, dtype=np.int64), np.diff(ptr.astype(np.int64)))
+    order = np.lexsort((ind, rows))
+    return ptr.astype(np.int32), ind[order].astype(np.int32), val[order].astype(np.float32)
+
+
+def permute(ptr, ind, val, row_perm: np.ndarray | None, col_perm: np.ndarray | None) -> Csr:
+    """B[i, j] = A[row_perm[i], col_perm[j]] (new2old permutations); rows
+    re-sorted."""
+    n = ptr.shape[0] - 1
+    ptr64 = ptr.astype(np.int64)
+    if row_perm is not None:
+        lens = np.diff(ptr64)[row_perm]
+        new_ptr = np.zeros(n + 1, np.int64)
+        np.cumsum(lens, out=new_ptr[1:])
+        src = np.repeat(ptr64[row_perm] - new_ptr[:-1], lens) + np.arange(new_ptr[-1])
+        ind = ind[src]
+        val = val[src]
+        ptr64 = new_ptr
+    if col_perm is not None:
+        inv = np.empty(n, np.int64)
+        inv[col_perm] = np.arange(n)
+        ind = inv[ind]
+    return _sort_rows(ptr64, ind, val)
+
+
+def planted(n: int, blocks: int, nnz_per_row: int, seed: int, in_frac: float = 0.8) -> Csr:
+    """Planted-block matrix: row i of block b has round(in_frac*nnz_per_row)
+    distinct columns inside b's column range and the rest uniform over all
+    columns (all distinct); values U(-1,1); then independent random row and
+    column permutations."""
+    rng = _rng(seed)
+    sizes = np.full(blocks, n // blocks, np.int64)
+    sizes[: n % blocks] += 1
+    starts = np.zeros(blocks + 1, np.int64)
+    np.cumsum(sizes, out=starts[1:])
+    row_block = np.repeat(np.arange(blocks), sizes)
+    bs = starts[row_block]
+    bl = sizes[row_block]
+    n_in = int(round(in_frac * nnz_per_row))
+    n_out = nnz_per_row - n_in
+    width = int(sizes.max())
+    cols = np.empty((n, nnz_per_row), np.int64)
+    step = 1 << 18
+    for r0 in range(0, n, step):
+        r1 = min(n, r0 + step)
+        keys = rng.random((r1 - r0, width), dtype=np.float32)
+        keys[np.arange(width)[None, :] >= bl[r0:r1, None]] = 2.0
+        pick = np.argpartition(keys, n_in - 1, axis=1)[:, :n_in]
+        cols[r0:r1, :n_in] = bs[r0:r1, None] + pick
+    if n_out:
+        cols[:, n_in:] = rng.integers(0, n, size=(n, n_out))
+        # Resample uniform columns that collide with another column of the row.
+        while True:
+            srt = np.sort(cols, axis=1)
+            dup_rows = np.nonzero((srt[:, 1:] == srt[:, :-1]).any(axis=1))[0]
+            if dup_rows.size == 0:
+                break
+            cols[dup_rows, n_in:] = rng.integers(0, n, size=(dup_rows.size, n_out))
+    vals = rng.uniform(-1.0, 1.0, size=(n, nnz_per_row)).astype(np.float32)
+    row_perm = rng.permutation(n)
+    col_perm = rng.permutation(n)
+    # Every row has the same length, so the permutations and the per-row sort
+    # work on the dense (n, nnz_per_row) layout.
+    inv = np.empty(n, np.int64)
+    inv[col_perm] = np.arange(n)
+    cols = inv[cols[row_perm]]
+    vals = vals[row_perm]
+    order = np.argsort(cols, axis=1, kind="stable")
+    cols = np.take_along_axis(cols, order, axis=1)
+    vals = np.take_along_axis(vals, order, axis=1)
+    ptr = np.arange(n + 1, dtype=np.int64) * nnz_per_row
+    return ptr.astype(np.int32), cols.reshape(-1).astype(np.int32), vals.reshape(-1)
+
+
+def config1(seed: int = 1) -> Csr:
+    return planted(20_000, 256, 10, seed)
+
+
+def config2(seed: int = 2, n: int = 1_048_576, blocks: int = 16_384) -> Csr:
+    return planted(n, blocks, 16, seed)
+
+
+def rmat(scale: int, edge_factor: int, seed: int, a=0.57, b=0.19, c=0.19) -> Csr:
+    """R-MAT graph (Chakrabarti, Zhan, Faloutsos 2004): edge_factor * 2^scale
+    edges, each placed by `scale` independent quadrant choices; symmetrized,
+    deduplicated, self loops removed; values 1/deg(row)."""
+    rng = _rng(seed)
+    n = 1 << scale
+    m = edge_factor * n
+    keys = []
+    step = 1 << 22
+    for e0 in range(0, m, step):
+        cnt = min(step, m - e0)
+        u = np.zeros(cnt, np.int64)
+        v = np.zeros(cnt, np.int64)
+        for _ in range(scale):
+            r = rng.random(cnt)
+            down = r >= a + b          # quadrants c, d
+            right = ((r >= a) & (r < a + b)) | (r >= a + b + c)  # b, d
+            u = (u << 1) | down
+            v = (v << 1) | right
+        keep = u != v
+        u, v = u[keep], v[keep]
+        keys.append(u * n + v)
+        keys.append(v * n + u)
+    k = np.unique(np.concatenate(keys))
+    rows = k // n
+    cols = k % n
+    counts = np.bincount(rows, minlength=n)
+    ptr = np.zeros(n + 1, np.int64)
+    np.cumsum(counts, out=ptr[1:])
+    deg = np.maximum(counts, 1).astype(np.float32)
+    val = (1.0 / deg)[rows].astype(np.float32)
+    return ptr.astype(np.int32), cols.astype(np.int32), val
+
+
+def config3(seed: int = 3, scale: int = 22) -> Csr:
+    return rmat(scale, 16, seed)
+
+
+def stencil7(g: int, seed: int, scramble: bool = True) -> Csr:
+    """7-point stencil on a g^3 grid (6 on the diagonal, -1 off it), with a
+    random symmetric permutation P A P^T."""
+    n = g ** 3
+    idx = np.arange(n, dtype=np.int64)
+    x, y, z = idx % g, (idx // g) % g, idx // (g * g)
+    rows, cols, vals = [idx], [idx], [np.full(n, 6.0, np.float32)]
+    for d, coord in ((1, x), (g, y), (g * g, z)):
+        m = coord < g - 1
+        rows += [idx[m], idx[m] + d]
+        cols += [idx[m] + d, idx[m]]
+        vals += [np.full(int(m.sum()), -1.0, np.float32)] * 2
+    ptr, ind, val = _coo_to_csr(n, np.concatenate(rows), np.concatenate(cols),
+                                np.concatenate(vals))
+    if scramble:
+        p = _rng(seed).permutation(n)
+        ptr, ind, val = permute(ptr, ind, val, p, p)
+    return ptr, ind, val
+
+
+def config4(seed: int = 4, g: int = 160) -> Csr:
+    return stencil7(g, seed)
+
+
+def chung_lu(n: int, exponent: float, avg_degree: float, seed: int) -> Csr:
+    """Chung-Lu graph with expected degrees w_i proportional to
+    (i + 1)^(-1/(exponent-1)), scaled to `avg_degree`: n*avg_degree/2 edges with
+    both endpoints drawn proportional to w; symmetrized, deduplicated, self
+    loops replaced by the identity; values D^-1/2 (A + I) D^-1/2."""
+    rng = _rng(seed)
+    w = (np.arange(n, dtype=np.float64) + 1.0) ** (-1.0 / (exponent - 1.0))
+    cdf = np.cumsum(w)
+    cdf /= cdf[-1]
+    m = int(n * avg_degree / 2)
+    keys = []
+    step = 1 << 22
+    for e0 in range(0, m, step):
+        cnt = min(step, m - e0)
+        u = np.searchsorted(cdf, rng.random(cnt), side="right")
+        v = np.searchsorted(cdf, rng.random(cnt), side="right")
+        u = np.minimum(u, n - 1)
+        v = np.minimum(v, n - 1)
+        keep = u != v
+        u, v = u[keep], v[keep]
+        keys += [u * n + v, v * n + u]
+    keys.append(np.arange(n, dtype=np.int64) * (n + 1))  # self loops
+    k = np.unique(np.concatenate(keys))
+    # Scramble vertex ids so that degree does not follow the index.
+    p = rng.permutation(n)
+    rows, cols = p[k // n], p[k % n]
+    deg = np.bincount(rows, minlength=n).astype(np.float64)
+    dinv = 1.0 / np.sqrt(deg)
+    vals = (dinv[rows] * dinv[cols]).astype(np.float32)
+    return _coo_to_csr(n, rows, cols, vals)
+
+
+def config5(seed: int = 5, n: int = 2_449_029) -> Csr:
+    return chung_lu(n, 2.1, 25.0, seed)
+
+
+def band(n: int, half_width: int = 2) -> Csr:
+    """Symmetric band pattern |i - j| <= half_width, values 1 (the reference's
+    smoke matrix, sporder/tests/smoke.c:58-70, with half_width 2)."""
+    rows, cols = [], []
+    for d in range(-half_width, half_width + 1):
+        i = np.arange(max(0, -d), min(n, n - d), dtype=np.int64)
+        rows.append(i)
+        cols.append(i + d)
+    r = np.concatenate(rows)
+    c = np.concatenate(cols)
+    return _coo_to_csr(n, r, c, np.ones(r.shape[0], np.float32))
+
+
+def is_pattern_symmetric(ptr, ind) -> bool:
+    """Pattern equals its transpose (the harness test of
+    bench/reorder/reorder_bench/loader.py:86-88 on the pattern)."""
+    import scipy.sparse as sp
+
+    n = ptr.shape[0] - 1
+    a = sp.csr_matrix((np.ones(ind.shape[0], np.int8), ind, ptr), shape=(n, n))
+    return (a != a.T).nnz == 0
+
+
+CONFIGS = {
+    "C1": config1,
+    "C2": config2,
+    "C3": config3,
+    "C4": config4,
+    "C5": config5,
+}

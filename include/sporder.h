@@ -1,0 +1,294 @@
+#ifndef SPORDER_H
+#define SPORDER_H
+
+/*
+ * sporder -- C ABI of the MI355X (gfx950) sparse-matrix reordering library
+ * (libsporder_hip.so).
+ *
+ * Every entry point below keeps the name, argument list and struct layout of
+ * the reference's C ABI (sporder/include/sporder.h of Siaaa-3/ChunkedGreedy;
+ * each declaration cites the line it replaces), so an existing binding
+ * (nanobind, ctypes, cgo, ...) links against this library unchanged.  Entry
+ * points marked "(new)" have no counterpart there.
+ *
+ * Conventions shared by every entry point (reference sporder.h:13-41):
+ *   - Synchronous: calls return only after device outputs and host
+ *     out-parameters are ready.
+ *   - d_-prefixed pointers are device memory on the context's device; all
+ *     other pointers are host memory.
+ *   - The library runs on a private HIP stream (created blocking, default
+ *     priority), so inputs produced on another non-default stream must be
+ *     synchronized by the caller first.
+ *   - CSR patterns are square (n rows and columns), zero-based, with column
+ *     indices sorted within each row.
+ *   - Invalid arguments and HIP errors abort the process with a diagnostic on
+ *     stderr (no return codes), as in the reference.
+ *   - Permutations are in new2old form: d_new_order[p] = the original row
+ *     that belongs in new position p.
+ *   - Timing and stats pointers are optional (NULL to skip).
+ *   - Scratch memory comes from a grow-only workspace owned by the context;
+ *     steady-state calls of equal or smaller size allocate nothing.
+ */
+
+#include <stdbool.h>
+#include <stdint.h>
+
+#define SPORDER_API __attribute__((visibility("default")))
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct sporder_context_struct *sporder_context_t;
+
+/* Context bound to the device current at creation; one thread at a time.
+ * Reference: sporder.h:43-52. */
+SPORDER_API sporder_context_t sporder_context_create(void);
+SPORDER_API void sporder_context_destroy(sporder_context_t h);
+
+/* Reference: sporder.h:54-58. */
+typedef struct {
+  int32_t k;
+  float oversampling;
+  int32_t max_rounds;
+} sporder_options_t;
+
+/* Reference: sporder.h:64-72. */
+typedef struct {
+  double wall_ms;
+  float csr2csc_ms;
+  float similarity_ms;
+  float matching_ms;
+  float advance_ms;
+  float *matching_per_level_ms;
+  float *advance_per_level_ms;
+} sporder_hm_timing_t;
+
+/* Reference: sporder.h:85-94. */
+typedef struct {
+  int32_t k_used;
+  int32_t m_used;
+  double avg_degree;
+  double avg_edge_weight;
+  int32_t zero_degree_rows;
+  int32_t *level_size;
+  int32_t *matched_pairs;
+  int32_t *rounds;
+} sporder_hm_stats_t;
+
+/* Hierarchical matching.  Not built in this library (a different algorithm
+ * from the Chunked Greedy path): the symbol exists for link compatibility and
+ * aborts with a diagnostic.  Reference: sporder.h:119-123. */
+SPORDER_API void sporder_hierarchical_matching(
+    sporder_context_t ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
+    const int32_t *d_ind, bool is_symmetric, int32_t num_levels,
+    const sporder_options_t *opts, int32_t *d_new_order,
+    sporder_hm_timing_t *timing, sporder_hm_stats_t *stats);
+
+/* Reference: sporder.h:128-133. */
+typedef struct {
+  double wall_ms;
+  float csr2csc_ms;
+  float similarity_ms;
+  float chunk_greedy_ms;
+} sporder_cg_timing_t;
+
+/* Reference: sporder.h:154-167. */
+typedef struct {
+  int32_t k_used;
+  int32_t m_used;
+  double avg_degree;
+  double avg_edge_weight;
+  int32_t zero_degree_rows;
+  int32_t chunk_size_used;
+  int32_t chain_restarts;
+  double avg_followed_weight;
+  double cut_weight_fraction;
+} sporder_cg_stats_t;
+
+/* Global-sketch chunk greedy (sporder-cg).  Not built yet: aborts with a
+ * diagnostic.  Reference: sporder.h:176-182. */
+SPORDER_API void sporder_chunk_greedy(sporder_context_t ctx, int32_t n,
+                                      int32_t nnz, const int32_t *d_ptr,
+                                      const int32_t *d_ind, bool is_symmetric,
+                                      int32_t k, float oversampling,
+                                      int32_t chunk_size, int32_t *d_new_order,
+                                      sporder_cg_timing_t *timing,
+                                      sporder_cg_stats_t *stats);
+
+/* Reference: sporder.h:203-208. */
+typedef struct {
+  double wall_ms;
+  float csr2csc_ms;
+  float similarity_ms;
+  float chunk_greedy_ms;
+} sporder_csg_timing_t;
+
+/* Reference: sporder.h:213-222. */
+typedef struct {
+  int32_t k_used;
+  int32_t m_used;
+  double avg_degree;
+  double avg_edge_weight;
+  int32_t zero_degree_rows;
+  int32_t chunk_size_used;
+  int32_t chain_restarts;
+  double avg_followed_weight;
+} sporder_csg_stats_t;
+
+/*
+ * Chunked Greedy reordering (sporder-csg).  Reference: sporder.h:224-228,
+ * bridge sporder/src/sporder.cpp:140-166.
+ *
+ * Defaults: k <= 0 -> min(256, max(16, nnz / n)); oversampling <= 0 -> 4;
+ * chunk_size <= 0 -> 1024.  Requires (int)(k * oversampling) <= 512.
+ * Rows are cut into aligned chunks; each row's top-k Dice neighbours within
+ * its chunk come from a 32-lane space-saving sketch of capacity
+ * m = 32 * ceil((int)(k*oversampling) / 32); a greedy chain per chunk writes
+ * d_new_order[start..end).  The output equals the reference's bit for bit.
+ * is_symmetric says the pattern equals its transpose; the transpose is then
+ * taken to be the CSR itself, as in the reference.
+ */
+SPORDER_API void sporder_chunk_similarity_greedy(
+    sporder_context_t ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
+    const int32_t *d_ind, bool is_symmetric, int32_t k, float oversampling,
+    int32_t chunk_size, int32_t *d_new_order, sporder_csg_timing_t *timing,
+    sporder_csg_stats_t *stats);
+
+/* Reference: sporder.h:230-233. */
+typedef enum {
+  SPORDER_REORDER_ROWS = 0,
+  SPORDER_REORDER_SYMMETRIC = 1,
+} sporder_reorder_mode_t;
+
+/*
+ * Apply a new2old permutation: ROWS copies old row new_order[p] to row p;
+ * SYMMETRIC also maps column c to old2new[c] and re-sorts each row (values
+ * follow).  Reference: sporder.h:253-258, sporder/src/reorder.cu:72-149.
+ */
+SPORDER_API void
+sporder_reorder(sporder_context_t ctx, int32_t n, int32_t nnz,
+                const int32_t *d_ptr_old, const int32_t *d_ind_old,
+                const float *d_val_old, const int32_t *d_new_order,
+                sporder_reorder_mode_t mode, int32_t *d_ptr_new,
+                int32_t *d_ind_new, float *d_val_new);
+
+/* Pillar count.  Not built yet: aborts with a diagnostic.
+ * Reference: sporder.h:276-279. */
+SPORDER_API void sporder_count_pillars(sporder_context_t ctx, int32_t n,
+                                       int32_t nnz, const int32_t *d_ptr,
+                                       const int32_t *d_ind, int32_t height,
+                                       int32_t *count);
+
+/*
+ * SpMM benchmark hook.  Same symbol and arguments as the reference
+ * (sporder.h:295-299, sporder/src/bench_cusparse_spmm.cu:25-103); the kernel
+ * timed is this library's CSR SpMM (row-split, fp32), not cuSPARSE.  A's
+ * values and a row-major B are U(0,1] from Philox4x32-10 keyed by `seed`
+ * (the reference used cuRAND XORWOW and a column-major B).  *wall_ms is the
+ * mean time per repeat, measured with HIP events on the library stream.
+ */
+SPORDER_API void sporder_bench_cusparse_spmm(sporder_context_t ctx, int32_t n,
+                                             int32_t nnz, const int32_t *d_ptr,
+                                             const int32_t *d_ind, int32_t cols,
+                                             int32_t warmup, int32_t repeat,
+                                             uint64_t seed, float *wall_ms);
+
+/* Reference: sporder.h:312-317. */
+typedef struct {
+  double wall_ms;
+  float csr2csc_ms;
+  float similarity_ms;
+  float unpack_ms;
+} sporder_sim_timing_t;
+
+/* Reference: sporder.h:322-328. */
+typedef struct {
+  int32_t k_used;
+  int32_t m_used;
+  double avg_degree;
+  double avg_edge_weight;
+  int32_t zero_degree_rows;
+} sporder_sim_stats_t;
+
+/*
+ * Global top-k Dice similarity graph from the space-saving sketch.
+ * Defaults: k <= 0 -> min(32, max(16, 2 * (nnz / n))); oversampling <= 0 -> 2.
+ * Computed by the same sketch kernel as the csg path with one chunk spanning
+ * all rows.  Reference: sporder.h:330-335, sporder/src/similarity_graph.cu.
+ */
+SPORDER_API void sporder_similarity_graph(
+    sporder_context_t ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
+    const int32_t *d_ind, bool is_symmetric, int32_t k, float oversampling,
+    int32_t *d_indices, float *d_weights, sporder_sim_timing_t *timing,
+    sporder_sim_stats_t *stats);
+
+/* Reference: sporder.h:353-360. */
+typedef struct {
+  double wall_ms;
+  float csr2csc_ms;
+  float spgemm_ms;
+  float dice_ms;
+  float sort_ms;
+  float select_ms;
+} sporder_sim_exact_timing_t;
+
+/* Reference: sporder.h:365-371. */
+typedef struct {
+  int32_t k_used;
+  int64_t c_nnz;
+  double avg_degree;
+  double avg_edge_weight;
+  int32_t zero_degree_rows;
+} sporder_sim_exact_stats_t;
+
+/* Exact similarity via SpGEMM.  Not built (a validation tool resting on a
+ * closed library in the reference): aborts with a diagnostic.
+ * Reference: sporder.h:373-377. */
+SPORDER_API void sporder_similarity_graph_exact(
+    sporder_context_t ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
+    const int32_t *d_ind, bool is_symmetric, int32_t k, int32_t *d_indices,
+    float *d_weights, sporder_sim_exact_timing_t *timing,
+    sporder_sim_exact_stats_t *stats);
+
+/*
+ * (new) The csg sketch table on its own: for each row, its top-k in-chunk
+ * neighbours, d_indices/d_weights n*k, unused entries (-1, 0.0f).  k,
+ * oversampling and chunk_size must be resolved (> 0).  This is the
+ * reference's internal stage multi_chunk_similarity_top_k
+ * (sporder/src/common/chunk_similarity_top_k.h:23-28), exported so the sketch
+ * can be checked bit for bit.
+ */
+SPORDER_API void sporder_chunk_similarity_top_k(
+    sporder_context_t ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
+    const int32_t *d_ind, bool is_symmetric, int32_t k, float oversampling,
+    int32_t chunk_size, int32_t *d_indices, float *d_weights);
+
+/* (new) SpMM kernel variants. */
+typedef enum {
+  SPORDER_SPMM_AUTO = 0,     /* row-split, or merge-path for skewed rows */
+  SPORDER_SPMM_ROW_SPLIT = 1,
+  SPORDER_SPMM_MERGE_PATH = 2,
+} sporder_spmm_algo_t;
+
+/*
+ * (new) C = A * B for a CSR A (n x n, values d_val) and row-major dense
+ * B (n x cols) and C (n x cols), fp32.  ROW_SPLIT computes each C element as
+ * acc = fmaf(a_p, B[col_p][j], acc) over p in CSR order from 0.0f (bit-exact
+ * with a CPU loop in that order); MERGE_PATH splits long rows and adds the
+ * partial sums, so it matches within rounding.  *kernel_ms (optional) gets
+ * the kernel time from HIP events on the library stream.  The reference
+ * harness contract this serves is SpMMMethod.run
+ * (bench/spmm/spmm_bench/base.py:48-59).
+ */
+SPORDER_API void sporder_spmm_csr(sporder_context_t ctx, int32_t n,
+                                  int32_t nnz, const int32_t *d_ptr,
+                                  const int32_t *d_ind, const float *d_val,
+                                  int32_t cols, const float *d_b, float *d_c,
+                                  sporder_spmm_algo_t algo, float *kernel_ms);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SPORDER_H */

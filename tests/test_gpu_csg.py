@@ -1,0 +1,187 @@
+"""GPU parity of the Chunked Greedy path: HIP library vs the CPU oracle.
+
+Bit-exact comparisons (integer and index work, and the fp32 sketch weights,
+whose accumulation order the reference fixes).  Inputs are seeded synthetic
+matrices at sizes the oracle finishes in seconds, plus the full headline
+configuration (C2) where the oracle is still fast.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from chunkedgreedy_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def dev_csr(ptr, ind, dev="cuda:0"):
+    return (torch.from_numpy(np.ascontiguousarray(ptr, np.int32)).to(dev),
+            torch.from_numpy(np.ascontiguousarray(ind, np.int32)).to(dev))
+
+
+def weight_bits(w):
+    return np.ascontiguousarray(w, np.float32).view(np.uint32)
+
+
+def small_matrices():
+    out = {
+        "band1000": synth.band(1000)[:2],
+        "C1": synth.config1(11)[:2],
+        "planted64k": synth.planted(1 << 16, 1024, 16, 12)[:2],
+        "stencil20": synth.stencil7(20, 13)[:2],
+        "stencil20_ordered": synth.stencil7(20, 13, scramble=False)[:2],
+        "rmat13": synth.rmat(13, 16, 14)[:2],
+        "rmat11": synth.rmat(11, 16, 16)[:2],
+        "chunglu20k": synth.chung_lu(20000, 2.1, 25, 15)[:2],
+    }
+    return out
+
+
+MATS = small_matrices()
+
+
+def check_table(sp, ptr, ind, k, ovs, chunk, sym):
+    print(f"[table] n={ptr.shape[0]-1} nnz={ind.shape[0]} k={k} ovs={ovs} chunk={chunk} "
+          f"sym={sym}", flush=True)
+    dptr, dind = dev_csr(ptr, ind)
+    gi, gw = sp.chunk_similarity_top_k(dptr, dind, k=k, oversampling=ovs, chunk_size=chunk,
+                                       is_symmetric=sym)
+    t = oracle.chunk_similarity_top_k(ptr, ind, k, chunk, ovs, is_symmetric=sym)
+    oi, ow = oracle.unpack_table(t)
+    gi = gi.cpu().numpy()
+    gw = gw.cpu().numpy()
+    mism = np.nonzero((gi != oi).any(axis=1) | (weight_bits(gw) != weight_bits(ow)).any(axis=1))[0]
+    assert mism.size == 0, (f"{mism.size} rows differ; first row {mism[0]}: gpu "
+                            f"{gi[mism[0]]} {gw[mism[0]]} oracle {oi[mism[0]]} {ow[mism[0]]}")
+    return oi, ow
+
+
+@pytest.mark.parametrize("name", sorted(MATS))
+@pytest.mark.parametrize("k,ovs,chunk", [(16, 4.0, 1024), (8, 4.0, 256), (16, 1.0, 4096),
+                                         (24, 4.0, 1024), (5, 3.5, 333), (32, 16.0, 2048)])
+def test_chunk_table_bit_exact(sporder, name, k, ovs, chunk):
+    ptr, ind = MATS[name]
+    sym = synth.is_pattern_symmetric(ptr, ind)
+    check_table(sporder, ptr, ind, k, ovs, chunk, sym)
+
+
+@pytest.mark.parametrize("name", ["rmat13", "chunglu20k", "C1"])
+def test_chunk_table_nonsymmetric_path(sporder, name):
+    """Symmetric patterns through the transpose path give the same table."""
+    ptr, ind = MATS[name]
+    check_table(sporder, ptr, ind, 16, 4.0, 1024, False)
+
+
+@pytest.mark.parametrize("ovs", [1.0, 2.0, 4.0, 8.0, 16.0, 32.0])
+def test_global_sketch_all_capacities(sporder, ovs):
+    """Sketch capacities 32..512 (CELLS 1..16) on a hub-heavy graph, one chunk
+    spanning all rows (heavy eviction)."""
+    ptr, ind = MATS["rmat11"]
+    n = ptr.shape[0] - 1
+    check_table(sporder, ptr, ind, 16, ovs, n, True)
+
+
+@pytest.mark.parametrize("k,ovs", [(3, 32.0), (7, 13.0), (10, 10.0), (48, 2.0), (100, 5.0),
+                                   (256, 2.0)])
+def test_global_sketch_odd_capacities(sporder, k, ovs):
+    ptr, ind = MATS["chunglu20k"]
+    n = ptr.shape[0] - 1
+    check_table(sporder, ptr, ind, k, ovs, n, True)
+
+
+def test_band_known_answer(sporder):
+    """Band |i-j|<=2 (the reference smoke matrix), k=8, ovs=4 -> M=32: row 0's
+    neighbours are 1,2,3,4 with weights 3 sequential adds of fl(2/7), 0.75,
+    0.5, 0.25 (golden vector)."""
+    ptr, ind = MATS["band1000"]
+    dptr, dind = dev_csr(ptr, ind)
+    idx, wgt = sporder.similarity_graph(dptr, dind, is_symmetric=True, k=8, oversampling=4.0)
+    idx = idx.cpu().numpy()
+    wgt = wgt.cpu().numpy()
+    assert idx[0].tolist() == [1, 2, 3, 4, -1, -1, -1, -1]
+    assert weight_bits(wgt[0]).tolist() == [0x3F5B6DB8, 0x3F400000, 0x3F000000, 0x3E800000,
+                                            0, 0, 0, 0]
+    assert 0 < idx[0, 0] < 1000
+
+
+@pytest.mark.parametrize("name", sorted(MATS))
+@pytest.mark.parametrize("k,ovs,chunk", [(0, 0.0, 0), (16, 4.0, 256), (24, 2.0, 5000),
+                                         (8, 4.0, 1)])
+def test_csg_permutation_bit_exact(sporder, name, k, ovs, chunk):
+    ptr, ind = MATS[name]
+    sym = synth.is_pattern_symmetric(ptr, ind)
+    print(f"[csg] {name} k={k} ovs={ovs} chunk={chunk}", flush=True)
+    dptr, dind = dev_csr(ptr, ind)
+    order, timing, stats = sporder.chunk_similarity_greedy(
+        dptr, dind, is_symmetric=sym, k=k, oversampling=ovs, chunk_size=chunk,
+        with_timing=True, with_stats=True)
+    o_order, o_stats = oracle.chunk_similarity_greedy(ptr, ind, is_symmetric=sym, k=k,
+                                                      oversampling=ovs, chunk_size=chunk)
+    g = order.cpu().numpy()
+    assert np.array_equal(g, o_order)
+    for key in ("k_used", "m_used", "zero_degree_rows", "chunk_size_used", "chain_restarts"):
+        assert stats[key] == o_stats[key], key
+    for key in ("avg_degree", "avg_edge_weight", "avg_followed_weight"):
+        # Doubles summed with atomics: order-dependent low bits.
+        assert stats[key] == pytest.approx(o_stats[key], rel=1e-9, abs=1e-12), key
+    assert set(timing) == {"wall_ms", "csr2csc_ms", "similarity_ms", "chunk_greedy_ms"}
+    assert timing["wall_ms"] >= timing["chunk_greedy_ms"] >= 0.0
+
+
+def test_csg_return_shapes(sporder):
+    ptr, ind = MATS["C1"]
+    dptr, dind = dev_csr(ptr, ind)
+    o = sporder.chunk_similarity_greedy(dptr, dind)
+    assert isinstance(o, torch.Tensor) and o.dtype == torch.int32 and o.shape == (20000,)
+    o2, t = sporder.chunk_similarity_greedy(dptr, dind, with_timing=True)
+    assert torch.equal(o, o2) and isinstance(t, dict)
+    o3, s = sporder.chunk_similarity_greedy(dptr, dind, with_stats=True)
+    assert torch.equal(o, o3) and s["k_used"] == 16 and s["m_used"] == 64
+    o4, t4, s4 = sporder.chunk_similarity_greedy(dptr, dind, with_timing=True, with_stats=True)
+    assert torch.equal(o, o4)
+
+
+def test_csg_edge_cases(sporder):
+    # Empty rows, a single row, no nonzeros at all, chunk larger than n.
+    cases = [
+        (np.array([0, 0], np.int32), np.zeros(0, np.int32)),
+        (np.array([0, 1], np.int32), np.array([0], np.int32)),
+        (np.array([0, 0, 2, 2, 4, 4], np.int32), np.array([1, 3, 1, 3], np.int32)),
+        (np.zeros(101, np.int32), np.zeros(0, np.int32)),
+    ]
+    for ptr, ind in cases:
+        for chunk in (0, 1, 3, 1000):
+            dptr, dind = dev_csr(ptr, ind)
+            g = sporder.chunk_similarity_greedy(dptr, dind, chunk_size=chunk).cpu().numpy()
+            o, _ = oracle.chunk_similarity_greedy(ptr, ind, chunk_size=chunk)
+            assert np.array_equal(g, o), (ptr, ind, chunk)
+
+
+def test_csg_rejects_bad_sizes(sporder):
+    with pytest.raises(ValueError):
+        sporder.chunk_similarity_greedy(torch.zeros(1, dtype=torch.int32, device="cuda"),
+                                        torch.zeros(0, dtype=torch.int32, device="cuda"))
+    with pytest.raises(TypeError):
+        sporder.chunk_similarity_greedy(torch.zeros(3, dtype=torch.int64, device="cuda"),
+                                        torch.zeros(0, dtype=torch.int32, device="cuda"))
+
+
+def test_csg_headline_config_bit_exact(sporder):
+    """Full C2 (n = 2^20, 16 nnz/row): permutation and table bit-exact."""
+    ptr, ind, _ = synth.config2(seed=2)
+    print("[csg] C2 full", flush=True)
+    dptr, dind = dev_csr(ptr, ind)
+    order, stats = sporder.chunk_similarity_greedy(dptr, dind, with_stats=True)
+    o_order, o_stats, o_table = oracle.chunk_similarity_greedy(ptr, ind, return_table=True)
+    assert np.array_equal(order.cpu().numpy(), o_order)
+    assert stats["chain_restarts"] == o_stats["chain_restarts"]
+    gi, gw = sporder.chunk_similarity_top_k(dptr, dind, k=16, oversampling=4.0, chunk_size=1024)
+    oi, ow = oracle.unpack_table(o_table)
+    assert np.array_equal(gi.cpu().numpy(), oi)
+    assert np.array_equal(weight_bits(gw.cpu().numpy()), weight_bits(ow))
+    # Size-independent property: each chunk's slice is a permutation of itself.
+    n = ptr.shape[0] - 1
+    g = order.cpu().numpy().reshape(-1, 1024)
+    assert np.array_equal(np.sort(g, axis=1), np.arange(n).reshape(-1, 1024))
