@@ -185,3 +185,24 @@ def test_csg_headline_config_bit_exact(sporder):
     n = ptr.shape[0] - 1
     g = order.cpu().numpy().reshape(-1, 1024)
     assert np.array_equal(np.sort(g, axis=1), np.arange(n).reshape(-1, 1024))
+
+
+GOLDEN = __import__("json").loads(
+    (__import__("pathlib").Path(__file__).parent / "golden" / "sketch_cases.json").read_text())
+
+
+@pytest.mark.parametrize("case", GOLDEN["csr_cases"], ids=lambda c: c["name"])
+def test_golden_csr_cases(sporder, case):
+    """Hand-worked eviction / Dice-weight cases (tests/golden/make_golden.py)."""
+    ptr = np.array(case["ptr"], np.int32)
+    ind = np.array(case["ind"], np.int32)
+    dptr, dind = dev_csr(ptr, ind)
+    k = case["k"]
+    for chk in case["checks"]:
+        gi, gw = sporder.chunk_similarity_top_k(dptr, dind, k=k, oversampling=case["oversampling"],
+                                                chunk_size=chk["chunk"])
+        r = chk["row"]
+        exp_idx = [e[0] for e in chk["expected"]] + [-1] * (k - len(chk["expected"]))
+        exp_bits = chk["expected_bits"] + [0] * (k - len(chk["expected"]))
+        assert gi.cpu().numpy()[r].tolist() == exp_idx, chk
+        assert weight_bits(gw.cpu().numpy()[r]).tolist() == exp_bits, chk
