@@ -147,11 +147,27 @@ size_t csr2csc_ws_bytes(int32_t n, int32_t nnz);
 void csr2csc(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
              const int32_t *d_ind, int32_t *d_col_ptr, int32_t *d_row_ind);
 
-// Chunk-restricted sketch + top-k table (u64 weighted_index, n*k).
+// Chunk-restricted sketch + top-k table (u64 weighted_index, n*k) from the
+// global CSC.  With d_chunks non-null only the rows of the chunks listed in
+// d_chunks[0 .. *d_chunk_count) are computed.
 void chunk_sketch_top_k(Context &ctx, int32_t n, int32_t k, int32_t chunk_size,
                         int32_t m_capacity, const int32_t *d_ptr,
                         const int32_t *d_ind, const int32_t *d_col_ptr,
-                        const int32_t *d_row_ind, uint64_t *d_table);
+                        const int32_t *d_row_ind, uint64_t *d_table,
+                        const int32_t *d_chunks = nullptr,
+                        const int32_t *d_chunk_count = nullptr);
+
+// Chunk-local variant: one workgroup per chunk with the chunk's transpose in
+// LDS.  Applicable when chunk_local_supported(n, chunk_size); chunks with more
+// than kLocalKeyCap nonzeros are appended to d_overflow (count in
+// *d_overflow_count, which the caller zeroes) and their rows left unwritten.
+constexpr int kLocalKeyCap = 32768;
+constexpr int kLocalRowCap = 4096;
+bool chunk_local_supported(int32_t n, int32_t chunk_size);
+void chunk_local_sketch_top_k(Context &ctx, int32_t n, int32_t k, int32_t chunk_size,
+                              int32_t m_capacity, const int32_t *d_ptr, const int32_t *d_ind,
+                              uint64_t *d_table, int32_t *d_overflow,
+                              int32_t *d_overflow_count);
 
 // Degree / weight totals of a top-k table (reference
 // sporder/src/common/similarity_top_k.cu:120-172).

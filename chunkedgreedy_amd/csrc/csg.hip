@@ -1,34 +1,31 @@
-// csg.hip -- Chunked Greedy (sporder-csg): chunk-restricted space-saving
-// sketch + top-k, the per-chunk greedy chain, table statistics and the C-ABI
-// entry points sporder_chunk_similarity_greedy, sporder_similarity_graph and
+// csg.hip -- Chunked Greedy (sporder-csg): the global-CSC sketch kernel, the
+// per-chunk greedy chain, table statistics, and the C-ABI entry points
+// sporder_chunk_similarity_greedy, sporder_similarity_graph and
 // sporder_chunk_similarity_top_k.
 //
 // Semantics follow the reference bit for bit:
 //   sketch stream  sporder/src/common/chunk_similarity_top_k.cu:30-88
-//   space-saving   sporder/src/common/warp_spacesaving.cuh:12-151
-//   arg-reductions sporder/src/common/cuda_util.cuh:66-87
+//   space-saving   sporder/src/common/warp_spacesaving.cuh:12-151 (sketch.hpp)
 //   greedy         sporder/src/csg/chunk_similarity_greedy.cu:14-98
 //   stats          sporder/src/common/similarity_top_k.cu:120-172,
 //                  sporder/src/csg/stats_collector.cu:43-63
 //
-// Mapping to gfx950 (wave64).  The reference's sketch lives in one 32-lane
-// warp: logical lane L owns cells c = 0..CELLS-1 (M = 32*CELLS slots).  Here
-// one wave64 serves one row and spreads the slots over all 64 lanes: physical
-// lane p holds logical lane L = p & 31 and the cells c = 2j + (p >> 5),
-// j = 0..ceil(CELLS/2)-1.  Every tie rule of the reference depends only on
-// (L, c), so the arrangement is free:
-//   - a new key goes to the first empty slot in order s = L*CELLS + c, which
-//     is a wave-uniform counter instead of a find(-1) + ballot;
-//   - eviction takes the minimum of (weight, c*32 + L), reduced over the
-//     wave with a butterfly;
-//   - top-k output merges the per-logical-lane selection-sorted lists with
-//     ties to the smaller logical lane.
-// The candidate stream of a row is gathered 64 entries at a time from the
-// concatenation of its columns' CSC segments (a wave prefix sum over segment
-// lengths finds each lane's segment), so a row's column walks are issued in
-// parallel instead of one column after another; items are then applied in
-// stream order.
+// Table construction picks, per call:
+//   - chunk-local (csg_local.hip): one workgroup per chunk, transpose in LDS,
+//     when chunk_size <= kLocalRowCap and the packed keys fit 32 bits; chunks
+//     with more nonzeros than LDS holds overflow to
+//   - global-CSC (this file): the reference's access pattern (transpose, or
+//     the CSR itself when is_symmetric), one wave per row.  The candidate
+//     stream is gathered 64 entries at a time from the concatenation of the
+//     row's column segments, so a row's column walks are issued together.
+// Both produce the same table.
+//
+// Greedy: one wave per chunk.  For chunk_size <= kGreedyCompactRows the
+// chunk's table slice is compacted into LDS (valid entries only, with
+// per-row offsets) so the serial chain touches only LDS; otherwise the chain
+// reads the table in global memory.
 #include "common.hpp"
+#include "sketch.hpp"
 
 #include <algorithm>
 #include <chrono>
@@ -44,194 +41,8 @@ constexpr int kSketchWaves = kSketchBlock / kWave;
 // chunk filter rejects are skipped, so the stream is unchanged.
 constexpr int kTrimLen = 64;
 
-__device__ __forceinline__ int32_t lower_bound_dev(const int32_t *a, int32_t lo,
-                                                   int32_t hi, int32_t t) {
-  while (lo < hi) {
-    int32_t mid = lo + (hi - lo) / 2;
-    if (a[mid] < t) {
-      lo = mid + 1;
-    } else {
-      hi = mid;
-    }
-  }
-  return lo;
-}
-
-// Space-saving sketch of capacity 32*CELLS spread over one wave64.
-template <int CELLS> struct WaveSketch {
-  static constexpr int LC = (CELLS + 1) / 2; // cells held per physical lane
-  static constexpr int M = 32 * CELLS;
-  int32_t key[LC];
-  float wt[LC];
-  int32_t filled; // wave-uniform: slots taken so far (fill order L*CELLS+c)
-
-  __device__ __forceinline__ void clear() {
-#pragma unroll
-    for (int j = 0; j < LC; ++j) {
-      key[j] = -1;
-      wt[j] = 0.0f;
-    }
-    filled = 0;
-  }
-
-  // Apply one item; k and w are wave-uniform.
-  __device__ __forceinline__ void add(int32_t k, float w) {
-    const int lane = lane_id();
-    bool hit = false;
-#pragma unroll
-    for (int j = 0; j < LC; ++j) {
-      if (key[j] == k) {
-        wt[j] += w;
-        hit = true;
-      }
-    }
-    if (ballot(hit)) {
-      return;
-    }
-    if (filled < M) {
-      // Slot s = L*CELLS + c: logical lane L, cell c -> physical lane
-      // L + 32*(c & 1), local cell c >> 1.
-      int L = filled / CELLS, c = filled - L * CELLS;
-      int owner = L + 32 * (c & 1), jj = c >> 1;
-#pragma unroll
-      for (int j = 0; j < LC; ++j) {
-        if (lane == owner && j == jj) {
-          key[j] = k;
-          wt[j] = w;
-        }
-      }
-      filled += 1;
-      return;
-    }
-    // Evict argmin over slots of (weight, c*32 + L).
-    const int L = lane & 31, h = lane >> 5;
-    float best_w = __builtin_inff();
-    int32_t best_k = 0x7fffffff;
-#pragma unroll
-    for (int j = 0; j < LC; ++j) {
-      int c = 2 * j + h;
-      if (c < CELLS) {
-        int32_t ck = (c << 5) | L;
-        if (wt[j] < best_w || (wt[j] == best_w && ck < best_k)) {
-          best_w = wt[j];
-          best_k = ck;
-        }
-      }
-    }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-      float ow = __shfl_xor(best_w, off, kWave);
-      int32_t ok = __shfl_xor(best_k, off, kWave);
-      if (ow < best_w || (ow == best_w && ok < best_k)) {
-        best_w = ow;
-        best_k = ok;
-      }
-    }
-    int c = best_k >> 5;
-    int owner = (best_k & 31) + 32 * (c & 1), jj = c >> 1;
-#pragma unroll
-    for (int j = 0; j < LC; ++j) {
-      if (lane == owner && j == jj) {
-        key[j] = k;
-        wt[j] += w; // inherits the evicted weight
-      }
-    }
-  }
-
-  // Reference select_top_k: per-logical-lane selection sort (strict '>',
-  // stop at -1), then up to k rounds emitting the head of the lane with the
-  // largest head weight (ties -> smaller lane; exhausted lanes show 0.0f).
-  // Writes all k entries of `out` (unused ones as the zero entry).
-  __device__ __forceinline__ void select_top_k(int32_t k, uint64_t *out) {
-    const int lane = lane_id();
-    // Gather logical lane L's cells into physical lane L (< 32).
-    int32_t fk[CELLS];
-    float fw[CELLS];
-#pragma unroll
-    for (int j = 0; j < LC; ++j) {
-      int32_t hk = __shfl(key[j], (lane & 31) + 32, kWave);
-      float hw = __shfl(wt[j], (lane & 31) + 32, kWave);
-      fk[2 * j] = key[j];
-      fw[2 * j] = wt[j];
-      if (2 * j + 1 < CELLS) {
-        fk[2 * j + 1] = hk;
-        fw[2 * j + 1] = hw;
-      }
-    }
-    // Selection sort, literally as the reference (not stable).
-#pragma unroll
-    for (int i = 0; i < CELLS - 1; ++i) {
-      if (fk[i] == -1) break;
-      int best = i;
-      float bw = fw[i];
-#pragma unroll
-      for (int j = i + 1; j < CELLS; ++j) {
-        if (fk[j] == -1) break;
-        if (fw[j] > bw) {
-          best = j;
-          bw = fw[j];
-        }
-      }
-      if (best != i) {
-        // Swap cells i and best (best is a run-time index: select by loop).
-        int32_t tk = fk[i];
-        float tw = fw[i];
-#pragma unroll
-        for (int j = i + 1; j < CELLS; ++j) {
-          if (j == best) {
-            fk[i] = fk[j];
-            fw[i] = fw[j];
-            fk[j] = tk;
-            fw[j] = tw;
-          }
-        }
-      }
-    }
-    // k-way merge; lane (i & 63) keeps output entry i in register i >> 6.
-    uint64_t outv[4] = {0, 0, 0, 0};
-    for (int32_t i = 0; i < k; ++i) {
-      bool live = lane < 32 && fk[0] != -1;
-      if (ballot(live) == 0) break;
-      float v = lane < 32 ? fw[0] : -__builtin_inff();
-      int32_t who = lane;
-#pragma unroll
-      for (int off = 32; off > 0; off >>= 1) {
-        float ov = __shfl_xor(v, off, kWave);
-        int32_t ow = __shfl_xor(who, off, kWave);
-        if (ov > v || (ov == v && ow < who)) {
-          v = ov;
-          who = ow;
-        }
-      }
-      int winner = __builtin_amdgcn_readfirstlane(who);
-      int32_t wk = readlane(fk[0], winner);
-      float ww = readlane_f(fw[0], winner);
-      int slot = i >> 6;
-      if (lane == (i & 63)) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          if (r == slot) outv[r] = pack_wi(wk, ww);
-        }
-      }
-      if (lane == winner) {
-#pragma unroll
-        for (int j = 0; j < CELLS - 1; ++j) {
-          fk[j] = fk[j + 1];
-          fw[j] = fw[j + 1];
-        }
-        fk[CELLS - 1] = -1;
-        fw[CELLS - 1] = 0.0f;
-      }
-    }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      int idx = r * 64 + lane;
-      if (idx < k) out[idx] = outv[r];
-    }
-  }
-};
-
 // One wave per row (grid-stride).  Rows of length 0 get an all-zero table row.
+// With `chunks` non-null, the waves cover only the rows of the listed chunks.
 template <int CELLS>
 __global__ void __launch_bounds__(kSketchBlock)
     chunk_sketch_kernel(int32_t n, int32_t k, int32_t chunk_size,
@@ -239,14 +50,22 @@ __global__ void __launch_bounds__(kSketchBlock)
                         const int32_t *__restrict__ col_ind,
                         const int32_t *__restrict__ col_ptr,
                         const int32_t *__restrict__ row_ind,
-                        uint64_t *__restrict__ table) {
+                        uint64_t *__restrict__ table,
+                        const int32_t *__restrict__ chunks,
+                        const int32_t *__restrict__ chunk_count) {
   const int lane = lane_id();
   const int64_t wave0 =
       static_cast<int64_t>(blockIdx.x) * kSketchWaves + threadIdx.x / kWave;
   const int64_t nwaves = static_cast<int64_t>(gridDim.x) * kSketchWaves;
+  const int64_t work = chunks ? static_cast<int64_t>(*chunk_count) * chunk_size : n;
   WaveSketch<CELLS> store;
 
-  for (int64_t row64 = wave0; row64 < n; row64 += nwaves) {
+  for (int64_t w = wave0; w < work; w += nwaves) {
+    int64_t row64 = w;
+    if (chunks) {
+      row64 = static_cast<int64_t>(chunks[w / chunk_size]) * chunk_size + (w % chunk_size);
+      if (row64 >= n) continue;
+    }
     const int32_t row = static_cast<int32_t>(row64);
     uint64_t *out = table + static_cast<size_t>(row) * k;
     const int32_t rs = row_ptr[row], re = row_ptr[row + 1];
@@ -317,10 +136,12 @@ template <int CELLS>
 void launch_sketch(Context &ctx, int32_t n, int32_t k, int32_t chunk_size,
                    const int32_t *d_ptr, const int32_t *d_ind,
                    const int32_t *d_col_ptr, const int32_t *d_row_ind,
-                   uint64_t *d_table) {
+                   uint64_t *d_table, const int32_t *d_chunks,
+                   const int32_t *d_chunk_count) {
   int g = ctx.grid_for(ceil_div64(n, kSketchWaves), kSketchBlock, 4);
   chunk_sketch_kernel<CELLS><<<g, kSketchBlock, 0, ctx.stream>>>(
-      n, k, chunk_size, d_ptr, d_ind, d_col_ptr, d_row_ind, d_table);
+      n, k, chunk_size, d_ptr, d_ind, d_col_ptr, d_row_ind, d_table, d_chunks,
+      d_chunk_count);
   SP_LAUNCH_CHECK();
 }
 
@@ -332,11 +153,54 @@ struct ChainCounters {
   double link_weight_sum;
 };
 
+// The visited bitmap of a chain is written by every lane of the wave with the
+// same value (each lane ORs the same bit into the same word), so each lane's
+// own program order makes its later reads see every update: no cross-lane
+// fence is needed inside the chain loop.
+__device__ __forceinline__ void mark_visited(uint32_t *bm, int32_t b) {
+  bm[b >> 5] |= 1u << (b & 31);
+}
+
+// Lowest unvisited bit at or after word *low_word; advances *low_word (the
+// lowest unvisited row never moves backwards).  Returns -1 when none is left.
+__device__ __forceinline__ int32_t next_unvisited(const uint32_t *bm, int32_t words,
+                                                  uint32_t tail_mask, int32_t *low_word) {
+  const int lane = lane_id();
+  while (*low_word < words) {
+    int32_t w = *low_word + lane;
+    uint32_t free_bits = 0u;
+    if (w < words) free_bits = ~bm[w] & (w == words - 1 ? tail_mask : 0xFFFFFFFFu);
+    uint64_t m = ballot(free_bits != 0u);
+    if (m) {
+      int first = __builtin_ctzll(m);
+      uint32_t fb = static_cast<uint32_t>(readlane(static_cast<int32_t>(free_bits), first));
+      *low_word += first;
+      return *low_word * 32 + __builtin_ctz(fb);
+    }
+    *low_word += kWave;
+  }
+  return -1;
+}
+
+// Best (max weight, ties -> smaller index) over the wave; all lanes get it.
+__device__ __forceinline__ void wave_argmax(float *w, int32_t *c) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    float ow = __shfl_xor(*w, off, kWave);
+    int32_t oc = __shfl_xor(*c, off, kWave);
+    if (ow > *w || (ow == *w && oc < *c)) {
+      *w = ow;
+      *c = oc;
+    }
+  }
+}
+
 constexpr int kGreedyBlock = 256;
 constexpr int kGreedyWaves = kGreedyBlock / kWave;
 
-// One wave per chunk.  `words_per_wave` u32 words of visited bitmap per wave
-// live in LDS (use_lds) or in `gbitmap` at chunk * words_per_wave.
+// General greedy: one wave per chunk, table rows read from global memory.
+// `words_per_wave` u32 words of visited bitmap per wave live in LDS (use_lds)
+// or in `gbitmap` at chunk * words_per_wave.
 __global__ void __launch_bounds__(kGreedyBlock)
     greedy_kernel(int32_t n, int32_t k, int32_t chunk_size, int32_t num_chunks,
                   const uint64_t *__restrict__ table, int32_t *__restrict__ order,
@@ -345,7 +209,7 @@ __global__ void __launch_bounds__(kGreedyBlock)
   extern __shared__ uint32_t lds_bitmap[];
   const int lane = lane_id();
   const int wave = threadIdx.x / kWave;
-  const int64_t chunk = static_cast<int64_t>(blockIdx.x) * kGreedyWaves + wave;
+  const int64_t chunk = static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWave) + wave;
   if (chunk >= num_chunks) return;
   const int64_t start64 = chunk * chunk_size;
   const int32_t start = static_cast<int32_t>(start64);
@@ -356,27 +220,23 @@ __global__ void __launch_bounds__(kGreedyBlock)
   const int32_t words = (size + 31) >> 5;
   uint32_t *bm = use_lds ? lds_bitmap + static_cast<size_t>(wave) * words_per_wave
                          : gbitmap + static_cast<size_t>(chunk) * words_per_wave;
-  for (int32_t w = lane; w < words; w += kWave) bm[w] = 0u;
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  // Every lane clears every word, so each lane's later reads follow its own
+  // writes (see mark_visited).
+  for (int32_t w = 0; w < words; ++w) bm[w] = 0u;
 
-  const uint32_t tail_mask =
-      (size & 31) ? ((1u << (size & 31)) - 1u) : 0xFFFFFFFFu;
+  const uint32_t tail_mask = (size & 31) ? ((1u << (size & 31)) - 1u) : 0xFFFFFFFFu;
   int32_t cur = start, pos = start, low_word = 0;
   int32_t restarts = 0, links = 0;
   float link_w = 0.0f;
 
   while (true) {
-    if (lane == 0) {
-      int32_t b = cur - start;
-      bm[b >> 5] |= 1u << (b & 31);
-      order[pos] = cur;
+    mark_visited(bm, cur - start);
+    if (!use_lds) {
+      // Global-memory bitmap: order the store before the loads that test it.
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     }
+    if (lane == 0) order[pos] = cur;
     pos += 1;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
     const uint64_t *row = table + static_cast<size_t>(cur) * k;
     float best_w = -1.0f;
@@ -394,15 +254,7 @@ __global__ void __launch_bounds__(kGreedyBlock)
         best_c = cand;
       }
     }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-      float ow = __shfl_xor(best_w, off, kWave);
-      int32_t oc = __shfl_xor(best_c, off, kWave);
-      if (ow > best_w || (ow == best_w && oc < best_c)) {
-        best_w = ow;
-        best_c = oc;
-      }
-    }
+    wave_argmax(&best_w, &best_c);
     best_c = __builtin_amdgcn_readfirstlane(best_c);
     if (best_c >= 0) {
       links += 1;
@@ -410,24 +262,7 @@ __global__ void __launch_bounds__(kGreedyBlock)
       cur = best_c;
       continue;
     }
-    // Restart at the lowest unvisited row; it never moves backwards.
-    int32_t nxt = -1;
-    while (low_word < words) {
-      int32_t w = low_word + lane;
-      uint32_t free_bits = 0u;
-      if (w < words) {
-        free_bits = ~bm[w] & (w == words - 1 ? tail_mask : 0xFFFFFFFFu);
-      }
-      uint64_t m = ballot(free_bits != 0u);
-      if (m) {
-        int first = __builtin_ctzll(m);
-        uint32_t fb = static_cast<uint32_t>(readlane(static_cast<int32_t>(free_bits), first));
-        low_word += first;
-        nxt = low_word * 32 + __builtin_ctz(fb);
-        break;
-      }
-      low_word += kWave;
-    }
+    int32_t nxt = next_unvisited(bm, words, tail_mask, &low_word);
     if (nxt < 0) break;
     restarts += 1;
     cur = start + nxt;
@@ -439,8 +274,147 @@ __global__ void __launch_bounds__(kGreedyBlock)
   }
 }
 
+// Compact greedy: chunks of at most kGreedyCompactRows rows.  Four waves
+// count each row's valid entries, scan them into per-row offsets and copy
+// the valid entries as (weight bits << 32 | local index) into LDS; then wave
+// 0 runs the chain on LDS alone.  A slice with more than `entry_cap` valid
+// entries keeps the offsets in LDS and reads the entries from global memory.
+constexpr int kGreedyCompactRows = 4096;
+
+// Dynamic LDS layout: entries u64[entry_cap] | offsets i32[rows_cap + 1] |
+// bitmap u32[ceil(rows_cap / 32)].
+size_t greedy_compact_lds(int32_t rows_cap, int32_t entry_cap) {
+  return static_cast<size_t>(entry_cap) * 8u + static_cast<size_t>(rows_cap + 1) * 4u +
+         static_cast<size_t>((rows_cap + 31) / 32) * 4u;
+}
+
+__global__ void __launch_bounds__(kGreedyBlock)
+    greedy_compact_kernel(int32_t n, int32_t k, int32_t chunk_size,
+                          const uint64_t *__restrict__ table, int32_t *__restrict__ order,
+                          ChainCounters *counters, int32_t rows_cap, int32_t entry_cap) {
+  extern __shared__ uint64_t smem_u64[];
+  __shared__ int32_t s_total;
+  uint64_t *s_ent = smem_u64;
+  int32_t *s_off = reinterpret_cast<int32_t *>(smem_u64 + entry_cap);
+  uint32_t *s_bm = reinterpret_cast<uint32_t *>(s_off + rows_cap + 1);
+
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int wave = tid / kWave;
+  const int64_t chunk = blockIdx.x;
+  const int64_t start64 = chunk * chunk_size;
+  const int32_t start = static_cast<int32_t>(start64);
+  const int32_t end =
+      static_cast<int32_t>(start64 + chunk_size > n ? n : start64 + chunk_size);
+  const int32_t size = end - start;
+  const int32_t words = (size + 31) >> 5;
+  const uint64_t *slice = table + static_cast<size_t>(start) * k;
+  const int64_t slice_len = static_cast<int64_t>(size) * k;
+
+  for (int32_t r = tid; r <= size; r += kGreedyBlock) s_off[r] = 0;
+  for (int32_t w = tid; w < words; w += kGreedyBlock) s_bm[w] = 0u;
+  __syncthreads();
+  // Per-row valid counts (valid entries form a prefix of each row).
+  for (int64_t e0 = static_cast<int64_t>(tid) * 4; e0 < slice_len;
+       e0 += static_cast<int64_t>(kGreedyBlock) * 4) {
+    uint64_t v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) v[u] = (e0 + u < slice_len) ? slice[e0 + u] : 0;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if (e0 + u < slice_len && wi_index(v[u]) >= 0) {
+        atomicAdd(&s_off[(e0 + u) / k + 1], 1);
+      }
+    }
+  }
+  __syncthreads();
+  // Inclusive scan of s_off[1..size] by wave 0 -> offsets.
+  if (wave == 0) {
+    int32_t carry = 0;
+    for (int32_t base = 1; base <= size; base += kWave) {
+      int32_t i = base + lane;
+      int32_t v = i <= size ? s_off[i] : 0;
+      int32_t incl = wave_incl_scan(v) + carry;
+      if (i <= size) s_off[i] = incl;
+      carry = readlane(incl, kWave - 1);
+    }
+    if (lane == 0) s_total = carry;
+  }
+  __syncthreads();
+  const int32_t total = s_total;
+  const bool compact = total <= entry_cap;
+  if (compact) {
+    for (int64_t e = tid; e < slice_len; e += kGreedyBlock) {
+      uint64_t v = slice[e];
+      int32_t c = wi_index(v);
+      if (c >= 0) {
+        int32_t r = static_cast<int32_t>(e / k), j = static_cast<int32_t>(e % k);
+        uint32_t local = (c >= start && c < end) ? static_cast<uint32_t>(c - start)
+                                                 : 0xFFFFFFFFu;
+        s_ent[s_off[r] + j] = (v & 0xFFFFFFFF00000000ull) | local;
+      }
+    }
+  }
+  __syncthreads();
+  if (wave != 0) return;
+
+  const uint32_t tail_mask = (size & 31) ? ((1u << (size & 31)) - 1u) : 0xFFFFFFFFu;
+  int32_t cur = 0, pos = start, low_word = 0;
+  int32_t restarts = 0, links = 0;
+  float link_w = 0.0f;
+  while (true) {
+    mark_visited(s_bm, cur);
+    if (lane == 0) order[pos] = start + cur;
+    pos += 1;
+    const int32_t d0 = s_off[cur], d1 = s_off[cur + 1];
+    float best_w = -1.0f;
+    int32_t best_c = -1;
+    if (d1 > d0) {
+      for (int32_t j = lane; j < d1 - d0; j += kWave) {
+        int32_t cl;
+        float w;
+        if (compact) {
+          uint64_t e = s_ent[d0 + j];
+          cl = static_cast<int32_t>(static_cast<uint32_t>(e));
+          w = wi_weight(e);
+        } else {
+          uint64_t e = slice[static_cast<size_t>(cur) * k + j];
+          int32_t c = wi_index(e);
+          cl = (c >= start && c < end) ? c - start : -1;
+          w = wi_weight(e);
+        }
+        if (cl < 0) continue; // outside the chunk
+        if (s_bm[cl >> 5] & (1u << (cl & 31))) continue;
+        if (w > best_w || (w == best_w && cl < best_c)) {
+          best_w = w;
+          best_c = cl;
+        }
+      }
+      wave_argmax(&best_w, &best_c);
+      best_c = __builtin_amdgcn_readfirstlane(best_c);
+    }
+    if (best_c >= 0) {
+      links += 1;
+      link_w += readlane_f(best_w, 0);
+      cur = best_c;
+      continue;
+    }
+    int32_t nxt = next_unvisited(s_bm, words, tail_mask, &low_word);
+    if (nxt < 0) break;
+    restarts += 1;
+    cur = nxt;
+  }
+  if (counters != nullptr && lane == 0) {
+    atomicAdd(&counters->restarts, restarts);
+    atomicAdd(&counters->links, links);
+    atomicAdd(&counters->link_weight_sum, static_cast<double>(link_w));
+  }
+}
+
 // ---- table statistics -------------------------------------------------------
 
+// One lane per row; each wave reads its 64 rows' entries as a coalesced
+// column sweep (entry j of 64 consecutive rows per step).
 __global__ void __launch_bounds__(256)
     top_k_stats_kernel(int32_t n, int32_t k, const uint64_t *__restrict__ table,
                        TopKTotals *totals) {
@@ -506,9 +480,13 @@ void validate_sketch_args(int32_t k, float oversampling, int32_t chunk_size) {
   SP_EXPECT(m <= 512, "expect k * oversampling <= 512");
 }
 
-// Workspace of the sketch stage: table + optional CSC.
-size_t sketch_ws_bytes(int32_t n, int32_t nnz, int32_t k, bool is_symmetric) {
+// ---- table construction (both paths) ---------------------------------------
+
+size_t table_ws_bytes(int32_t n, int32_t nnz, int32_t k, int32_t chunk_size,
+                      bool is_symmetric) {
   size_t b = ws_bytes<uint64_t>(static_cast<size_t>(n) * k);
+  int64_t chunks = ceil_div64(n, chunk_size);
+  b += ws_bytes<int32_t>(static_cast<size_t>(chunks)) + ws_bytes<int32_t>(2);
   if (!is_symmetric) {
     b += ws_bytes<int32_t>(static_cast<size_t>(n) + 1) +
          ws_bytes<int32_t>(static_cast<size_t>(nnz)) + csr2csc_ws_bytes(n, nnz);
@@ -516,19 +494,71 @@ size_t sketch_ws_bytes(int32_t n, int32_t nnz, int32_t k, bool is_symmetric) {
   return b;
 }
 
-struct ResolvedCsc {
-  const int32_t *ptr;
-  const int32_t *ind;
-};
+// Fills `table` (n*k) for the chunked sketch.  Records the transpose and
+// similarity spans when the spans are enabled.
+void build_table(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
+                 const int32_t *d_ind, bool is_symmetric, int32_t k, int32_t m_cap,
+                 int32_t chunk_size, uint64_t *table, EventSpan *t_csc,
+                 EventSpan *t_sim) {
+  const int64_t chunks = ceil_div64(n, chunk_size);
+  int32_t *overflow = ctx.take<int32_t>(static_cast<size_t>(chunks));
+  int32_t *overflow_count = ctx.take<int32_t>(2);
+  const bool local = chunk_local_supported(n, chunk_size);
 
-ResolvedCsc resolve_csc(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
-                        const int32_t *d_ind, bool is_symmetric) {
-  // Reference: sporder/src/common/csr2csc.h:49-59.
-  if (is_symmetric) return {d_ptr, d_ind};
-  int32_t *cp = ctx.take<int32_t>(static_cast<size_t>(n) + 1);
-  int32_t *ri = ctx.take<int32_t>(static_cast<size_t>(nnz));
-  csr2csc(ctx, n, nnz, d_ptr, d_ind, cp, ri);
-  return {cp, ri};
+  auto global_csc = [&](const int32_t **cp, const int32_t **ri) {
+    // Reference: sporder/src/common/csr2csc.h:49-59.
+    if (is_symmetric) {
+      *cp = d_ptr;
+      *ri = d_ind;
+      return;
+    }
+    int32_t *p = ctx.take<int32_t>(static_cast<size_t>(n) + 1);
+    int32_t *r = ctx.take<int32_t>(static_cast<size_t>(nnz));
+    csr2csc(ctx, n, nnz, d_ptr, d_ind, p, r);
+    *cp = p;
+    *ri = r;
+  };
+
+  if (!local) {
+    const int32_t *cp, *ri;
+    t_csc->begin(ctx.stream);
+    global_csc(&cp, &ri);
+    t_csc->end(ctx.stream);
+    t_sim->begin(ctx.stream);
+    chunk_sketch_top_k(ctx, n, k, chunk_size, m_cap, d_ptr, d_ind, cp, ri, table);
+    t_sim->end(ctx.stream);
+    return;
+  }
+
+  fill_u32(ctx, overflow_count, 2, 0u);
+  t_sim->begin(ctx.stream);
+  chunk_local_sketch_top_k(ctx, n, k, chunk_size, m_cap, d_ptr, d_ind, table, overflow,
+                           overflow_count);
+  if (is_symmetric) {
+    // The CSR is its own transpose: run the fallback over the overflow list
+    // without waiting for its length (an empty list exits at once).
+    chunk_sketch_top_k(ctx, n, k, chunk_size, m_cap, d_ptr, d_ind, d_ptr, d_ind, table,
+                       overflow, overflow_count);
+    t_sim->end(ctx.stream);
+    t_csc->begin(ctx.stream);
+    t_csc->end(ctx.stream);
+    return;
+  }
+  t_sim->end(ctx.stream);
+  int32_t h_overflow = 0;
+  SP_HIP(hipMemcpyAsync(&h_overflow, overflow_count, sizeof(int32_t), hipMemcpyDeviceToHost,
+                        ctx.stream));
+  ctx.sync();
+  t_csc->begin(ctx.stream);
+  if (h_overflow > 0) {
+    const int32_t *cp, *ri;
+    global_csc(&cp, &ri);
+    t_csc->end(ctx.stream);
+    chunk_sketch_top_k(ctx, n, k, chunk_size, m_cap, d_ptr, d_ind, cp, ri, table, overflow,
+                       overflow_count);
+  } else {
+    t_csc->end(ctx.stream);
+  }
 }
 
 } // namespace
@@ -536,13 +566,14 @@ ResolvedCsc resolve_csc(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_p
 void chunk_sketch_top_k(Context &ctx, int32_t n, int32_t k, int32_t chunk_size,
                         int32_t m_capacity, const int32_t *d_ptr,
                         const int32_t *d_ind, const int32_t *d_col_ptr,
-                        const int32_t *d_row_ind, uint64_t *d_table) {
+                        const int32_t *d_row_ind, uint64_t *d_table,
+                        const int32_t *d_chunks, const int32_t *d_chunk_count) {
   SP_EXPECT(k <= 256, "k must be <= 256");
   switch (m_capacity / 32) {
 #define SP_CASE(C)                                                             \
   case C:                                                                      \
     launch_sketch<C>(ctx, n, k, chunk_size, d_ptr, d_ind, d_col_ptr,           \
-                     d_row_ind, d_table);                                      \
+                     d_row_ind, d_table, d_chunks, d_chunk_count);             \
     break;
     SP_CASE(1) SP_CASE(2) SP_CASE(3) SP_CASE(4) SP_CASE(5) SP_CASE(6)
     SP_CASE(7) SP_CASE(8) SP_CASE(9) SP_CASE(10) SP_CASE(11) SP_CASE(12)
@@ -589,27 +620,27 @@ void sporder_chunk_similarity_greedy(sporder_context_t h, int32_t n,
     stats->chunk_size_used = chunk_size;
   }
   const int64_t num_chunks = ceil_div64(n, chunk_size);
-  const int64_t words64 = ceil_div64(std::min<int64_t>(chunk_size, n), 32);
-  SP_EXPECT(words64 < (int64_t(1) << 30), "chunk too large");
-  const int32_t words = static_cast<int32_t>(words64);
+  const int32_t rows_max = static_cast<int32_t>(std::min<int64_t>(chunk_size, n));
+  const bool compact = rows_max <= kGreedyCompactRows;
+  const int32_t words = static_cast<int32_t>(ceil_div64(rows_max, 32));
+  // General greedy: bitmap in LDS when small enough, else in the workspace.
   const size_t lds_need = static_cast<size_t>(words) * 4u;
-  // Up to 4 chunks per workgroup share the LDS; very large chunks fall back
-  // to a bitmap in the workspace.
-  const bool use_lds = lds_need <= 64u * 1024u && lds_need <= ctx.lds_per_block;
-  const int waves_per_block =
-      use_lds ? static_cast<int>(std::max<size_t>(
-                    1, std::min<size_t>(kGreedyWaves, (64u * 1024u) / std::max<size_t>(lds_need, 1))))
-              : kGreedyWaves;
+  const bool bitmap_lds = lds_need <= 64u * 1024u && lds_need <= ctx.lds_per_block;
+  const int general_wpb =
+      bitmap_lds ? static_cast<int>(std::max<size_t>(
+                       1, std::min<size_t>(kGreedyWaves, (64u * 1024u) / std::max<size_t>(lds_need, 1))))
+                 : kGreedyWaves;
 
-  size_t need = sketch_ws_bytes(n, nnz, k, is_symmetric) + ws_bytes<ChainCounters>(1) +
-                ws_bytes<TopKTotals>(1);
-  if (!use_lds) need += ws_bytes<uint32_t>(static_cast<size_t>(num_chunks) * words);
+  size_t need = table_ws_bytes(n, nnz, k, chunk_size, is_symmetric) +
+                ws_bytes<ChainCounters>(1) + ws_bytes<TopKTotals>(1);
+  if (!compact && !bitmap_lds) need += ws_bytes<uint32_t>(static_cast<size_t>(num_chunks) * words);
   ctx.reserve(need);
   uint64_t *table = ctx.take<uint64_t>(static_cast<size_t>(n) * k);
   ChainCounters *counters = ctx.take<ChainCounters>(1);
   TopKTotals *totals = ctx.take<TopKTotals>(1);
-  uint32_t *gbitmap =
-      use_lds ? nullptr : ctx.take<uint32_t>(static_cast<size_t>(num_chunks) * words);
+  uint32_t *gbitmap = (!compact && !bitmap_lds)
+                          ? ctx.take<uint32_t>(static_cast<size_t>(num_chunks) * words)
+                          : nullptr;
 
   EventSpan t_csc, t_sim, t_greedy;
   t_csc.create(timing != nullptr);
@@ -617,30 +648,30 @@ void sporder_chunk_similarity_greedy(sporder_context_t h, int32_t n,
   t_greedy.create(timing != nullptr);
 
   if (stats) {
-    // Zeroed by a kernel (not a memset node) so the call stays capturable.
     zero_words(ctx, counters, sizeof(ChainCounters));
     zero_words(ctx, totals, sizeof(TopKTotals));
   }
 
-  t_csc.begin(ctx.stream);
-  ResolvedCsc csc = resolve_csc(ctx, n, nnz, d_ptr, d_ind, is_symmetric);
-  t_csc.end(ctx.stream);
-
-  t_sim.begin(ctx.stream);
-  chunk_sketch_top_k(ctx, n, k, chunk_size, m_cap, d_ptr, d_ind, csc.ptr, csc.ind,
-                     table);
-  t_sim.end(ctx.stream);
+  build_table(ctx, n, nnz, d_ptr, d_ind, is_symmetric, k, m_cap, chunk_size, table, &t_csc,
+              &t_sim);
   if (stats) top_k_stats(ctx, n, k, table, totals);
 
   t_greedy.begin(ctx.stream);
-  {
-    int wpb = use_lds ? waves_per_block : kGreedyWaves;
-    int64_t blocks = ceil_div64(num_chunks, wpb);
-    size_t lds = use_lds ? static_cast<size_t>(wpb) * words * 4u : 0;
-    greedy_kernel<<<dim3(static_cast<unsigned>(blocks)), wpb * kWave, lds,
-                    ctx.stream>>>(n, k, chunk_size, static_cast<int32_t>(num_chunks),
-                                  table, d_new_order, stats ? counters : nullptr,
-                                  gbitmap, words, use_lds ? 1 : 0);
+  if (compact) {
+    // About 20 KiB of LDS per chunk at chunk_size 1024: several chunks per CU.
+    const int32_t entry_cap = 2048;
+    greedy_compact_kernel<<<dim3(static_cast<unsigned>(num_chunks)), kGreedyBlock,
+                            greedy_compact_lds(rows_max, entry_cap), ctx.stream>>>(
+        n, k, chunk_size, table, d_new_order, stats ? counters : nullptr, rows_max,
+        entry_cap);
+    SP_LAUNCH_CHECK();
+  } else {
+    int64_t blocks = ceil_div64(num_chunks, general_wpb);
+    size_t lds = bitmap_lds ? static_cast<size_t>(general_wpb) * words * 4u : 0;
+    greedy_kernel<<<dim3(static_cast<unsigned>(blocks)), general_wpb * kWave, lds,
+                    ctx.stream>>>(n, k, chunk_size, static_cast<int32_t>(num_chunks), table,
+                                  d_new_order, stats ? counters : nullptr, gbitmap, words,
+                                  bitmap_lds ? 1 : 0);
     SP_LAUNCH_CHECK();
   }
   t_greedy.end(ctx.stream);
@@ -688,11 +719,11 @@ void sporder_chunk_similarity_top_k(sporder_context_t h, int32_t n, int32_t nnz,
   SP_EXPECT(n >= 1 && nnz >= 0, "expect n >= 1 and nnz >= 0");
   validate_sketch_args(k, oversampling, chunk_size);
   Context &ctx = h->impl;
-  ctx.reserve(sketch_ws_bytes(n, nnz, k, is_symmetric));
+  ctx.reserve(table_ws_bytes(n, nnz, k, chunk_size, is_symmetric));
   uint64_t *table = ctx.take<uint64_t>(static_cast<size_t>(n) * k);
-  ResolvedCsc csc = resolve_csc(ctx, n, nnz, d_ptr, d_ind, is_symmetric);
-  chunk_sketch_top_k(ctx, n, k, chunk_size, sketch_m(k, oversampling), d_ptr, d_ind,
-                     csc.ptr, csc.ind, table);
+  EventSpan off_a, off_b;
+  build_table(ctx, n, nnz, d_ptr, d_ind, is_symmetric, k, sketch_m(k, oversampling),
+              chunk_size, table, &off_a, &off_b);
   int64_t count = static_cast<int64_t>(n) * k;
   int g = ctx.grid_for(ceil_div64(count, 256), 256, 4);
   unpack_table_kernel<<<g, 256, 0, ctx.stream>>>(count, table, d_indices, d_weights);
@@ -721,7 +752,7 @@ void sporder_similarity_graph(sporder_context_t h, int32_t n, int32_t nnz,
     stats->k_used = k;
     stats->m_used = m_cap;
   }
-  ctx.reserve(sketch_ws_bytes(n, nnz, k, is_symmetric) + ws_bytes<TopKTotals>(1));
+  ctx.reserve(table_ws_bytes(n, nnz, k, n, is_symmetric) + ws_bytes<TopKTotals>(1));
   uint64_t *table = ctx.take<uint64_t>(static_cast<size_t>(n) * k);
   TopKTotals *totals = ctx.take<TopKTotals>(1);
   EventSpan t_csc, t_sim, t_unpack;
@@ -729,12 +760,7 @@ void sporder_similarity_graph(sporder_context_t h, int32_t n, int32_t nnz,
   t_sim.create(timing != nullptr);
   t_unpack.create(timing != nullptr);
 
-  t_csc.begin(ctx.stream);
-  ResolvedCsc csc = resolve_csc(ctx, n, nnz, d_ptr, d_ind, is_symmetric);
-  t_csc.end(ctx.stream);
-  t_sim.begin(ctx.stream);
-  chunk_sketch_top_k(ctx, n, k, n, m_cap, d_ptr, d_ind, csc.ptr, csc.ind, table);
-  t_sim.end(ctx.stream);
+  build_table(ctx, n, nnz, d_ptr, d_ind, is_symmetric, k, m_cap, n, table, &t_csc, &t_sim);
   if (stats) {
     zero_words(ctx, totals, sizeof(TopKTotals));
     top_k_stats(ctx, n, k, table, totals);

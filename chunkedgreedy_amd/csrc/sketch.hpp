@@ -1,0 +1,209 @@
+// sketch.hpp -- the wave64 space-saving sketch shared by the csg kernels.
+//
+// Semantics: reference sporder/src/common/warp_spacesaving.cuh:12-151 and the
+// arg-reductions of sporder/src/common/cuda_util.cuh:66-87.  The reference
+// keeps M = 32*CELLS slots in one 32-lane warp: logical lane L owns cells
+// c = 0..CELLS-1.  Here one wave64 holds the slots of one row: physical lane p
+// holds logical lane L = p & 31 and the cells c = 2j + (p >> 5),
+// j = 0..ceil(CELLS/2)-1.  Every tie rule of the reference depends only on
+// (L, c), so the arrangement is free:
+//   - a new key goes to the first empty slot in order s = L*CELLS + c (slots
+//     never empty again), a wave-uniform counter instead of find(-1) + ballot;
+//   - eviction takes the minimum of (weight, c*32 + L), reduced over the wave
+//     with a butterfly, and the new key inherits the evicted weight;
+//   - output merges the per-logical-lane selection-sorted lists, largest head
+//     weight first, ties to the smaller logical lane.
+#pragma once
+
+#include "common.hpp"
+
+namespace sporder_hip {
+
+__device__ __forceinline__ int32_t lower_bound_dev(const int32_t *a, int32_t lo,
+                                                   int32_t hi, int32_t t) {
+  while (lo < hi) {
+    int32_t mid = lo + (hi - lo) / 2;
+    if (a[mid] < t) {
+      lo = mid + 1;
+    } else {
+      hi = mid;
+    }
+  }
+  return lo;
+}
+
+// Space-saving sketch of capacity 32*CELLS spread over one wave64.
+template <int CELLS> struct WaveSketch {
+  static constexpr int LC = (CELLS + 1) / 2; // cells held per physical lane
+  static constexpr int M = 32 * CELLS;
+  int32_t key[LC];
+  float wt[LC];
+  int32_t filled; // wave-uniform: slots taken so far (fill order L*CELLS+c)
+
+  __device__ __forceinline__ void clear() {
+#pragma unroll
+    for (int j = 0; j < LC; ++j) {
+      key[j] = -1;
+      wt[j] = 0.0f;
+    }
+    filled = 0;
+  }
+
+  // Apply one item; k and w are wave-uniform.
+  __device__ __forceinline__ void add(int32_t k, float w) {
+    const int lane = lane_id();
+    bool hit = false;
+#pragma unroll
+    for (int j = 0; j < LC; ++j) {
+      if (key[j] == k) {
+        wt[j] += w;
+        hit = true;
+      }
+    }
+    if (ballot(hit)) {
+      return;
+    }
+    if (filled < M) {
+      // Slot s = L*CELLS + c: logical lane L, cell c -> physical lane
+      // L + 32*(c & 1), local cell c >> 1.
+      int L = filled / CELLS, c = filled - L * CELLS;
+      int owner = L + 32 * (c & 1), jj = c >> 1;
+#pragma unroll
+      for (int j = 0; j < LC; ++j) {
+        if (lane == owner && j == jj) {
+          key[j] = k;
+          wt[j] = w;
+        }
+      }
+      filled += 1;
+      return;
+    }
+    // Evict argmin over slots of (weight, c*32 + L).
+    const int L = lane & 31, h = lane >> 5;
+    float best_w = __builtin_inff();
+    int32_t best_k = 0x7fffffff;
+#pragma unroll
+    for (int j = 0; j < LC; ++j) {
+      int c = 2 * j + h;
+      if (c < CELLS) {
+        int32_t ck = (c << 5) | L;
+        if (wt[j] < best_w || (wt[j] == best_w && ck < best_k)) {
+          best_w = wt[j];
+          best_k = ck;
+        }
+      }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      float ow = __shfl_xor(best_w, off, kWave);
+      int32_t ok = __shfl_xor(best_k, off, kWave);
+      if (ow < best_w || (ow == best_w && ok < best_k)) {
+        best_w = ow;
+        best_k = ok;
+      }
+    }
+    int c = best_k >> 5;
+    int owner = (best_k & 31) + 32 * (c & 1), jj = c >> 1;
+#pragma unroll
+    for (int j = 0; j < LC; ++j) {
+      if (lane == owner && j == jj) {
+        key[j] = k;
+        wt[j] += w; // inherits the evicted weight
+      }
+    }
+  }
+
+  // Reference select_top_k: per-logical-lane selection sort (strict '>',
+  // stop at -1), then up to k rounds emitting the head of the lane with the
+  // largest head weight (ties -> smaller lane; exhausted lanes show 0.0f).
+  // Writes all k entries of `out` (unused ones as the zero entry).
+  __device__ __forceinline__ void select_top_k(int32_t k, uint64_t *out) {
+    const int lane = lane_id();
+    // Gather logical lane L's cells into physical lane L (< 32).
+    int32_t fk[CELLS];
+    float fw[CELLS];
+#pragma unroll
+    for (int j = 0; j < LC; ++j) {
+      int32_t hk = __shfl(key[j], (lane & 31) + 32, kWave);
+      float hw = __shfl(wt[j], (lane & 31) + 32, kWave);
+      fk[2 * j] = key[j];
+      fw[2 * j] = wt[j];
+      if (2 * j + 1 < CELLS) {
+        fk[2 * j + 1] = hk;
+        fw[2 * j + 1] = hw;
+      }
+    }
+    // Selection sort, literally as the reference (not stable).
+#pragma unroll
+    for (int i = 0; i < CELLS - 1; ++i) {
+      if (fk[i] == -1) break;
+      int best = i;
+      float bw = fw[i];
+#pragma unroll
+      for (int j = i + 1; j < CELLS; ++j) {
+        if (fk[j] == -1) break;
+        if (fw[j] > bw) {
+          best = j;
+          bw = fw[j];
+        }
+      }
+      if (best != i) {
+        // Swap cells i and best (best is a run-time index: select by loop).
+        int32_t tk = fk[i];
+        float tw = fw[i];
+#pragma unroll
+        for (int j = i + 1; j < CELLS; ++j) {
+          if (j == best) {
+            fk[i] = fk[j];
+            fw[i] = fw[j];
+            fk[j] = tk;
+            fw[j] = tw;
+          }
+        }
+      }
+    }
+    // k-way merge; lane (i & 63) keeps output entry i in register i >> 6.
+    uint64_t outv[4] = {0, 0, 0, 0};
+    for (int32_t i = 0; i < k; ++i) {
+      bool live = lane < 32 && fk[0] != -1;
+      if (ballot(live) == 0) break;
+      float v = lane < 32 ? fw[0] : -__builtin_inff();
+      int32_t who = lane;
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) {
+        float ov = __shfl_xor(v, off, kWave);
+        int32_t ow = __shfl_xor(who, off, kWave);
+        if (ov > v || (ov == v && ow < who)) {
+          v = ov;
+          who = ow;
+        }
+      }
+      int winner = __builtin_amdgcn_readfirstlane(who);
+      int32_t wk = readlane(fk[0], winner);
+      float ww = readlane_f(fw[0], winner);
+      int slot = i >> 6;
+      if (lane == (i & 63)) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          if (r == slot) outv[r] = pack_wi(wk, ww);
+        }
+      }
+      if (lane == winner) {
+#pragma unroll
+        for (int j = 0; j < CELLS - 1; ++j) {
+          fk[j] = fk[j + 1];
+          fw[j] = fw[j + 1];
+        }
+        fk[CELLS - 1] = -1;
+        fw[CELLS - 1] = 0.0f;
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      int idx = r * 64 + lane;
+      if (idx < k) out[idx] = outv[r];
+    }
+  }
+};
+
+} // namespace sporder_hip

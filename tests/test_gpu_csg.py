@@ -206,3 +206,43 @@ def test_golden_csr_cases(sporder, case):
         exp_bits = chk["expected_bits"] + [0] * (k - len(chk["expected"]))
         assert gi.cpu().numpy()[r].tolist() == exp_idx, chk
         assert weight_bits(gw.cpu().numpy()[r]).tolist() == exp_bits, chk
+
+
+def dense_random(n, deg, seed, symmetric):
+    rng = np.random.default_rng(seed)
+    rows = np.repeat(np.arange(n), deg)
+    cols = rng.integers(0, n, size=n * deg)
+    if symmetric:
+        rows, cols = np.concatenate([rows, cols]), np.concatenate([cols, rows])
+    keys = np.unique(rows.astype(np.int64) * n + cols)
+    r, c = keys // n, keys % n
+    ptr = np.zeros(n + 1, np.int64)
+    np.cumsum(np.bincount(r, minlength=n), out=ptr[1:])
+    return ptr.astype(np.int32), c.astype(np.int32)
+
+
+@pytest.mark.parametrize("symmetric", [False, True])
+@pytest.mark.parametrize("chunk", [4096, 1500])
+def test_overflow_chunks_take_global_path(sporder, symmetric, chunk):
+    """Chunks with more nonzeros than the LDS key capacity (32768) go to the
+    global-CSC kernel; the result is still bit-exact."""
+    ptr, ind = dense_random(12000, 20 if symmetric else 40, 31, symmetric)
+    assert synth.is_pattern_symmetric(ptr, ind) == symmetric
+    check_table(sporder, ptr, ind, 16, 4.0, chunk, symmetric)
+    dptr, dind = dev_csr(ptr, ind)
+    g = sporder.chunk_similarity_greedy(dptr, dind, is_symmetric=symmetric, chunk_size=chunk)
+    o, _ = oracle.chunk_similarity_greedy(ptr, ind, is_symmetric=symmetric, chunk_size=chunk)
+    assert np.array_equal(g.cpu().numpy(), o)
+
+
+def test_greedy_compact_overflow_entries(sporder):
+    """A chunk whose top-k slice has more valid entries than the compact LDS
+    capacity (2048) reads entries from global memory: same order."""
+    ptr, ind = dense_random(4096, 12, 32, True)
+    for chunk in (4096, 4000):
+        dptr, dind = dev_csr(ptr, ind)
+        g, s = sporder.chunk_similarity_greedy(dptr, dind, is_symmetric=True, chunk_size=chunk,
+                                               with_stats=True)
+        o, os_ = oracle.chunk_similarity_greedy(ptr, ind, is_symmetric=True, chunk_size=chunk)
+        assert s["avg_degree"] * 4096 > 2048
+        assert np.array_equal(g.cpu().numpy(), o)
