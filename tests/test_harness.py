@@ -1,0 +1,84 @@
+"""Host logic of the harness counterparts and the generators (CPU), and the
+plugins end to end on the GPU."""
+
+import numpy as np
+import pytest
+import scipy.sparse as sp
+
+import oracle
+from chunkedgreedy_amd import harness, synth
+
+
+def test_row_perm_and_apply_row_perm():
+    a = sp.random(50, 50, density=0.1, format="csr", random_state=1, dtype=np.float32)
+    perm = np.random.default_rng(0).permutation(50)
+    assert np.array_equal(harness.row_perm_from_order(perm, 50), perm)
+    with pytest.raises(ValueError):
+        harness.row_perm_from_order(perm[:-1], 50)
+    b = harness.apply_row_perm(a, perm)
+    assert np.allclose(b.toarray(), a.toarray()[perm][:, perm])
+
+
+def test_spmm_registry():
+    m = harness.SpMMMethod.create("hip-csr-spmm")
+    assert m.name == "hip-csr-spmm" and m.tc_h == 0 and m.uses_feature_dim
+    assert harness.SpMMMethod.create("hip-csr-spmm-merge").algo == "merge_path"
+    with pytest.raises(ValueError):
+        harness.SpMMMethod.create("cusparse-spmm")
+
+
+@pytest.mark.parametrize("gen,sym", [(lambda: synth.config1(1), False),
+                                     (lambda: synth.stencil7(6, 2), True),
+                                     (lambda: synth.rmat(9, 8, 3), True),
+                                     (lambda: synth.chung_lu(3000, 2.1, 25, 4), True)])
+def test_generators_shape(gen, sym):
+    ptr, ind, val = gen()
+    n = ptr.shape[0] - 1
+    assert ptr[0] == 0 and ptr[-1] == ind.shape[0] == val.shape[0]
+    assert ind.min() >= 0 and ind.max() < n
+    rows = np.repeat(np.arange(n), np.diff(ptr))
+    key = rows.astype(np.int64) * n + ind
+    assert np.all(np.diff(key) > 0)  # sorted, distinct per row
+    assert synth.is_pattern_symmetric(ptr, ind) == sym
+
+
+def test_config1_planted_structure():
+    ptr, ind, val = synth.config1(1)
+    assert ptr.shape[0] - 1 == 20_000 and ind.shape[0] == 200_000
+    assert np.all(np.diff(ptr) == 10)
+    assert val.min() >= -1.0 and val.max() < 1.0
+
+
+def test_stencil_nnz_closed_form():
+    g = 9
+    ptr, _, val = synth.stencil7(g, 1)
+    assert ptr[-1] == 7 * g**3 - 6 * g**2
+    assert np.isclose(val.sum(), 6 * g**3 - (6 * g**3 - 6 * g**2))
+
+
+@pytest.mark.gpu
+def test_reorder_plugin_matches_oracle(sporder):
+    ptr, ind, val = synth.config1(8)
+    a = sp.csr_matrix((val, ind, ptr), shape=(20_000, 20_000))
+    res = harness.reorder(a, {"k": 0, "oversampling": 0.0, "chunk_size": 0,
+                              "auto_detect_symmetric": True})
+    o, _ = oracle.chunk_similarity_greedy(ptr, ind, is_symmetric=False)
+    assert np.array_equal(res.row_perm, o.astype(np.int64))
+    assert res.reorder_time_ms > 0 and res.effective_params == {"is_symmetric": False}
+    assert set(res.timing_breakdown) == {"csr2csc_ms", "similarity_ms", "chunk_greedy_ms"}
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", ["hip-csr-spmm", "hip-csr-spmm-merge"])
+def test_spmm_plugin(sporder, name):
+    ptr, ind, val = synth.config1(9)
+    a = sp.csr_matrix((val, ind, ptr), shape=(20_000, 20_000))
+    m = harness.SpMMMethod.create(name)
+    m.build()
+    prepared = m.prepare(a)
+    B = harness.generate_dense(20_000, 32, device="cuda:0")
+    out, ms = m.run(prepared, B)
+    ref = a.astype(np.float64) @ B.cpu().numpy().astype(np.float64)
+    assert np.abs(out.cpu().numpy() - ref).max() / np.abs(ref).max() < 1e-5
+    assert ms > 0
+    assert harness.time_run(m, prepared, B, warmup=2, iterations=3) > 0
