@@ -63,6 +63,9 @@ def main():
     ap.add_argument("--rows", type=int, default=1 << 20, help="C2 row count (default 2^20)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--spmm-iters", type=int, default=100)
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
+                    help="first run one device-to-device copy of BYTES (a kernel of known "
+                         "traffic for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -80,6 +83,14 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+
+    if args.copy_calibration > 0:
+        src = torch.ones(args.copy_calibration // 4, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copy calibration: {args.copy_calibration} bytes read + written")
+        del src, dst
 
     n_rows = args.rows
     blocks = n_rows // 64

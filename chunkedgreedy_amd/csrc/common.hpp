@@ -40,7 +40,7 @@ namespace sporder_hip {
 
 constexpr int kWave = 64;
 
-inline int64_t ceil_div64(int64_t a, int64_t b) { return (a + b - 1) / b; }
+__host__ __device__ inline int64_t ceil_div64(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // Bump allocator over a grow-only device buffer owned by the context.
 // reserve() must be called with the call's total before any take().
@@ -158,16 +158,16 @@ void chunk_sketch_top_k(Context &ctx, int32_t n, int32_t k, int32_t chunk_size,
                         const int32_t *d_chunk_count = nullptr);
 
 // Chunk-local variant: one workgroup per chunk with the chunk's transpose in
-// LDS.  Applicable when chunk_local_supported(n, chunk_size); chunks with more
-// than kLocalKeyCap nonzeros are appended to d_overflow (count in
-// *d_overflow_count, which the caller zeroes) and their rows left unwritten.
-constexpr int kLocalKeyCap = 32768;
+// LDS.  Applicable when chunk_local_supported(n, chunk_size).  d_lists holds
+// 2*num_chunks int32 and d_counts 2 int32 (zeroed by the caller).  Chunks too
+// large for LDS are left unwritten and listed in *d_overflow[0 ..
+// **d_overflow_count) for the global-CSC kernel.
 constexpr int kLocalRowCap = 4096;
 bool chunk_local_supported(int32_t n, int32_t chunk_size);
 void chunk_local_sketch_top_k(Context &ctx, int32_t n, int32_t k, int32_t chunk_size,
                               int32_t m_capacity, const int32_t *d_ptr, const int32_t *d_ind,
-                              uint64_t *d_table, int32_t *d_overflow,
-                              int32_t *d_overflow_count);
+                              uint64_t *d_table, int32_t *d_lists, int32_t *d_counts,
+                              int32_t **d_overflow, int32_t **d_overflow_count);
 
 // Degree / weight totals of a top-k table (reference
 // sporder/src/common/similarity_top_k.cu:120-172).

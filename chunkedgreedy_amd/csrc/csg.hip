@@ -486,7 +486,7 @@ size_t table_ws_bytes(int32_t n, int32_t nnz, int32_t k, int32_t chunk_size,
                       bool is_symmetric) {
   size_t b = ws_bytes<uint64_t>(static_cast<size_t>(n) * k);
   int64_t chunks = ceil_div64(n, chunk_size);
-  b += ws_bytes<int32_t>(static_cast<size_t>(chunks)) + ws_bytes<int32_t>(2);
+  b += ws_bytes<int32_t>(2 * static_cast<size_t>(chunks)) + ws_bytes<int32_t>(2);
   if (!is_symmetric) {
     b += ws_bytes<int32_t>(static_cast<size_t>(n) + 1) +
          ws_bytes<int32_t>(static_cast<size_t>(nnz)) + csr2csc_ws_bytes(n, nnz);
@@ -501,8 +501,9 @@ void build_table(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
                  int32_t chunk_size, uint64_t *table, EventSpan *t_csc,
                  EventSpan *t_sim) {
   const int64_t chunks = ceil_div64(n, chunk_size);
-  int32_t *overflow = ctx.take<int32_t>(static_cast<size_t>(chunks));
-  int32_t *overflow_count = ctx.take<int32_t>(2);
+  int32_t *lists = ctx.take<int32_t>(2 * static_cast<size_t>(chunks));
+  int32_t *counts = ctx.take<int32_t>(2);
+  int32_t *overflow = nullptr, *overflow_count = nullptr;
   const bool local = chunk_local_supported(n, chunk_size);
 
   auto global_csc = [&](const int32_t **cp, const int32_t **ri) {
@@ -530,10 +531,10 @@ void build_table(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
     return;
   }
 
-  fill_u32(ctx, overflow_count, 2, 0u);
+  fill_u32(ctx, counts, 2, 0u);
   t_sim->begin(ctx.stream);
-  chunk_local_sketch_top_k(ctx, n, k, chunk_size, m_cap, d_ptr, d_ind, table, overflow,
-                           overflow_count);
+  chunk_local_sketch_top_k(ctx, n, k, chunk_size, m_cap, d_ptr, d_ind, table, lists, counts,
+                           &overflow, &overflow_count);
   if (is_symmetric) {
     // The CSR is its own transpose: run the fallback over the overflow list
     // without waiting for its length (an empty list exits at once).

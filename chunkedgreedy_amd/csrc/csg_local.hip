@@ -6,22 +6,29 @@
 // when they fall inside r's chunk (sporder/src/common/chunk_similarity_top_k.cu
 // :53-83).  Restricted to one chunk, those rows are exactly the chunk's own
 // rows holding c, so the global transpose (a device-wide sort of every
-// nonzero) and the random CSC walks can be replaced by a transpose of the
-// chunk's row block alone:
+// nonzero) and the random CSC walks are replaced by a transpose of the
+// chunk's row block alone, in LDS:
 //
-//   1. keys (c << lb) | local_row for the chunk's E nonzeros go to LDS;
-//   2. a bitonic sort in LDS orders them by (column, row);
+//   1. every nonzero (c, local row) becomes the key (c << lb) | local_row and is
+//      counting-sorted into NB buckets by a multiplicative hash of c (keys of
+//      one column share a bucket);
+//   2. each bucket is sorted by key: one thread per bucket (insertion sort)
+//      for small buckets, one wave per bucket (bitonic network in LDS) for
+//      large ones.  A column's keys are now one run, rows ascending;
 //   3. a row whose columns all occur once in the chunk has no candidates and
 //      gets the all-zero table row at once;
-//   4. other rows (one wave each) binary-search each column's run of keys in
-//      LDS and feed the run's rows, ascending, to the wave64 sketch.
+//   4. the other rows (one wave each) binary-search each column's run inside
+//      its bucket and feed the run's rows, ascending, to the wave64 sketch.
 //
 // The stream, and therefore the table, is identical to the reference's.
-// Chunks with more nonzeros than kLocalKeyCap are appended to an overflow list
-// for the global-CSC kernel.  Requires ceil(log2 n) + ceil(log2 C) <= 32 and
-// C <= kLocalRowCap (checked by the host).
+// Two LDS tiers: up to 16384 nonzeros and 2048 rows per chunk (~78 KiB, two
+// workgroups per CU) and up to 32768 nonzeros and 4096 rows (~156 KiB).
+// Larger chunks go to an overflow list for the global-CSC kernel.  Requires
+// ceil(log2 n) + ceil(log2 C) <= 32 (checked by the host).
 #include "common.hpp"
 #include "sketch.hpp"
+
+#include <algorithm>
 
 namespace sporder_hip {
 
@@ -29,26 +36,17 @@ namespace {
 
 constexpr int kLocalThreads = 1024;
 constexpr int kLocalWaves = kLocalThreads / kWave;
+// Buckets up to this size are sorted by one thread.
+constexpr int kSmallBucket = 48;
 
-// First index in [0, count) with keys[i] > bound (keys sorted ascending).
-__device__ __forceinline__ int32_t lds_upper_bound(const uint32_t *keys, int32_t count,
-                                                   uint32_t bound) {
-  int32_t lo = 0, hi = count;
-  while (lo < hi) {
-    int32_t mid = (lo + hi) >> 1;
-    if (keys[mid] <= bound) {
-      lo = mid + 1;
-    } else {
-      hi = mid;
-    }
-  }
-  return lo;
+__device__ __forceinline__ uint32_t bucket_of(uint32_t col, int nb_log2) {
+  // Fibonacci hashing (Knuth, TAOCP vol. 3, 6.4): high bits of col * 2^32/phi.
+  return (col * 0x9E3779B9u) >> (32 - nb_log2);
 }
 
-// First index in [0, count) with keys[i] >= bound.
-__device__ __forceinline__ int32_t lds_lower_bound(const uint32_t *keys, int32_t count,
-                                                   uint32_t bound) {
-  int32_t lo = 0, hi = count;
+// First index in [lo, hi) with keys[i] >= bound.
+__device__ __forceinline__ int32_t lds_lower_bound(const uint32_t *keys, int32_t lo,
+                                                   int32_t hi, uint32_t bound) {
   while (lo < hi) {
     int32_t mid = (lo + hi) >> 1;
     if (keys[mid] < bound) {
@@ -60,147 +58,257 @@ __device__ __forceinline__ int32_t lds_lower_bound(const uint32_t *keys, int32_t
   return lo;
 }
 
-template <int CELLS>
+// First index in [lo, hi) with keys[i] > bound.
+__device__ __forceinline__ int32_t lds_upper_bound(const uint32_t *keys, int32_t lo,
+                                                   int32_t hi, uint32_t bound) {
+  while (lo < hi) {
+    int32_t mid = (lo + hi) >> 1;
+    if (keys[mid] <= bound) {
+      lo = mid + 1;
+    } else {
+      hi = mid;
+    }
+  }
+  return lo;
+}
+
+__device__ __forceinline__ void wave_lds_fence() {
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+}
+
+// Ascending sort of a[0, size) in LDS by one wave: bitonic network in the
+// "mirror" form (first stage of each merge compares i with its mirror in the
+// block, later stages are half-cleaners), in which every exchange is
+// ascending, so positions >= size act as +infinity and are never touched.
+__device__ void wave_sort_lds(uint32_t *a, int32_t size) {
+  const int lane = lane_id();
+  int32_t p2 = 1;
+  while (p2 < size) p2 <<= 1;
+  for (int32_t kk = 2; kk <= p2; kk <<= 1) {
+    for (int32_t j = kk >> 1; j > 0; j >>= 1) {
+      for (int32_t t = lane; t < (p2 >> 1); t += kWave) {
+        const int32_t lo = ((t & ~(j - 1)) << 1) | (t & (j - 1));
+        // First stage of the level: partner is the mirror inside the block.
+        const int32_t hi = (j == (kk >> 1)) ? (lo | (kk - 1)) - (lo & (kk - 1)) : lo + j;
+        if (hi < size) {
+          const uint32_t x = a[lo], y = a[hi];
+          if (x > y) {
+            a[lo] = y;
+            a[hi] = x;
+          }
+        }
+      }
+      wave_lds_fence();
+    }
+  }
+}
+
+template <int CELLS, int KEYCAP, int ROWCAP, int NB_LOG2>
 __global__ void __launch_bounds__(kLocalThreads)
     chunk_local_sketch_kernel(int32_t n, int32_t k, int32_t chunk_size, int32_t lb,
                               const int32_t *__restrict__ row_ptr,
                               const int32_t *__restrict__ col_ind,
-                              uint64_t *__restrict__ table, int32_t *__restrict__ overflow,
+                              uint64_t *__restrict__ table,
+                              const int32_t *__restrict__ chunk_list,
+                              const int32_t *__restrict__ chunk_list_count,
+                              int32_t *__restrict__ overflow,
                               int32_t *__restrict__ overflow_count) {
-  __shared__ uint32_t s_keys[kLocalKeyCap];
-  __shared__ int32_t s_size[kLocalRowCap];
-  __shared__ uint8_t s_multi[kLocalRowCap];
+  constexpr int NB = 1 << NB_LOG2;
+  __shared__ uint32_t s_keys[KEYCAP];
+  __shared__ int32_t s_bend[NB];      // after the scatter: end of bucket b
+  __shared__ int32_t s_size[ROWCAP];
+  __shared__ uint8_t s_multi[ROWCAP];
 
   const int tid = threadIdx.x;
   const int lane = lane_id();
   const int wave = tid / kWave;
-  const int32_t chunk = blockIdx.x;
-  const int32_t cs = chunk * chunk_size;
-  const int32_t ce = (n - cs > chunk_size) ? cs + chunk_size : n;
-  const int32_t rows = ce - cs;
-  const int32_t e0 = row_ptr[cs];
-  const int32_t E = row_ptr[ce] - e0;
-  if (E > kLocalKeyCap) {
-    if (tid == 0) overflow[atomicAdd(overflow_count, 1)] = chunk;
-    return;
-  }
   const uint32_t rmask = (lb == 0) ? 0u : ((1u << lb) - 1u);
-  int32_t epad = 1;
-  while (epad < E) epad <<= 1;
+  const int64_t num_chunks = ceil_div64(n, chunk_size);
+  const int64_t work = chunk_list ? *chunk_list_count : num_chunks;
 
-  // Stage the chunk's column indices with coalesced loads, then let one
-  // thread per row turn its entries into (column << lb | local row) keys.
-  for (int32_t i = tid; i < E; i += kLocalThreads) {
-    s_keys[i] = static_cast<uint32_t>(col_ind[e0 + i]);
-  }
-  for (int32_t i = E + tid; i < epad; i += kLocalThreads) s_keys[i] = 0xFFFFFFFFu;
-  for (int32_t r = tid; r < rows; r += kLocalThreads) {
-    s_size[r] = row_ptr[cs + r + 1] - row_ptr[cs + r];
-    s_multi[r] = 0;
-  }
-  __syncthreads();
-  for (int32_t r = tid; r < rows; r += kLocalThreads) {
-    const int32_t off = row_ptr[cs + r] - e0;
-    const int32_t len = s_size[r];
-    for (int32_t q = 0; q < len; ++q) {
-      s_keys[off + q] = (s_keys[off + q] << lb) | static_cast<uint32_t>(r);
+  for (int64_t t = blockIdx.x; t < work; t += gridDim.x) {
+    const int32_t chunk = chunk_list ? chunk_list[t] : static_cast<int32_t>(t);
+    const int32_t cs = chunk * chunk_size;
+    const int32_t ce = (n - cs > chunk_size) ? cs + chunk_size : n;
+    const int32_t rows = ce - cs;
+    const int32_t e0 = row_ptr[cs];
+    const int32_t E = row_ptr[ce] - e0;
+    if (E > KEYCAP || rows > ROWCAP) {
+      if (tid == 0) overflow[atomicAdd(overflow_count, 1)] = chunk;
+      continue; // uniform across the workgroup
     }
-  }
-  __syncthreads();
 
-  // Bitonic sort of s_keys[0, epad).
-  for (int32_t kk = 2; kk <= epad; kk <<= 1) {
-    for (int32_t j = kk >> 1; j > 0; j >>= 1) {
-      for (int32_t i = tid; i < (epad >> 1); i += kLocalThreads) {
-        const int32_t lo = ((i & ~(j - 1)) << 1) | (i & (j - 1));
-        const int32_t hi = lo + j;
-        const uint32_t a = s_keys[lo], b = s_keys[hi];
-        const bool asc = (lo & kk) == 0;
-        if (asc ? (a > b) : (a < b)) {
-          s_keys[lo] = b;
-          s_keys[hi] = a;
+    // 1. Bucket counts (coalesced column reads) and row sizes.
+    for (int32_t b = tid; b < NB; b += kLocalThreads) s_bend[b] = 0;
+    for (int32_t r = tid; r < rows; r += kLocalThreads) {
+      s_size[r] = row_ptr[cs + r + 1] - row_ptr[cs + r];
+      s_multi[r] = 0;
+    }
+    __syncthreads();
+    for (int32_t i = tid; i < E; i += kLocalThreads) {
+      atomicAdd(&s_bend[bucket_of(static_cast<uint32_t>(col_ind[e0 + i]), NB_LOG2)], 1);
+    }
+    __syncthreads();
+    // Exclusive scan of the counts (wave 0): s_bend[b] = start of bucket b.
+    if (wave == 0) {
+      int32_t carry = 0;
+      for (int32_t base = 0; base < NB; base += kWave) {
+        const int32_t v = s_bend[base + lane];
+        const int32_t incl = wave_incl_scan(v);
+        s_bend[base + lane] = carry + incl - v;
+        carry += readlane(incl, kWave - 1);
+      }
+    }
+    __syncthreads();
+    // 2a. Scatter: one thread per row writes its keys; the bucket cursor
+    //     moves s_bend[b] from the start to the end of bucket b.
+    for (int32_t r = tid; r < rows; r += kLocalThreads) {
+      const int32_t rb = row_ptr[cs + r];
+      const int32_t len = s_size[r];
+#pragma unroll 4
+      for (int32_t q = 0; q < len; ++q) {
+        const uint32_t c = static_cast<uint32_t>(col_ind[rb + q]);
+        const int32_t slot = atomicAdd(&s_bend[bucket_of(c, NB_LOG2)], 1);
+        s_keys[slot] = (c << lb) | static_cast<uint32_t>(r);
+      }
+    }
+    __syncthreads();
+    // 2b. Sort each bucket: small ones by one thread (insertion sort) ...
+    for (int32_t b = tid; b < NB; b += kLocalThreads) {
+      const int32_t lo = b ? s_bend[b - 1] : 0, hi = s_bend[b];
+      if (hi - lo <= kSmallBucket) {
+        for (int32_t i = lo + 1; i < hi; ++i) {
+          const uint32_t x = s_keys[i];
+          int32_t j = i - 1;
+          while (j >= lo && s_keys[j] > x) {
+            s_keys[j + 1] = s_keys[j];
+            --j;
+          }
+          s_keys[j + 1] = x;
         }
       }
-      __syncthreads();
     }
-  }
-
-  // Rows holding a column that another chunk row also holds.
-  for (int32_t i = tid; i < E; i += kLocalThreads) {
-    const uint32_t key = s_keys[i];
-    const uint32_t c = key >> lb;
-    const bool multi = (i > 0 && (s_keys[i - 1] >> lb) == c) ||
-                       (i + 1 < E && (s_keys[i + 1] >> lb) == c);
-    if (multi) s_multi[key & rmask] = 1;
-  }
-  __syncthreads();
-
-  WaveSketch<CELLS> store;
-  for (int32_t r = wave; r < rows; r += kLocalWaves) {
-    const int32_t row = cs + r;
-    uint64_t *out = table + static_cast<size_t>(row) * k;
-    const int32_t row_size = s_size[r];
-    if (row_size == 0 || s_multi[r] == 0) {
-      for (int32_t j = lane; j < k; j += kWave) out[j] = 0;
-      continue;
+    // ... large ones by one wave each.
+    for (int32_t b = wave; b < NB; b += kLocalWaves) {
+      const int32_t lo = b ? s_bend[b - 1] : 0, hi = s_bend[b];
+      if (hi - lo > kSmallBucket) wave_sort_lds(s_keys + lo, hi - lo);
     }
-    store.clear();
-    const int32_t rb = row_ptr[row], re = rb + row_size;
-    for (int32_t pb = rb; pb < re; pb += kWave) {
-      const int32_t p = pb + lane;
-      int32_t a = 0, b = 0;
-      if (p < re) {
-        const uint32_t base = static_cast<uint32_t>(col_ind[p]) << lb;
-        a = lds_lower_bound(s_keys, E, base);
-        b = lds_upper_bound(s_keys, E, base | rmask);
+    __syncthreads();
+
+    // 3. Rows holding a column that another chunk row also holds (equal
+    //    columns are adjacent now).
+    for (int32_t i = tid; i < E; i += kLocalThreads) {
+      const uint32_t key = s_keys[i];
+      const uint32_t c = key >> lb;
+      const bool multi = (i > 0 && (s_keys[i - 1] >> lb) == c) ||
+                         (i + 1 < E && (s_keys[i + 1] >> lb) == c);
+      if (multi) s_multi[key & rmask] = 1;
+    }
+    __syncthreads();
+
+    // 4. Sketch, one wave per row.
+    WaveSketch<CELLS> store;
+    for (int32_t r = wave; r < rows; r += kLocalWaves) {
+      const int32_t row = cs + r;
+      uint64_t *out = table + static_cast<size_t>(row) * k;
+      const int32_t row_size = s_size[r];
+      if (row_size == 0 || s_multi[r] == 0) {
+        for (int32_t j = lane; j < k; j += kWave) out[j] = 0;
+        continue;
       }
-      const int32_t len = b - a;
-      const int32_t incl = wave_incl_scan(len);
-      const int32_t excl = incl - len;
-      const int32_t total = readlane(incl, kWave - 1);
-      for (int32_t f0 = 0; f0 < total; f0 += kWave) {
-        const int32_t f = f0 + lane;
-        int32_t j = 0;
+      store.clear();
+      const int32_t rb = row_ptr[row], re = rb + row_size;
+      for (int32_t pb = rb; pb < re; pb += kWave) {
+        const int32_t p = pb + lane;
+        int32_t a = 0, bnd = 0;
+        if (p < re) {
+          const uint32_t c = static_cast<uint32_t>(col_ind[p]);
+          const uint32_t bk = bucket_of(c, NB_LOG2);
+          const int32_t blo = bk ? s_bend[bk - 1] : 0, bhi = s_bend[bk];
+          const uint32_t base = c << lb;
+          a = lds_lower_bound(s_keys, blo, bhi, base);
+          bnd = lds_upper_bound(s_keys, a, bhi, base | rmask);
+        }
+        const int32_t len = bnd - a;
+        const int32_t incl = wave_incl_scan(len);
+        const int32_t excl = incl - len;
+        const int32_t total = readlane(incl, kWave - 1);
+        for (int32_t f0 = 0; f0 < total; f0 += kWave) {
+          const int32_t f = f0 + lane;
+          int32_t j = 0;
 #pragma unroll
-        for (int step = 32; step > 0; step >>= 1) {
-          const int32_t t = j + step;
-          const int32_t e = __shfl(excl, t & (kWave - 1), kWave);
-          if (t < kWave && e <= f) j = t;
-        }
-        const int32_t seg_a = __shfl(a, j, kWave);
-        const int32_t seg_x = __shfl(excl, j, kWave);
-        bool item = false;
-        int32_t other = -1;
-        float alpha = 0.0f;
-        if (f < total) {
-          const int32_t ol = static_cast<int32_t>(s_keys[seg_a + (f - seg_x)] & rmask);
-          if (ol != r) {
-            other = cs + ol;
-            alpha = 2.0f / static_cast<float>(row_size + s_size[ol]);
-            item = true;
+          for (int step = 32; step > 0; step >>= 1) {
+            const int32_t tt = j + step;
+            const int32_t e = __shfl(excl, tt & (kWave - 1), kWave);
+            if (tt < kWave && e <= f) j = tt;
+          }
+          const int32_t seg_a = __shfl(a, j, kWave);
+          const int32_t seg_x = __shfl(excl, j, kWave);
+          bool item = false;
+          int32_t other = -1;
+          float alpha = 0.0f;
+          if (f < total) {
+            const int32_t ol = static_cast<int32_t>(s_keys[seg_a + (f - seg_x)] & rmask);
+            if (ol != r) {
+              other = cs + ol;
+              alpha = 2.0f / static_cast<float>(row_size + s_size[ol]);
+              item = true;
+            }
+          }
+          uint64_t mask = ballot(item);
+          while (mask) {
+            const int i = __builtin_ctzll(mask);
+            store.add(readlane(other, i), readlane_f(alpha, i));
+            mask &= mask - 1;
           }
         }
-        uint64_t mask = ballot(item);
-        while (mask) {
-          const int i = __builtin_ctzll(mask);
-          store.add(readlane(other, i), readlane_f(alpha, i));
-          mask &= mask - 1;
-        }
       }
+      store.select_top_k(k, out);
     }
-    store.select_top_k(k, out);
+    __syncthreads(); // LDS is reused by the next chunk of this workgroup
   }
+}
+
+// Tier parameters: (key capacity, row capacity, log2 buckets).
+constexpr int kT1Keys = 16384, kT1Rows = 2048, kT1Nb = 10;
+constexpr int kT2Keys = 32768, kT2Rows = 4096, kT2Nb = 11;
+
+template <int CELLS, int KEYCAP, int ROWCAP, int NB_LOG2>
+void launch_tier(Context &ctx, int32_t n, int32_t k, int32_t chunk_size, int32_t lb,
+                 const int32_t *d_ptr, const int32_t *d_ind, uint64_t *d_table,
+                 const int32_t *list, const int32_t *list_count, int32_t *ovf,
+                 int32_t *ovf_count, int per_cu) {
+  const int64_t chunks = ceil_div64(n, chunk_size);
+  // A fixed grid striding over the work: no launch per chunk of an empty list.
+  int64_t grid = list ? std::min<int64_t>(chunks, static_cast<int64_t>(ctx.num_cus) * per_cu)
+                      : chunks;
+  chunk_local_sketch_kernel<CELLS, KEYCAP, ROWCAP, NB_LOG2>
+      <<<dim3(static_cast<unsigned>(grid)), kLocalThreads, 0, ctx.stream>>>(
+          n, k, chunk_size, lb, d_ptr, d_ind, d_table, list, list_count, ovf, ovf_count);
+  SP_LAUNCH_CHECK();
 }
 
 template <int CELLS>
 void launch_local(Context &ctx, int32_t n, int32_t k, int32_t chunk_size, int32_t lb,
                   const int32_t *d_ptr, const int32_t *d_ind, uint64_t *d_table,
-                  int32_t *d_overflow, int32_t *d_overflow_count) {
+                  int32_t *lists, int32_t *counts, int32_t **final_list,
+                  int32_t **final_count) {
   const int64_t chunks = ceil_div64(n, chunk_size);
-  chunk_local_sketch_kernel<CELLS><<<dim3(static_cast<unsigned>(chunks)), kLocalThreads, 0,
-                                     ctx.stream>>>(n, k, chunk_size, lb, d_ptr, d_ind, d_table,
-                                                   d_overflow, d_overflow_count);
-  SP_LAUNCH_CHECK();
+  int32_t *list_a = lists, *list_b = lists + chunks;
+  if (chunk_size <= kT1Rows) {
+    launch_tier<CELLS, kT1Keys, kT1Rows, kT1Nb>(ctx, n, k, chunk_size, lb, d_ptr, d_ind,
+                                                d_table, nullptr, nullptr, list_a, counts, 2);
+    launch_tier<CELLS, kT2Keys, kT2Rows, kT2Nb>(ctx, n, k, chunk_size, lb, d_ptr, d_ind,
+                                                d_table, list_a, counts, list_b, counts + 1,
+                                                1);
+  } else {
+    launch_tier<CELLS, kT2Keys, kT2Rows, kT2Nb>(ctx, n, k, chunk_size, lb, d_ptr, d_ind,
+                                                d_table, nullptr, nullptr, list_b, counts + 1,
+                                                1);
+  }
+  *final_list = list_b;
+  *final_count = counts + 1;
 }
 
 } // namespace
@@ -211,16 +319,16 @@ bool chunk_local_supported(int32_t n, int32_t chunk_size) {
 
 void chunk_local_sketch_top_k(Context &ctx, int32_t n, int32_t k, int32_t chunk_size,
                               int32_t m_capacity, const int32_t *d_ptr, const int32_t *d_ind,
-                              uint64_t *d_table, int32_t *d_overflow,
-                              int32_t *d_overflow_count) {
+                              uint64_t *d_table, int32_t *d_lists, int32_t *d_counts,
+                              int32_t **d_overflow, int32_t **d_overflow_count) {
   SP_EXPECT(k <= 256, "k must be <= 256");
   SP_EXPECT(chunk_local_supported(n, chunk_size), "chunk-local sketch not applicable");
   const int32_t lb = bits_for(chunk_size - 1);
   switch (m_capacity / 32) {
 #define SP_CASE(C)                                                                       \
   case C:                                                                                \
-    launch_local<C>(ctx, n, k, chunk_size, lb, d_ptr, d_ind, d_table, d_overflow,        \
-                    d_overflow_count);                                                   \
+    launch_local<C>(ctx, n, k, chunk_size, lb, d_ptr, d_ind, d_table, d_lists, d_counts, \
+                    d_overflow, d_overflow_count);                                       \
     break;
     SP_CASE(1) SP_CASE(2) SP_CASE(3) SP_CASE(4) SP_CASE(5) SP_CASE(6)
     SP_CASE(7) SP_CASE(8) SP_CASE(9) SP_CASE(10) SP_CASE(11) SP_CASE(12)
