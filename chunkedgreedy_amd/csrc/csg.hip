@@ -399,7 +399,38 @@ __global__ void __launch_bounds__(kGreedyBlock)
       cur = best_c;
       continue;
     }
-    int32_t nxt = next_unvisited(s_bm, words, tail_mask, &low_word);
+    // Restart.  The chain now visits the lowest unvisited row; a row with no
+    // table entries at all restarts again at once, so the free rows of one
+    // bitmap word below the first row that has entries are exactly the next
+    // restarts, in index order: emit them in one step.
+    int32_t nxt = -1;
+    while (true) {
+      nxt = next_unvisited(s_bm, words, tail_mask, &low_word);
+      if (nxt < 0) break;
+      const int32_t w = nxt >> 5;
+      const uint32_t free_bits =
+          ~s_bm[w] & (w == words - 1 ? tail_mask : 0xFFFFFFFFu);
+      const int32_t r = w * 32 + (lane & 31);
+      const bool free_here = lane < 32 && ((free_bits >> (lane & 31)) & 1u);
+      const bool has_entries = free_here && s_off[r + 1] > s_off[r];
+      const uint32_t with_entries = static_cast<uint32_t>(ballot(has_entries));
+      const uint32_t emit = with_entries
+                                ? free_bits & ((with_entries & (0u - with_entries)) - 1u)
+                                : free_bits;
+      if (emit) {
+        if (lane < 32 && ((emit >> lane) & 1u)) {
+          order[pos + __popc(emit & ((1u << lane) - 1u))] = start + r;
+        }
+        s_bm[w] |= emit; // every lane writes the same value
+        const int32_t m = __popc(emit);
+        pos += m;
+        restarts += m;
+      }
+      if (with_entries) {
+        nxt = w * 32 + __builtin_ctz(with_entries);
+        break;
+      }
+    }
     if (nxt < 0) break;
     restarts += 1;
     cur = nxt;

@@ -43,36 +43,79 @@ __global__ void invert_perm(int32_t n, const int32_t *__restrict__ src,
   }
 }
 
-// One wave per new row: copy the source row's columns (optionally mapped by
-// col_map) and values.  With val_new set and val_old NULL the values written
-// are 0.0f, as in the reference's gather_rows (reorder.cu:37-45).
-__global__ void gather_rows(int32_t n, const int32_t *__restrict__ ptr_old,
-                            const int32_t *__restrict__ ind_old,
-                            const float *__restrict__ val_old,
-                            const int32_t *__restrict__ new2old,
-                            const int32_t *__restrict__ col_map,
-                            const int32_t *__restrict__ ptr_new,
-                            int32_t *__restrict__ ind_new,
-                            float *__restrict__ val_new) {
+// G lanes per new row (64/G rows per wave).  Copies old row new2old[p] to row
+// p, mapping columns through col_map when given.  With col_map (SYMMETRIC) a
+// row of at most G entries is also sorted in registers (bitonic network over
+// the group's lanes) and written in final order; a longer row is written
+// unsorted to key_tmp/val_tmp and appended to `long_rows`.  Without col_map
+// (ROWS) rows are copied verbatim at any length.  With val_new set and
+// val_old NULL the values written are 0.0f, as in the reference's gather_rows
+// (reorder.cu:37-45).
+template <int G>
+__global__ void __launch_bounds__(256)
+    permute_rows(int32_t n, const int32_t *__restrict__ ptr_old,
+                 const int32_t *__restrict__ ind_old, const float *__restrict__ val_old,
+                 const int32_t *__restrict__ new2old, const int32_t *__restrict__ col_map,
+                 const int32_t *__restrict__ ptr_new, int32_t *__restrict__ ind_new,
+                 float *__restrict__ val_new, int32_t *__restrict__ key_tmp,
+                 float *__restrict__ val_tmp, int32_t *__restrict__ long_rows,
+                 int32_t *__restrict__ long_count) {
+  constexpr int kRowsPerWave = kWave / G;
   const int lane = lane_id();
+  const int gl = lane % G;
   const int64_t wave0 = (blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x) / kWave;
   const int64_t nwaves = static_cast<int64_t>(gridDim.x) * blockDim.x / kWave;
-  for (int64_t p = wave0; p < n; p += nwaves) {
-    int32_t o = new2old[p];
-    int32_t src = ptr_old[o], src_end = ptr_old[o + 1];
-    int32_t dst = ptr_new[p];
-    for (int32_t q = src + lane; q < src_end; q += kWave) {
-      int32_t c = ind_old[q];
-      int32_t off = dst + (q - src);
-      ind_new[off] = col_map ? col_map[c] : c;
-      if (val_new) val_new[off] = val_old ? val_old[q] : 0.0f;
+  for (int64_t pb = wave0 * kRowsPerWave; pb < n; pb += nwaves * kRowsPerWave) {
+    const int64_t p = pb + lane / G;
+    const bool row_ok = p < n;
+    int32_t src = 0, len = 0, dst = 0;
+    if (row_ok) {
+      const int32_t o = new2old[p];
+      src = ptr_old[o];
+      len = ptr_old[o + 1] - src;
+      dst = ptr_new[p];
+    }
+    const bool sort_here = col_map != nullptr && len <= G;
+    if (sort_here) {
+      const bool in = gl < len;
+      int32_t key = in ? col_map[ind_old[src + gl]] : 0x7fffffff;
+      float v = (in && val_old) ? val_old[src + gl] : 0.0f;
+#pragma unroll
+      for (int kk = 2; kk <= G; kk <<= 1) {
+#pragma unroll
+        for (int j = kk >> 1; j > 0; j >>= 1) {
+          const int32_t ok = __shfl_xor(key, j, G);
+          const float ov = __shfl_xor(v, j, G);
+          const bool ascending = (gl & kk) == 0;
+          const bool lower = (gl & j) == 0;
+          if ((ascending == lower) ? (ok < key) : (ok > key)) {
+            key = ok;
+            v = ov;
+          }
+        }
+      }
+      if (in) {
+        ind_new[dst + gl] = key;
+        if (val_new) val_new[dst + gl] = v;
+      }
+    } else if (row_ok) {
+      int32_t *ki = col_map ? key_tmp : ind_new;
+      float *vo = col_map ? val_tmp : val_new;
+      for (int32_t q = gl; q < len; q += G) {
+        const int32_t c = ind_old[src + q];
+        ki[dst + q] = col_map ? col_map[c] : c;
+        if (vo) vo[dst + q] = val_old ? val_old[src + q] : 0.0f;
+      }
+      if (col_map && gl == 0) long_rows[atomicAdd(long_count, 1)] = static_cast<int32_t>(p);
     }
   }
 }
 
-// Rows of up to 64 entries: bitonic network across the lanes of one wave.
-// Longer rows are appended to `long_rows` for the next stages.
-__global__ void sort_rows_wave(int32_t n, const int32_t *__restrict__ ptr,
+// Listed rows of up to 64 entries: bitonic network across the lanes of one
+// wave.  Longer rows are appended to `long_rows` for the next stage.
+__global__ void sort_rows_wave(const int32_t *__restrict__ rows,
+                               const int32_t *__restrict__ row_count,
+                               const int32_t *__restrict__ ptr,
                                const int32_t *__restrict__ key_in,
                                const float *__restrict__ val_in,
                                int32_t *__restrict__ key_out,
@@ -82,7 +125,9 @@ __global__ void sort_rows_wave(int32_t n, const int32_t *__restrict__ ptr,
   const int lane = lane_id();
   const int64_t wave0 = (blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x) / kWave;
   const int64_t nwaves = static_cast<int64_t>(gridDim.x) * blockDim.x / kWave;
-  for (int64_t r = wave0; r < n; r += nwaves) {
+  const int64_t count = *row_count;
+  for (int64_t t = wave0; t < count; t += nwaves) {
+    const int32_t r = rows[t];
     int32_t s = ptr[r], e = ptr[r + 1], len = e - s;
     if (len > kWave) {
       if (lane == 0) long_rows[atomicAdd(long_count, 1)] = static_cast<int32_t>(r);
@@ -169,6 +214,38 @@ __global__ void __launch_bounds__(kBlockSortThreads)
   }
 }
 
+template <int G>
+void launch_permute_g(Context &ctx, int32_t n, const int32_t *ptr_old, const int32_t *ind_old,
+                      const float *val_old, const int32_t *new2old, const int32_t *col_map,
+                      const int32_t *ptr_new, int32_t *ind_new, float *val_new,
+                      int32_t *key_tmp, float *val_tmp, int32_t *long_rows,
+                      int32_t *long_count) {
+  constexpr int rows_per_block = 4 * (kWave / G);
+  const int g = ctx.grid_for(ceil_div64(n, rows_per_block), 256, 4);
+  permute_rows<G><<<g, 256, 0, ctx.stream>>>(n, ptr_old, ind_old, val_old, new2old, col_map,
+                                            ptr_new, ind_new, val_new, key_tmp, val_tmp,
+                                            long_rows, long_count);
+  SP_LAUNCH_CHECK();
+}
+
+void launch_permute(Context &ctx, int G, int32_t n, const int32_t *ptr_old,
+                    const int32_t *ind_old, const float *val_old, const int32_t *new2old,
+                    const int32_t *col_map, const int32_t *ptr_new, int32_t *ind_new,
+                    float *val_new, int32_t *key_tmp, float *val_tmp, int32_t *long_rows,
+                    int32_t *long_count) {
+  switch (G) {
+#define SP_CASE(V)                                                                       \
+  case V:                                                                                \
+    launch_permute_g<V>(ctx, n, ptr_old, ind_old, val_old, new2old, col_map, ptr_new,    \
+                        ind_new, val_new, key_tmp, val_tmp, long_rows, long_count);      \
+    break;
+    SP_CASE(4) SP_CASE(8) SP_CASE(16) SP_CASE(32) SP_CASE(64)
+#undef SP_CASE
+  default:
+    SP_EXPECT(false, "internal: bad group width");
+  }
+}
+
 } // namespace
 
 } // namespace sporder_hip
@@ -191,7 +268,7 @@ extern "C" void sporder_reorder(sporder_context_t h, int32_t n, int32_t nnz,
   size_t need = ws_bytes<int32_t>(scan_tmp_elems(static_cast<int64_t>(n) + 1));
   if (symmetric) {
     need += ws_bytes<int32_t>(n) + ws_bytes<int32_t>(nnz) + ws_bytes<float>(nnz) +
-            2 * ws_bytes<int32_t>(static_cast<size_t>(n) + 2) + ws_bytes<int32_t>(2);
+            3 * ws_bytes<int32_t>(static_cast<size_t>(n) + 2) + ws_bytes<int32_t>(3);
   }
   ctx.reserve(need);
   int32_t *scan_tmp = ctx.take<int32_t>(scan_tmp_elems(static_cast<int64_t>(n) + 1));
@@ -204,11 +281,14 @@ extern "C" void sporder_reorder(sporder_context_t h, int32_t n, int32_t nnz,
   SP_LAUNCH_CHECK();
   scan_i32(ctx, d_ptr_new, d_ptr_new, static_cast<int64_t>(n) + 1, true, scan_tmp);
 
+  // Lanes per row: the average row length rounded up to a power of two,
+  // between 4 and 64.
+  int G = 4;
+  while (G < 64 && static_cast<int64_t>(G) * n < nnz) G <<= 1;
+
   if (!symmetric) {
-    gather_rows<<<wave_grid, 256, 0, ctx.stream>>>(n, d_ptr_old, d_ind_old, d_val_old,
-                                                   d_new_order, nullptr, d_ptr_new,
-                                                   d_ind_new, d_val_new);
-    SP_LAUNCH_CHECK();
+    launch_permute(ctx, G, n, d_ptr_old, d_ind_old, d_val_old, d_new_order, nullptr,
+                   d_ptr_new, d_ind_new, d_val_new, nullptr, nullptr, nullptr, nullptr);
     ctx.sync();
     return;
   }
@@ -216,28 +296,30 @@ extern "C" void sporder_reorder(sporder_context_t h, int32_t n, int32_t nnz,
   int32_t *old2new = ctx.take<int32_t>(n);
   int32_t *unsorted = ctx.take<int32_t>(nnz);
   float *val_unsorted = ctx.take<float>(nnz);
+  int32_t *list1 = ctx.take<int32_t>(static_cast<size_t>(n) + 2);
   int32_t *long_rows = ctx.take<int32_t>(static_cast<size_t>(n) + 2);
   int32_t *huge_rows = ctx.take<int32_t>(static_cast<size_t>(n) + 2);
-  int32_t *counts = ctx.take<int32_t>(2);
+  int32_t *counts = ctx.take<int32_t>(3);
 
   invert_perm<<<row_grid, 256, 0, ctx.stream>>>(n, d_new_order, old2new);
   SP_LAUNCH_CHECK();
-  gather_rows<<<wave_grid, 256, 0, ctx.stream>>>(
-      n, d_ptr_old, d_ind_old, d_val_old, d_new_order, old2new, d_ptr_new, unsorted,
-      with_vals ? val_unsorted : nullptr);
-  SP_LAUNCH_CHECK();
-  fill_u32(ctx, counts, 2, 0u);
+  fill_u32(ctx, counts, 3, 0u);
+  // Rows of at most G entries are remapped, sorted and written in one pass;
+  // longer rows go to list1 (unsorted in the temporaries).
+  launch_permute(ctx, G, n, d_ptr_old, d_ind_old, d_val_old, d_new_order, old2new,
+                 d_ptr_new, d_ind_new, with_vals ? d_val_new : nullptr, unsorted,
+                 with_vals ? val_unsorted : nullptr, list1, counts);
   sort_rows_wave<<<wave_grid, 256, 0, ctx.stream>>>(
-      n, d_ptr_new, unsorted, with_vals ? val_unsorted : nullptr, d_ind_new,
-      with_vals ? d_val_new : nullptr, long_rows, counts);
+      list1, counts, d_ptr_new, unsorted, with_vals ? val_unsorted : nullptr, d_ind_new,
+      with_vals ? d_val_new : nullptr, long_rows, counts + 1);
   SP_LAUNCH_CHECK();
   sort_rows_block<<<ctx.num_cus * 4, kBlockSortThreads, 0, ctx.stream>>>(
-      d_ptr_new, long_rows, counts, unsorted, with_vals ? val_unsorted : nullptr,
-      d_ind_new, with_vals ? d_val_new : nullptr, huge_rows, counts + 1);
+      d_ptr_new, long_rows, counts + 1, unsorted, with_vals ? val_unsorted : nullptr,
+      d_ind_new, with_vals ? d_val_new : nullptr, huge_rows, counts + 2);
   SP_LAUNCH_CHECK();
 
   int32_t hcount = 0;
-  SP_HIP(hipMemcpyAsync(&hcount, counts + 1, sizeof(int32_t), hipMemcpyDeviceToHost,
+  SP_HIP(hipMemcpyAsync(&hcount, counts + 2, sizeof(int32_t), hipMemcpyDeviceToHost,
                         ctx.stream));
   ctx.sync();
   if (hcount > 0) {
