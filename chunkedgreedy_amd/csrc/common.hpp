@@ -199,21 +199,71 @@ __device__ __forceinline__ float readlane_f(float v, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
 
-// Inclusive prefix sum across the 64 lanes of a wave.
+// ---- wave64 reductions and scans on DPP --------------------------------------
+//
+// GFX9 data-parallel primitives move values between lanes inside the VALU
+// (a few cycles), where __shfl* goes through ds_bpermute (LDS latency).
+// Controls: quad_perm 0xB1 = [1,0,3,2], 0x4E = [2,3,0,1]; 0x141 row_half_mirror;
+// 0x140 row_mirror; 0x111.. row_shr:n (0x110 + n); 0x142 row_bcast:15 (lane 15
+// of each row to the next row, rows selected by row_mask 0xa); 0x143
+// row_bcast:31 (lane 31 to rows 2 and 3, row_mask 0xc).  Lanes that a control
+// does not write, or whose source lane is outside the row, receive `ident`.
+template <int CTRL, int ROWS = 0xf>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v, uint32_t ident) {
+  return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(
+      static_cast<int>(ident), static_cast<int>(v), CTRL, ROWS, 0xf, false));
+}
+
+// Minimum / maximum over the wave, returned wave-uniform.
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+  constexpr uint32_t I = 0xFFFFFFFFu;
+  v = min(v, dpp_u32<0xB1>(v, I));
+  v = min(v, dpp_u32<0x4E>(v, I));
+  v = min(v, dpp_u32<0x141>(v, I));
+  v = min(v, dpp_u32<0x140>(v, I));
+  v = min(v, dpp_u32<0x142, 0xa>(v, I));
+  v = min(v, dpp_u32<0x143, 0xc>(v, I));
+  return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 63));
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, dpp_u32<0xB1>(v, 0u));
+  v = max(v, dpp_u32<0x4E>(v, 0u));
+  v = max(v, dpp_u32<0x141>(v, 0u));
+  v = max(v, dpp_u32<0x140>(v, 0u));
+  v = max(v, dpp_u32<0x142, 0xa>(v, 0u));
+  v = max(v, dpp_u32<0x143, 0xc>(v, 0u));
+  return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 63));
+}
+
+// Inclusive prefix sum across the 64 lanes: Kogge-Stone inside each row of 16
+// (row_shr 1, 2, 4, 8), then the row totals carried by the two broadcasts.
 __device__ __forceinline__ int32_t wave_incl_scan(int32_t v) {
-  int l = lane_id();
-#pragma unroll
-  for (int off = 1; off < kWave; off <<= 1) {
-    int32_t o = __shfl_up(v, off, kWave);
-    if (l >= off) v += o;
-  }
-  return v;
+  uint32_t u = static_cast<uint32_t>(v);
+  u += dpp_u32<0x111>(u, 0u);
+  u += dpp_u32<0x112>(u, 0u);
+  u += dpp_u32<0x114>(u, 0u);
+  u += dpp_u32<0x118>(u, 0u);
+  u += dpp_u32<0x142, 0xa>(u, 0u);
+  u += dpp_u32<0x143, 0xc>(u, 0u);
+  return static_cast<int32_t>(u);
+}
+
+// Inclusive prefix maximum across the 64 lanes (same network as the sum).
+__device__ __forceinline__ int32_t wave_incl_max(int32_t v) {
+  // Offset by 2^31 so that signed order becomes unsigned order with 0 as the
+  // identity.
+  uint32_t u = static_cast<uint32_t>(v) ^ 0x80000000u;
+  u = max(u, dpp_u32<0x111>(u, 0u));
+  u = max(u, dpp_u32<0x112>(u, 0u));
+  u = max(u, dpp_u32<0x114>(u, 0u));
+  u = max(u, dpp_u32<0x118>(u, 0u));
+  u = max(u, dpp_u32<0x142, 0xa>(u, 0u));
+  u = max(u, dpp_u32<0x143, 0xc>(u, 0u));
+  return static_cast<int32_t>(u ^ 0x80000000u);
 }
 
 __device__ __forceinline__ int32_t wave_sum(int32_t v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
-  return v;
+  return __builtin_amdgcn_readlane(wave_incl_scan(v), 63);
 }
 
 // weighted_index packing (reference sporder/src/common/weighted_index.h:15-27).

@@ -183,16 +183,21 @@ __device__ __forceinline__ int32_t next_unvisited(const uint32_t *bm, int32_t wo
 }
 
 // Best (max weight, ties -> smaller index) over the wave; all lanes get it.
+// A lane offers a candidate when *c >= 0; candidate weights are table weights,
+// which are positive, so their bit patterns order like the values.  With no
+// candidate anywhere the result is (-1.0f, -1).
 __device__ __forceinline__ void wave_argmax(float *w, int32_t *c) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    float ow = __shfl_xor(*w, off, kWave);
-    int32_t oc = __shfl_xor(*c, off, kWave);
-    if (ow > *w || (ow == *w && oc < *c)) {
-      *w = ow;
-      *c = oc;
-    }
+  const uint32_t wb = *c >= 0 ? __float_as_uint(*w) : 0u;
+  const uint32_t wmax = wave_max_u32(wb);
+  if (wmax == 0u) {
+    *w = -1.0f;
+    *c = -1;
+    return;
   }
+  const uint32_t cmin =
+      wave_min_u32((*c >= 0 && wb == wmax) ? static_cast<uint32_t>(*c) : 0xFFFFFFFFu);
+  *w = __uint_as_float(wmax);
+  *c = static_cast<int32_t>(cmin);
 }
 
 constexpr int kGreedyBlock = 256;

@@ -9,10 +9,11 @@
 // (L, c), so the arrangement is free:
 //   - a new key goes to the first empty slot in order s = L*CELLS + c (slots
 //     never empty again), a wave-uniform counter instead of find(-1) + ballot;
-//   - eviction takes the minimum of (weight, c*32 + L), reduced over the wave
-//     with a butterfly, and the new key inherits the evicted weight;
+//   - eviction takes the minimum of (weight, c*32 + L): a DPP minimum of the
+//     weight bits, then ballots in tie order; the new key inherits the evicted
+//     weight;
 //   - output merges the per-logical-lane selection-sorted lists, largest head
-//     weight first, ties to the smaller logical lane.
+//     weight first (DPP maximum), ties to the smaller logical lane.
 #pragma once
 
 #include "common.hpp"
@@ -40,6 +41,12 @@ template <int CELLS> struct WaveSketch {
   float wt[LC];
   int32_t filled; // wave-uniform: slots taken so far (fill order L*CELLS+c)
 
+  // Physical lane p holds cell c = 2j + (p >> 5); for odd CELLS the upper
+  // half of the last j is not a cell.
+  static __device__ __forceinline__ bool cell_valid(int j, int lane) {
+    return (CELLS % 2 == 0) || j < LC - 1 || lane < 32;
+  }
+
   __device__ __forceinline__ void clear() {
 #pragma unroll
     for (int j = 0; j < LC; ++j) {
@@ -51,7 +58,6 @@ template <int CELLS> struct WaveSketch {
 
   // Apply one item; k and w are wave-uniform.
   __device__ __forceinline__ void add(int32_t k, float w) {
-    const int lane = lane_id();
     bool hit = false;
 #pragma unroll
     for (int j = 0; j < LC; ++j) {
@@ -66,6 +72,7 @@ template <int CELLS> struct WaveSketch {
     if (filled < M) {
       // Slot s = L*CELLS + c: logical lane L, cell c -> physical lane
       // L + 32*(c & 1), local cell c >> 1.
+      const int lane = lane_id();
       int L = filled / CELLS, c = filled - L * CELLS;
       int owner = L + 32 * (c & 1), jj = c >> 1;
 #pragma unroll
@@ -78,32 +85,28 @@ template <int CELLS> struct WaveSketch {
       filled += 1;
       return;
     }
-    // Evict argmin over slots of (weight, c*32 + L).
-    const int L = lane & 31, h = lane >> 5;
-    float best_w = __builtin_inff();
-    int32_t best_k = 0x7fffffff;
+    // Evict the argmin of (weight, c*32 + L).  With c = 2j + (p >> 5) and
+    // L = p & 31, c*32 + L = 64j + p, so ties go to the smallest cell index j
+    // and then the lowest physical lane p.  Weights are positive floats (sums
+    // of 2/(a+b)), so their bit patterns order like the values.
+    const int lane = lane_id();
+    uint32_t lmin = 0xFFFFFFFFu;
 #pragma unroll
     for (int j = 0; j < LC; ++j) {
-      int c = 2 * j + h;
-      if (c < CELLS) {
-        int32_t ck = (c << 5) | L;
-        if (wt[j] < best_w || (wt[j] == best_w && ck < best_k)) {
-          best_w = wt[j];
-          best_k = ck;
-        }
-      }
+      if (cell_valid(j, lane)) lmin = min(lmin, __float_as_uint(wt[j]));
     }
+    const uint32_t wmin = wave_min_u32(lmin);
+    int jj = LC - 1;
+    uint64_t m = 0;
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-      float ow = __shfl_xor(best_w, off, kWave);
-      int32_t ok = __shfl_xor(best_k, off, kWave);
-      if (ow < best_w || (ow == best_w && ok < best_k)) {
-        best_w = ow;
-        best_k = ok;
+    for (int j = LC - 1; j >= 0; --j) {
+      const uint64_t mj = ballot(cell_valid(j, lane) && __float_as_uint(wt[j]) == wmin);
+      if (mj) {
+        m = mj;
+        jj = j;
       }
     }
-    int c = best_k >> 5;
-    int owner = (best_k & 31) + 32 * (c & 1), jj = c >> 1;
+    const int owner = __builtin_ctzll(m);
 #pragma unroll
     for (int j = 0; j < LC; ++j) {
       if (lane == owner && j == jj) {
@@ -167,18 +170,13 @@ template <int CELLS> struct WaveSketch {
     for (int32_t i = 0; i < k; ++i) {
       bool live = lane < 32 && fk[0] != -1;
       if (ballot(live) == 0) break;
-      float v = lane < 32 ? fw[0] : -__builtin_inff();
-      int32_t who = lane;
-#pragma unroll
-      for (int off = 32; off > 0; off >>= 1) {
-        float ov = __shfl_xor(v, off, kWave);
-        int32_t ow = __shfl_xor(who, off, kWave);
-        if (ov > v || (ov == v && ow < who)) {
-          v = ov;
-          who = ow;
-        }
-      }
-      int winner = __builtin_amdgcn_readfirstlane(who);
+      // Largest head weight, ties to the smaller lane.  Live heads are
+      // positive, exhausted lanes present 0.0f and the upper half-wave holds
+      // no logical lane, so bit patterns compare like the weights.
+      const uint32_t v = live ? __float_as_uint(fw[0]) : 0u;
+      const uint32_t vmax = wave_max_u32(v);
+      const int who = __builtin_ctzll(ballot(live && v == vmax));
+      const int winner = who;
       int32_t wk = readlane(fk[0], winner);
       float ww = readlane_f(fw[0], winner);
       int slot = i >> 6;
