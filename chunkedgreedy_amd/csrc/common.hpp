@@ -150,7 +150,8 @@ void csr2csc(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
 // Chunk-restricted sketch + top-k table (u64 weighted_index, n*k) from the
 // global CSC.  With d_chunks non-null only the rows of the chunks listed in
 // d_chunks[0 .. *d_chunk_count) are computed.
-void chunk_sketch_top_k(Context &ctx, int32_t n, int32_t k, int32_t chunk_size,
+size_t chunk_sketch_ws_bytes(int32_t n, int32_t nnz, int32_t chunk_size);
+void chunk_sketch_top_k(Context &ctx, int32_t n, int32_t nnz, int32_t k, int32_t chunk_size,
                         int32_t m_capacity, const int32_t *d_ptr,
                         const int32_t *d_ind, const int32_t *d_col_ptr,
                         const int32_t *d_row_ind, uint64_t *d_table,

@@ -1,4 +1,4 @@
-// csg.hip -- Chunked Greedy (sporder-csg): the global-CSC sketch kernel, the
+// csg.hip -- Chunked Greedy (sporder-csg): table construction, the
 // per-chunk greedy chain, table statistics, and the C-ABI entry points
 // sporder_chunk_similarity_greedy, sporder_similarity_graph and
 // sporder_chunk_similarity_top_k.
@@ -14,10 +14,10 @@
 //   - chunk-local (csg_local.hip): one workgroup per chunk, transpose in LDS,
 //     when chunk_size <= kLocalRowCap and the packed keys fit 32 bits; chunks
 //     with more nonzeros than LDS holds overflow to
-//   - global-CSC (this file): the reference's access pattern (transpose, or
-//     the CSR itself when is_symmetric), one wave per row.  The candidate
-//     stream is gathered 64 entries at a time from the concatenation of the
-//     row's column segments, so a row's column walks are issued together.
+//   - global-CSC (csg_overflow.hip): the reference's access pattern
+//     (transpose, or the CSR itself when is_symmetric); each nonzero's run of
+//     chunk rows in its column is found by a device-wide pass, then one wave
+//     per row streams the runs into the sketch.
 // Both produce the same table.
 //
 // Greedy: one wave per chunk.  For chunk_size <= kGreedyCompactRows the
@@ -33,117 +33,6 @@
 namespace sporder_hip {
 
 namespace {
-
-constexpr int kSketchBlock = 256;
-constexpr int kSketchWaves = kSketchBlock / kWave;
-// Column segments longer than this are trimmed to the chunk's row range by
-// binary search before gathering (they are sorted by row).  Only entries the
-// chunk filter rejects are skipped, so the stream is unchanged.
-constexpr int kTrimLen = 64;
-
-// One wave per row (grid-stride).  Rows of length 0 get an all-zero table row.
-// With `chunks` non-null, the waves cover only the rows of the listed chunks.
-template <int CELLS>
-__global__ void __launch_bounds__(kSketchBlock)
-    chunk_sketch_kernel(int32_t n, int32_t k, int32_t chunk_size,
-                        const int32_t *__restrict__ row_ptr,
-                        const int32_t *__restrict__ col_ind,
-                        const int32_t *__restrict__ col_ptr,
-                        const int32_t *__restrict__ row_ind,
-                        uint64_t *__restrict__ table,
-                        const int32_t *__restrict__ chunks,
-                        const int32_t *__restrict__ chunk_count) {
-  const int lane = lane_id();
-  const int64_t wave0 =
-      static_cast<int64_t>(blockIdx.x) * kSketchWaves + threadIdx.x / kWave;
-  const int64_t nwaves = static_cast<int64_t>(gridDim.x) * kSketchWaves;
-  const int64_t work = chunks ? static_cast<int64_t>(*chunk_count) * chunk_size : n;
-  WaveSketch<CELLS> store;
-
-  for (int64_t w = wave0; w < work; w += nwaves) {
-    int64_t row64 = w;
-    if (chunks) {
-      row64 = static_cast<int64_t>(chunks[w / chunk_size]) * chunk_size + (w % chunk_size);
-      if (row64 >= n) continue;
-    }
-    const int32_t row = static_cast<int32_t>(row64);
-    uint64_t *out = table + static_cast<size_t>(row) * k;
-    const int32_t rs = row_ptr[row], re = row_ptr[row + 1];
-    const int32_t row_size = re - rs;
-    if (row_size == 0) {
-      for (int32_t j = lane; j < k; j += kWave) out[j] = 0;
-      continue;
-    }
-    const int32_t cs = (row / chunk_size) * chunk_size;
-    int32_t ce = cs + chunk_size;
-    if (ce > n || ce < cs) ce = n;
-
-    store.clear();
-    for (int32_t pb = rs; pb < re; pb += kWave) {
-      const int32_t p = pb + lane;
-      int32_t a = 0, b = 0;
-      if (p < re) {
-        int32_t col = col_ind[p];
-        a = col_ptr[col];
-        b = col_ptr[col + 1];
-        if (b - a > kTrimLen) {
-          int32_t lo = lower_bound_dev(row_ind, a, b, cs);
-          int32_t hi = lower_bound_dev(row_ind, lo, b, ce);
-          a = lo;
-          b = hi;
-        }
-      }
-      const int32_t len = b - a;
-      const int32_t incl = wave_incl_scan(len);
-      const int32_t excl = incl - len;
-      const int32_t total = readlane(incl, kWave - 1);
-      for (int32_t f0 = 0; f0 < total; f0 += kWave) {
-        const int32_t f = f0 + lane;
-        // Largest segment j with excl[j] <= f (excl is non-decreasing).
-        int32_t j = 0;
-#pragma unroll
-        for (int step = 32; step > 0; step >>= 1) {
-          int32_t t = j + step;
-          int32_t e = __shfl(excl, t & (kWave - 1), kWave);
-          if (t < kWave && e <= f) j = t;
-        }
-        const int32_t seg_a = __shfl(a, j, kWave);
-        const int32_t seg_x = __shfl(excl, j, kWave);
-        bool item = false;
-        int32_t other = -1;
-        float alpha = 0.0f;
-        if (f < total) {
-          other = row_ind[seg_a + (f - seg_x)];
-          if (other >= cs && other < ce && other != row) {
-            int32_t sz = row_ptr[other + 1] - row_ptr[other];
-            alpha = 2.0f / static_cast<float>(row_size + sz);
-            item = true;
-          }
-        }
-        uint64_t mask = ballot(item);
-        while (mask) {
-          int i = __builtin_ctzll(mask);
-          store.add(readlane(other, i), readlane_f(alpha, i));
-          mask &= mask - 1;
-        }
-      }
-    }
-    store.select_top_k(k, out);
-  }
-}
-
-template <int CELLS>
-void launch_sketch(Context &ctx, int32_t n, int32_t k, int32_t chunk_size,
-                   const int32_t *d_ptr, const int32_t *d_ind,
-                   const int32_t *d_col_ptr, const int32_t *d_row_ind,
-                   uint64_t *d_table, const int32_t *d_chunks,
-                   const int32_t *d_chunk_count) {
-  int g = ctx.grid_for(ceil_div64(n, kSketchWaves), kSketchBlock, 4);
-  chunk_sketch_kernel<CELLS><<<g, kSketchBlock, 0, ctx.stream>>>(
-      n, k, chunk_size, d_ptr, d_ind, d_col_ptr, d_row_ind, d_table, d_chunks,
-      d_chunk_count);
-  SP_LAUNCH_CHECK();
-}
 
 // ---- greedy chain ----------------------------------------------------------
 
@@ -523,6 +412,7 @@ size_t table_ws_bytes(int32_t n, int32_t nnz, int32_t k, int32_t chunk_size,
   size_t b = ws_bytes<uint64_t>(static_cast<size_t>(n) * k);
   int64_t chunks = ceil_div64(n, chunk_size);
   b += ws_bytes<int32_t>(2 * static_cast<size_t>(chunks)) + ws_bytes<int32_t>(2);
+  b += chunk_sketch_ws_bytes(n, nnz, chunk_size);
   if (!is_symmetric) {
     b += ws_bytes<int32_t>(static_cast<size_t>(n) + 1) +
          ws_bytes<int32_t>(static_cast<size_t>(nnz)) + csr2csc_ws_bytes(n, nnz);
@@ -562,7 +452,7 @@ void build_table(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
     global_csc(&cp, &ri);
     t_csc->end(ctx.stream);
     t_sim->begin(ctx.stream);
-    chunk_sketch_top_k(ctx, n, k, chunk_size, m_cap, d_ptr, d_ind, cp, ri, table);
+    chunk_sketch_top_k(ctx, n, nnz, k, chunk_size, m_cap, d_ptr, d_ind, cp, ri, table);
     t_sim->end(ctx.stream);
     return;
   }
@@ -574,7 +464,7 @@ void build_table(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
   if (is_symmetric) {
     // The CSR is its own transpose: run the fallback over the overflow list
     // without waiting for its length (an empty list exits at once).
-    chunk_sketch_top_k(ctx, n, k, chunk_size, m_cap, d_ptr, d_ind, d_ptr, d_ind, table,
+    chunk_sketch_top_k(ctx, n, nnz, k, chunk_size, m_cap, d_ptr, d_ind, d_ptr, d_ind, table,
                        overflow, overflow_count);
     t_sim->end(ctx.stream);
     t_csc->begin(ctx.stream);
@@ -591,7 +481,7 @@ void build_table(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
     const int32_t *cp, *ri;
     global_csc(&cp, &ri);
     t_csc->end(ctx.stream);
-    chunk_sketch_top_k(ctx, n, k, chunk_size, m_cap, d_ptr, d_ind, cp, ri, table, overflow,
+    chunk_sketch_top_k(ctx, n, nnz, k, chunk_size, m_cap, d_ptr, d_ind, cp, ri, table, overflow,
                        overflow_count);
   } else {
     t_csc->end(ctx.stream);
@@ -599,27 +489,6 @@ void build_table(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
 }
 
 } // namespace
-
-void chunk_sketch_top_k(Context &ctx, int32_t n, int32_t k, int32_t chunk_size,
-                        int32_t m_capacity, const int32_t *d_ptr,
-                        const int32_t *d_ind, const int32_t *d_col_ptr,
-                        const int32_t *d_row_ind, uint64_t *d_table,
-                        const int32_t *d_chunks, const int32_t *d_chunk_count) {
-  SP_EXPECT(k <= 256, "k must be <= 256");
-  switch (m_capacity / 32) {
-#define SP_CASE(C)                                                             \
-  case C:                                                                      \
-    launch_sketch<C>(ctx, n, k, chunk_size, d_ptr, d_ind, d_col_ptr,           \
-                     d_row_ind, d_table, d_chunks, d_chunk_count);             \
-    break;
-    SP_CASE(1) SP_CASE(2) SP_CASE(3) SP_CASE(4) SP_CASE(5) SP_CASE(6)
-    SP_CASE(7) SP_CASE(8) SP_CASE(9) SP_CASE(10) SP_CASE(11) SP_CASE(12)
-    SP_CASE(13) SP_CASE(14) SP_CASE(15) SP_CASE(16)
-#undef SP_CASE
-  default:
-    SP_EXPECT(false, "sketch capacity must be a multiple of 32 in [32, 512]");
-  }
-}
 
 void top_k_stats(Context &ctx, int32_t n, int32_t k, const uint64_t *d_table,
                  TopKTotals *d_totals) {
