@@ -10,9 +10,17 @@
 // Row-split: a group of G lanes owns one row, each lane 4 adjacent columns
 // (float4), so a wave covers 64/G rows and one B row gather per nonzero is a
 // single coalesced G*16-byte access.  The row's (col, val) pairs are loaded
-// cooperatively by the group and broadcast by lane shuffles.  Every output
-// element is acc = fmaf(a_p, B[col_p][j], acc) over p in CSR order starting
-// at 0.0f, bit-identical to a sequential CPU loop.
+// cooperatively by the group and broadcast by lane shuffles, U B-rows in
+// flight per group.  Stated accumulation order (bit-identical to the CPU loop
+// of oracle_spmm_csr):
+//   - a row with at most kLongRow nonzeros: acc = fmaf(a_p, B[col_p][j], acc)
+//     over p in CSR order starting at 0.0f;
+//   - a longer row: split into segments of kSegLen nonzeros from the row's
+//     start; each segment is such a chain from 0.0f, and
+//     C[i][j] = ((P_0 + P_1) + P_2) + ... left to right.
+// The segments of long rows are processed by many row groups of a second
+// launch (so one hub row does not serialise the whole SpMM); the group that
+// finishes a row's last segment adds the partials in the stated order.
 //
 // Merge-path: the nonzeros are cut into equal spans per wave (a row longer
 // than a span is split); each span's partial row sums are added into C with
@@ -25,84 +33,197 @@ namespace sporder_hip {
 namespace {
 
 constexpr int kSpmmBlock = 256;
+constexpr int kSpmmWaves = kSpmmBlock / kWave;
+constexpr int kSpmmDepth = 8; // B rows in flight per row group
+constexpr int kLongRow = SPORDER_SPMM_LONG_ROW;
+constexpr int kSegLen = SPORDER_SPMM_SEGMENT;
 
+// Long rows: descriptors appended by the row-split launch.
+struct LongRow {
+  int32_t row;
+  int32_t base;  // first segment unit
+  int32_t nseg;
+  int32_t done;  // segments finished
+};
+struct LongCtl {
+  int32_t rows;     // long rows registered
+  int32_t segments; // segment units allocated
+};
+
+// A[s, e) x B on the group's float4 column slice col0 (col_ok false: lanes
+// past N).  Every lane of the wave calls it together; groups with different
+// ranges iterate until the longest is done.  Accumulates fmaf in CSR order
+// starting from 0.0f.
+template <int G>
+__device__ __forceinline__ float4 group_dot(int32_t s, int32_t e, const int32_t *__restrict__ ind,
+                                            const float *__restrict__ val, int32_t N,
+                                            int32_t col0, bool col_ok,
+                                            const float *__restrict__ B, int gl, int gbase) {
+  constexpr int U = kSpmmDepth;
+  float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  for (int32_t pb = s;; pb += G) {
+    const int32_t rem = e - pb;
+    if (ballot(rem > 0) == 0) break;
+    int32_t my_c = 0;
+    float my_v = 0.0f;
+    if (gl < rem) {
+      my_c = __builtin_nontemporal_load(ind + pb + gl);
+      my_v = __builtin_nontemporal_load(val + pb + gl);
+    }
+    const int32_t cnt = rem < G ? rem : G;
+    // Wave maximum of cnt bounds the broadcast loop.
+    const int32_t cmax = static_cast<int32_t>(
+        wave_max_u32(static_cast<uint32_t>(cnt > 0 ? cnt : 0)));
+    for (int32_t t = 0; t < cmax; t += U) {
+      int32_t c[U];
+      float v[U];
+      float4 b[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        c[u] = __shfl(my_c, gbase + ((t + u) & (G - 1)), kWave);
+        v[u] = __shfl(my_v, gbase + ((t + u) & (G - 1)), kWave);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (t + u < cnt && col_ok) {
+          b[u] = *reinterpret_cast<const float4 *>(B + static_cast<int64_t>(c[u]) * N + col0);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (t + u < cnt && col_ok) {
+          acc.x = fmaf(v[u], b[u].x, acc.x);
+          acc.y = fmaf(v[u], b[u].y, acc.y);
+          acc.z = fmaf(v[u], b[u].z, acc.z);
+          acc.w = fmaf(v[u], b[u].w, acc.w);
+        }
+      }
+    }
+  }
+  return acc;
+}
+
+__device__ __forceinline__ void store_nt(float *dst, float4 v) {
+  __builtin_nontemporal_store(v.x, dst + 0);
+  __builtin_nontemporal_store(v.y, dst + 1);
+  __builtin_nontemporal_store(v.z, dst + 2);
+  __builtin_nontemporal_store(v.w, dst + 3);
+}
+
+// One pass over the rows, 64/G rows per wave, one wave per row set (no grid
+// stride).  Rows longer than kLongRow are registered in `longs` for the
+// segment launch (when `longs` is null every row is done here, in one chain).
+// C is written with non-temporal stores: it is not read again by this launch
+// and would only evict B from the caches.
 template <int G>
 __global__ void __launch_bounds__(kSpmmBlock)
     spmm_rowsplit_v4(int32_t n, const int32_t *__restrict__ ptr,
                      const int32_t *__restrict__ ind,
                      const float *__restrict__ val, int32_t N,
-                     const float *__restrict__ B, float *__restrict__ C) {
+                     const float *__restrict__ B, float *__restrict__ C,
+                     LongCtl *ctl, LongRow *longs, int32_t *owner) {
   constexpr int kRowsPerWave = kWave / G;
   const int lane = lane_id();
   const int sub = lane / G;  // row slot within the wave
   const int gl = lane % G;   // lane within the row group
   const int gbase = sub * G; // first lane of the group
-  const int64_t wave0 =
-      (blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x) / kWave;
-  const int64_t nwaves = static_cast<int64_t>(gridDim.x) * blockDim.x / kWave;
+  const int64_t wave = static_cast<int64_t>(blockIdx.x) * kSpmmWaves + threadIdx.x / kWave;
+  const int64_t row = wave * kRowsPerWave + sub;
+  const bool row_ok = row < n;
+  int32_t s = row_ok ? ptr[row] : 0;
+  const int32_t e = row_ok ? ptr[row + 1] : 0;
+  const bool is_long = longs != nullptr && e - s > kLongRow;
+  if (is_long) {
+    if (gl == 0) {
+      const int32_t nseg = (e - s + kSegLen - 1) / kSegLen;
+      const int32_t id = atomicAdd(&ctl->rows, 1);
+      const int32_t base = atomicAdd(&ctl->segments, nseg);
+      longs[id] = LongRow{static_cast<int32_t>(row), base, nseg, 0};
+      for (int32_t q = 0; q < nseg; ++q) owner[base + q] = id;
+    }
+    s = e; // the segment launch computes this row
+  }
+  for (int32_t col0 = gl * 4; col0 - gl * 4 < N; col0 += G * 4) {
+    const bool col_ok = col0 < N;
+    const float4 acc = group_dot<G>(s, e, ind, val, N, col0, col_ok, B, gl, gbase);
+    if (row_ok && col_ok && !is_long) store_nt(C + row * N + col0, acc);
+  }
+}
 
-  for (int64_t rb = wave0 * kRowsPerWave; rb < n; rb += nwaves * kRowsPerWave) {
-    const int64_t row = rb + sub;
-    const bool row_ok = row < n;
-    const int32_t s = row_ok ? ptr[row] : 0;
-    const int32_t e = row_ok ? ptr[row + 1] : 0;
+// Segment units of the long rows: each row group computes one segment's
+// partial into `part` (unit-major, N floats per unit); the group that brings
+// a row's completion count to nseg adds the row's partials left to right into
+// C.  Grid-stride over the units registered by the row-split launch.
+template <int G>
+__global__ void __launch_bounds__(kSpmmBlock)
+    spmm_long_segments(const int32_t *__restrict__ ptr, const int32_t *__restrict__ ind,
+                       const float *__restrict__ val, int32_t N,
+                       const float *__restrict__ B, float *__restrict__ C,
+                       const LongCtl *__restrict__ ctl, LongRow *longs,
+                       const int32_t *__restrict__ owner, float *part) {
+  constexpr int kRowsPerWave = kWave / G;
+  const int lane = lane_id();
+  const int sub = lane / G, gl = lane % G, gbase = sub * G;
+  const int64_t wave0 = static_cast<int64_t>(blockIdx.x) * kSpmmWaves + threadIdx.x / kWave;
+  const int64_t nwaves = static_cast<int64_t>(gridDim.x) * kSpmmWaves;
+  const int32_t units = ctl->segments;
+  for (int64_t ub = wave0 * kRowsPerWave; ub < units; ub += nwaves * kRowsPerWave) {
+    const int64_t u = ub + sub;
+    const bool ok = u < units;
+    LongRow lr{0, 0, 1, 0};
+    int32_t s = 0, e = 0;
+    if (ok) {
+      lr = longs[owner[u]];
+      const int32_t rs = ptr[lr.row], re = ptr[lr.row + 1];
+      s = rs + static_cast<int32_t>(u - lr.base) * kSegLen;
+      e = s + kSegLen < re ? s + kSegLen : re;
+    }
     for (int32_t col0 = gl * 4; col0 - gl * 4 < N; col0 += G * 4) {
       const bool col_ok = col0 < N;
-      float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-      for (int32_t pb = s;; pb += G) {
-        // Wave-uniform loop: continue while any group has nonzeros left.
-        int32_t rem = e - pb;
-        if (ballot(rem > 0) == 0) break;
-        int32_t my_c = 0;
-        float my_v = 0.0f;
-        if (gl < rem) {
-          my_c = ind[pb + gl];
-          my_v = val[pb + gl];
-        }
-        int32_t cnt = rem < G ? rem : G;
-        // Wave max of cnt bounds the broadcast loop.
-        int32_t cmax = cnt;
+      const float4 acc = group_dot<G>(s, e, ind, val, N, col0, col_ok, B, gl, gbase);
+      if (ok && col_ok) *reinterpret_cast<float4 *>(part + u * N + col0) = acc;
+    }
+    // Publish the partial, then count it; the last segment of a row sums.
+    __threadfence();
+    int32_t prev = 0;
+    if (ok && gl == 0) prev = atomicAdd(&longs[owner[u]].done, 1);
+    prev = __shfl(prev, gbase, kWave);
+    const bool last = ok && prev == lr.nseg - 1;
+    if (last) {
+      __threadfence();
+      const float *p0 = part + static_cast<int64_t>(lr.base) * N;
+      for (int32_t col0 = gl * 4; col0 < N; col0 += G * 4) {
+        float4 sum = *reinterpret_cast<const float4 *>(p0 + col0);
+        int32_t q = 1;
+        for (; q + 4 <= lr.nseg; q += 4) {
+          float4 t[4];
 #pragma unroll
-        for (int off = 32; off > 0; off >>= 1) {
-          int32_t o = __shfl_xor(cmax, off, kWave);
-          cmax = o > cmax ? o : cmax;
-        }
-        for (int32_t t = 0; t < cmax; t += 4) {
-          int32_t c[4];
-          float v[4];
-          float4 b[4];
+          for (int i = 0; i < 4; ++i)
+            t[i] = *reinterpret_cast<const float4 *>(p0 + static_cast<int64_t>(q + i) * N + col0);
 #pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            c[u] = __shfl(my_c, gbase + ((t + u) & (G - 1)), kWave);
-            v[u] = __shfl(my_v, gbase + ((t + u) & (G - 1)), kWave);
-          }
-#pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            if (t + u < cnt && col_ok) {
-              b[u] = *reinterpret_cast<const float4 *>(
-                  B + static_cast<int64_t>(c[u]) * N + col0);
-            }
-          }
-#pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            if (t + u < cnt && col_ok) {
-              acc.x = fmaf(v[u], b[u].x, acc.x);
-              acc.y = fmaf(v[u], b[u].y, acc.y);
-              acc.z = fmaf(v[u], b[u].z, acc.z);
-              acc.w = fmaf(v[u], b[u].w, acc.w);
-            }
+          for (int i = 0; i < 4; ++i) {
+            sum.x = sum.x + t[i].x;
+            sum.y = sum.y + t[i].y;
+            sum.z = sum.z + t[i].z;
+            sum.w = sum.w + t[i].w;
           }
         }
-      }
-      if (row_ok && col_ok) {
-        *reinterpret_cast<float4 *>(C + row * N + col0) = acc;
+        for (; q < lr.nseg; ++q) {
+          const float4 t = *reinterpret_cast<const float4 *>(p0 + static_cast<int64_t>(q) * N + col0);
+          sum.x = sum.x + t.x;
+          sum.y = sum.y + t.y;
+          sum.z = sum.z + t.z;
+          sum.w = sum.w + t.w;
+        }
+        store_nt(C + static_cast<int64_t>(lr.row) * N + col0, sum);
       }
     }
   }
 }
 
-// Scalar fallback for widths that are not a multiple of 4: one wave per row,
-// lanes over columns.
+// Scalar fallback for widths that are not a multiple of 4 (or unaligned
+// operands): one wave per row, lanes over columns, same stated order (long
+// rows as segment chains added left to right).
 __global__ void __launch_bounds__(kSpmmBlock)
     spmm_rowsplit_scalar(int32_t n, const int32_t *__restrict__ ptr,
                          const int32_t *__restrict__ ind,
@@ -114,12 +235,18 @@ __global__ void __launch_bounds__(kSpmmBlock)
   const int64_t nwaves = static_cast<int64_t>(gridDim.x) * blockDim.x / kWave;
   for (int64_t row = wave0; row < n; row += nwaves) {
     const int32_t s = ptr[row], e = ptr[row + 1];
+    const int32_t seg = e - s > kLongRow ? kSegLen : (e - s > 0 ? e - s : 1);
     for (int32_t j = lane; j < N; j += kWave) {
-      float acc = 0.0f;
-      for (int32_t p = s; p < e; ++p) {
-        acc = fmaf(val[p], B[static_cast<int64_t>(ind[p]) * N + j], acc);
+      float sum = 0.0f;
+      for (int32_t q0 = s; q0 < e || q0 == s; q0 += seg) {
+        const int32_t q1 = q0 + seg < e ? q0 + seg : e;
+        float acc = 0.0f;
+        for (int32_t p = q0; p < q1; ++p) {
+          acc = fmaf(val[p], B[static_cast<int64_t>(ind[p]) * N + j], acc);
+        }
+        sum = (q0 == s) ? acc : sum + acc;
       }
-      C[row * N + j] = acc;
+      C[row * N + j] = sum;
     }
   }
 }
@@ -225,20 +352,57 @@ __global__ void fill_uniform(int64_t count, float *__restrict__ vals, uint64_t s
   }
 }
 
+// Workspace of the long-row segments for an n x n CSR with nnz nonzeros and
+// N columns: descriptors, unit owners and unit partials, sized for the most
+// long rows and segments nnz nonzeros allow.
+struct SpmmLongWs {
+  LongCtl *ctl;
+  LongRow *longs;
+  int32_t *owner;
+  float *part;
+};
+
+int64_t max_long_rows(int32_t nnz) { return nnz / (kLongRow + 1) + 1; }
+int64_t max_segments(int32_t nnz) { return nnz / kSegLen + max_long_rows(nnz) + 1; }
+
+SpmmLongWs take_long_ws(Context &ctx, int32_t nnz, int32_t N) {
+  SpmmLongWs w;
+  w.ctl = ctx.take<LongCtl>(1);
+  w.longs = ctx.take<LongRow>(static_cast<size_t>(max_long_rows(nnz)));
+  w.owner = ctx.take<int32_t>(static_cast<size_t>(max_segments(nnz)));
+  w.part = ctx.take<float>(static_cast<size_t>(max_segments(nnz)) * N);
+  return w;
+}
+
 template <int G>
-void launch_rowsplit_g(Context &ctx, int32_t n, const int32_t *ptr, const int32_t *ind,
-                       const float *val, int32_t N, const float *B, float *C) {
+void launch_rowsplit_g(Context &ctx, int32_t n, int32_t nnz, const int32_t *ptr,
+                       const int32_t *ind, const float *val, int32_t N, const float *B,
+                       float *C, const SpmmLongWs &w) {
   constexpr int rpw = kWave / G;
-  int64_t waves = ceil_div64(n, rpw);
-  int g = ctx.grid_for(ceil_div64(waves, kSpmmBlock / kWave), kSpmmBlock, 8);
-  spmm_rowsplit_v4<G><<<g, kSpmmBlock, 0, ctx.stream>>>(n, ptr, ind, val, N, B, C);
+  const int64_t blocks = ceil_div64(ceil_div64(n, rpw), kSpmmWaves);
+  fill_u32(ctx, w.ctl, sizeof(LongCtl) / 4, 0u);
+  spmm_rowsplit_v4<G><<<dim3(static_cast<unsigned>(blocks)), kSpmmBlock, 0, ctx.stream>>>(
+      n, ptr, ind, val, N, B, C, w.ctl, w.longs, w.owner);
+  SP_LAUNCH_CHECK();
+  // Persistent grid over the registered segment units (none: exits at once).
+  const int g = ctx.grid_for(ceil_div64(max_segments(nnz), rpw * kSpmmWaves), kSpmmBlock, 2);
+  spmm_long_segments<G><<<g, kSpmmBlock, 0, ctx.stream>>>(ptr, ind, val, N, B, C, w.ctl,
+                                                            w.longs, w.owner, w.part);
   SP_LAUNCH_CHECK();
 }
 
 } // namespace
 
-void spmm_rowsplit(Context &ctx, int32_t n, const int32_t *ptr, const int32_t *ind,
-                   const float *val, int32_t N, const float *B, float *C) {
+size_t spmm_ws_bytes(int32_t nnz, int32_t N) {
+  return ws_bytes<LongCtl>(1) + ws_bytes<LongRow>(static_cast<size_t>(max_long_rows(nnz))) +
+         ws_bytes<int32_t>(static_cast<size_t>(max_segments(nnz))) +
+         ws_bytes<float>(static_cast<size_t>(max_segments(nnz)) * N);
+}
+
+// Row-split SpMM in the stated order; `w` comes from take_long_ws.
+void spmm_rowsplit(Context &ctx, int32_t n, int32_t nnz, const int32_t *ptr,
+                   const int32_t *ind, const float *val, int32_t N, const float *B, float *C,
+                   const SpmmLongWs &w) {
   bool aligned = (N % 4 == 0) && (reinterpret_cast<uintptr_t>(B) % 16 == 0) &&
                  (reinterpret_cast<uintptr_t>(C) % 16 == 0);
   if (!aligned) {
@@ -249,19 +413,19 @@ void spmm_rowsplit(Context &ctx, int32_t n, const int32_t *ptr, const int32_t *i
   }
   int32_t q = N / 4; // float4 columns
   if (q <= 1) {
-    launch_rowsplit_g<1>(ctx, n, ptr, ind, val, N, B, C);
+    launch_rowsplit_g<1>(ctx, n, nnz, ptr, ind, val, N, B, C, w);
   } else if (q <= 2) {
-    launch_rowsplit_g<2>(ctx, n, ptr, ind, val, N, B, C);
+    launch_rowsplit_g<2>(ctx, n, nnz, ptr, ind, val, N, B, C, w);
   } else if (q <= 4) {
-    launch_rowsplit_g<4>(ctx, n, ptr, ind, val, N, B, C);
+    launch_rowsplit_g<4>(ctx, n, nnz, ptr, ind, val, N, B, C, w);
   } else if (q <= 8) {
-    launch_rowsplit_g<8>(ctx, n, ptr, ind, val, N, B, C);
+    launch_rowsplit_g<8>(ctx, n, nnz, ptr, ind, val, N, B, C, w);
   } else if (q <= 16) {
-    launch_rowsplit_g<16>(ctx, n, ptr, ind, val, N, B, C);
+    launch_rowsplit_g<16>(ctx, n, nnz, ptr, ind, val, N, B, C, w);
   } else if (q <= 32) {
-    launch_rowsplit_g<32>(ctx, n, ptr, ind, val, N, B, C);
+    launch_rowsplit_g<32>(ctx, n, nnz, ptr, ind, val, N, B, C, w);
   } else {
-    launch_rowsplit_g<64>(ctx, n, ptr, ind, val, N, B, C);
+    launch_rowsplit_g<64>(ctx, n, nnz, ptr, ind, val, N, B, C, w);
   }
 }
 
@@ -303,11 +467,13 @@ void sporder_spmm_csr(sporder_context_t h, int32_t n, int32_t nnz,
   Context &ctx = h->impl;
   EventSpan t;
   t.create(kernel_ms != nullptr);
+  if (algo != SPORDER_SPMM_MERGE_PATH) ctx.reserve(spmm_ws_bytes(nnz, cols));
   t.begin(ctx.stream);
   if (algo == SPORDER_SPMM_MERGE_PATH) {
     spmm_merge(ctx, n, nnz, d_ptr, d_ind, d_val, cols, d_b, d_c);
   } else {
-    spmm_rowsplit(ctx, n, d_ptr, d_ind, d_val, cols, d_b, d_c);
+    const SpmmLongWs w = take_long_ws(ctx, nnz, cols);
+    spmm_rowsplit(ctx, n, nnz, d_ptr, d_ind, d_val, cols, d_b, d_c, w);
   }
   t.end(ctx.stream);
   ctx.sync();
@@ -326,10 +492,11 @@ void sporder_bench_cusparse_spmm(sporder_context_t h, int32_t n, int32_t nnz,
   SP_EXPECT(n >= 1 && nnz >= 0, "expect n >= 1 and nnz >= 0");
   Context &ctx = h->impl;
   const int64_t b_count = static_cast<int64_t>(n) * cols;
-  ctx.reserve(ws_bytes<float>(nnz) + 2 * ws_bytes<float>(b_count));
+  ctx.reserve(ws_bytes<float>(nnz) + 2 * ws_bytes<float>(b_count) + spmm_ws_bytes(nnz, cols));
   float *a_val = ctx.take<float>(nnz);
   float *b = ctx.take<float>(b_count);
   float *c = ctx.take<float>(b_count);
+  const SpmmLongWs w = take_long_ws(ctx, nnz, cols);
   // Values from seed ^ 0xA and seed ^ 0xB, as the reference keys its two fills
   // (bench_cusparse_spmm.cu:40,44).
   int ga = ctx.grid_for(ceil_div64(ceil_div64(nnz, 4), 256), 256, 4);
@@ -339,14 +506,14 @@ void sporder_bench_cusparse_spmm(sporder_context_t h, int32_t n, int32_t nnz,
   fill_uniform<<<gb, 256, 0, ctx.stream>>>(b_count, b, seed ^ 0xBull, 1u);
   SP_LAUNCH_CHECK();
   for (int32_t i = 0; i < warmup; ++i) {
-    spmm_rowsplit(ctx, n, d_ptr, d_ind, a_val, cols, b, c);
+    spmm_rowsplit(ctx, n, nnz, d_ptr, d_ind, a_val, cols, b, c, w);
   }
   ctx.sync();
   EventSpan t;
   t.create(true);
   t.begin(ctx.stream);
   for (int32_t i = 0; i < repeat; ++i) {
-    spmm_rowsplit(ctx, n, d_ptr, d_ind, a_val, cols, b, c);
+    spmm_rowsplit(ctx, n, nnz, d_ptr, d_ind, a_val, cols, b, c, w);
   }
   t.end(ctx.stream);
   ctx.sync();

@@ -266,21 +266,29 @@ SPORDER_API void sporder_chunk_similarity_top_k(
 
 /* (new) SpMM kernel variants. */
 typedef enum {
-  SPORDER_SPMM_AUTO = 0,     /* row-split, or merge-path for skewed rows */
+  SPORDER_SPMM_AUTO = 0,     /* row-split with long rows in segments */
   SPORDER_SPMM_ROW_SPLIT = 1,
   SPORDER_SPMM_MERGE_PATH = 2,
 } sporder_spmm_algo_t;
 
 /*
  * (new) C = A * B for a CSR A (n x n, values d_val) and row-major dense
- * B (n x cols) and C (n x cols), fp32.  ROW_SPLIT computes each C element as
- * acc = fmaf(a_p, B[col_p][j], acc) over p in CSR order from 0.0f (bit-exact
- * with a CPU loop in that order); MERGE_PATH splits long rows and adds the
- * partial sums, so it matches within rounding.  *kernel_ms (optional) gets
- * the kernel time from HIP events on the library stream.  The reference
+ * B (n x cols) and C (n x cols), fp32.  ROW_SPLIT (and AUTO) compute each
+ * C element in a stated order, bit-exact with a CPU loop in that order:
+ *   - a row with at most SPORDER_SPMM_LONG_ROW nonzeros:
+ *     acc = fmaf(a_p, B[col_p][j], acc) over p in CSR order from 0.0f;
+ *   - a longer row: segments of SPORDER_SPMM_SEGMENT nonzeros from the row's
+ *     start, each such a chain from 0.0f, added left to right
+ *     (((P0 + P1) + P2) + ...).
+ * Long rows are spread over many waves, so one hub row does not serialise the
+ * product.  MERGE_PATH splits rows at equal nonzero spans and adds the partial
+ * sums with atomics, so it matches within rounding.  *kernel_ms (optional)
+ * gets the time from HIP events on the library stream.  The reference
  * harness contract this serves is SpMMMethod.run
  * (bench/spmm/spmm_bench/base.py:48-59).
  */
+#define SPORDER_SPMM_LONG_ROW 512
+#define SPORDER_SPMM_SEGMENT 512
 SPORDER_API void sporder_spmm_csr(sporder_context_t ctx, int32_t n,
                                   int32_t nnz, const int32_t *d_ptr,
                                   const int32_t *d_ind, const float *d_val,

@@ -78,7 +78,8 @@ def lib():
         L.oracle_reorder.argtypes = [i32, i32, _P(i32), _P(i32), _P(f32), _P(i32), i32,
                                      _P(i32), _P(i32), _P(f32)]
         L.oracle_reorder.restype = None
-        L.oracle_spmm_csr.argtypes = [i32, _P(i32), _P(i32), _P(f32), i32, _P(f32), _P(f32)]
+        L.oracle_spmm_csr.argtypes = [i32, _P(i32), _P(i32), _P(f32), i32, _P(f32), _P(f32),
+                                       i32, i32]
         L.oracle_spmm_csr.restype = None
         L.oracle_num_threads.argtypes = []
         L.oracle_num_threads.restype = i32
@@ -238,7 +239,16 @@ def reorder(ptr, ind, new_order, val=None, symmetric=False):
     return ptr_new, ind_new[:nnz], val_new[:nnz]
 
 
-def spmm_csr(ptr, ind, val, B) -> np.ndarray:
+# The HIP library's stated SpMM order (include/sporder.h SPORDER_SPMM_LONG_ROW,
+# SPORDER_SPMM_SEGMENT): rows longer than LONG_ROW are summed in segments.
+SPMM_LONG_ROW = 512
+SPMM_SEGMENT = 512
+
+
+def spmm_csr(ptr, ind, val, B, long_row=SPMM_LONG_ROW, seg_len=SPMM_SEGMENT) -> np.ndarray:
+    """C = A @ B in the stated order: rows of at most long_row nonzeros as one
+    fmaf chain from 0.0f in CSR order; longer rows as chains over segments of
+    seg_len nonzeros added left to right."""
     ptr, ind = _i32(ptr), _i32(ind)
     val = np.ascontiguousarray(val, dtype=np.float32)
     B = np.ascontiguousarray(B, dtype=np.float32)
@@ -249,7 +259,7 @@ def spmm_csr(ptr, ind, val, B) -> np.ndarray:
     val_c = val if val.size else np.zeros(1, np.float32)
     lib().oracle_spmm_csr(n, _ptr(ptr, ctypes.c_int32), _ptr(ind_c, ctypes.c_int32),
                           _ptr(val_c, ctypes.c_float), N, _ptr(B, ctypes.c_float),
-                          _ptr(C, ctypes.c_float))
+                          _ptr(C, ctypes.c_float), int(long_row), int(seg_len))
     return C
 
 

@@ -586,28 +586,44 @@ void oracle_reorder(int32_t n, int32_t nnz, const int32_t *ptr_old,
 }
 
 // ---------------------------------------------------------------------------
-// CSR SpMM, fp32, row-major B (n x N) and C (n x N):
-//   C[i][j] = fold over p in CSR order of acc = fmaf(val[p], B[ind[p]][j], acc)
-//   starting at acc = 0.0f.
-// This is the accumulation order the HIP row-split kernel uses, so the two are
-// bit-identical.  The reference's SpMM is cuSPARSE (closed source,
+// CSR SpMM, fp32, row-major B (n x N) and C (n x N), in the order the HIP
+// row-split kernel states (include/sporder.h, SPORDER_SPMM_LONG_ROW and
+// SPORDER_SPMM_SEGMENT):
+//   - a row with at most long_row nonzeros: C[i][j] = fold over p in CSR order
+//     of acc = fmaf(val[p], B[ind[p]][j], acc) from acc = 0.0f;
+//   - a longer row: segments of seg_len nonzeros from the row start, each such
+//     a fold from 0.0f, then C[i][j] = ((P0 + P1) + P2) + ... left to right.
+// The reference's SpMM is cuSPARSE (closed source,
 // sporder/src/bench_cusparse_spmm.cu:51-100); its accumulation order is not
 // published, so parity with it is stated as fp64 A@B within 1e-5 relative.
-// Pinned by: fp64 scipy A@B within tolerance (tests/test_oracle_csr.py).
+// Pinned by: fp64 scipy A@B within tolerance, and each output against exact
+// rational arithmetic rounded once per operation in the stated order, with a
+// crafted row whose value depends on the segment boundary
+// (tests/test_oracle_csr.py).
 // ---------------------------------------------------------------------------
 void oracle_spmm_csr(int32_t n, const int32_t *ptr, const int32_t *ind,
-                     const float *val, int32_t N, const float *B, float *C) {
+                     const float *val, int32_t N, const float *B, float *C,
+                     int32_t long_row, int32_t seg_len) {
 #pragma omp parallel for schedule(dynamic, 256)
   for (int32_t i = 0; i < n; ++i) {
     float *crow = C + static_cast<size_t>(i) * N;
-    for (int32_t j = 0; j < N; ++j) {
-      crow[j] = 0.0f;
-    }
-    for (int32_t p = ptr[i]; p < ptr[i + 1]; ++p) {
-      float a = val[p];
-      const float *brow = B + static_cast<size_t>(ind[p]) * N;
+    const int32_t s = ptr[i], e = ptr[i + 1];
+    const int32_t seg = (e - s > long_row) ? seg_len : (e - s > 0 ? e - s : 1);
+    std::vector<float> part(static_cast<size_t>(N));
+    for (int32_t q0 = s; q0 < e || q0 == s; q0 += seg) {
+      const int32_t q1 = std::min(q0 + seg, e);
       for (int32_t j = 0; j < N; ++j) {
-        crow[j] = std::fmaf(a, brow[j], crow[j]);
+        part[j] = 0.0f;
+      }
+      for (int32_t p = q0; p < q1; ++p) {
+        float a = val[p];
+        const float *brow = B + static_cast<size_t>(ind[p]) * N;
+        for (int32_t j = 0; j < N; ++j) {
+          part[j] = std::fmaf(a, brow[j], part[j]);
+        }
+      }
+      for (int32_t j = 0; j < N; ++j) {
+        crow[j] = (q0 == s) ? part[j] : crow[j] + part[j];
       }
     }
   }

@@ -1,7 +1,8 @@
 """GPU parity of the permutation apply and the CSR SpMM.
 
 Reorder: bit-exact against the oracle (integers and copied fp32 values).
-SpMM row-split: bit-exact against the oracle's fmaf loop in CSR order; both
+SpMM row-split: bit-exact against the oracle's stated order (fmaf chains in
+CSR order, rows past SPORDER_SPMM_LONG_ROW in segments added left to right); both
 variants within 1e-5 relative of an fp64 reference (the tolerance north_star
 states for fp32 SpMM).
 """
@@ -35,12 +36,25 @@ def long_row_matrix(n=20000, seed=7):
     return ptr.astype(np.int32), ind.astype(np.int32), val
 
 
+def hub_matrix(n=300_000, hub=250_000, seed=8):
+    """Row 0 holds `hub` entries (489 SpMM segments), the rest 0..8 each."""
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(0, 9, size=n)
+    lens[0] = hub
+    ptr = np.zeros(n + 1, np.int64)
+    np.cumsum(lens, out=ptr[1:])
+    ind = np.concatenate([np.sort(rng.choice(n, size=L, replace=False)) for L in lens])
+    val = rng.standard_normal(ind.shape[0]).astype(np.float32)
+    return ptr.astype(np.int32), ind.astype(np.int32), val
+
+
 def mats():
     return {
         "C1": synth.config1(21),
         "rmat12": synth.rmat(12, 16, 22),
         "stencil16": synth.stencil7(16, 23),
         "longrows": long_row_matrix(),
+        "hub": hub_matrix(),
     }
 
 
