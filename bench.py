@@ -46,6 +46,23 @@ def spmm_bytes(n, nnz, N):
     return 4 * (n + 1) + 8 * nnz + 8 * n * N
 
 
+def pmc_traffic(kernel, n, nnz):
+    """HBM bytes per launch of `kernel` on this workload, from the committed
+    rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE summary (profiles/pmc_traffic.json,
+    counters scaled by a copy kernel of known size); None when absent."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                        "pmc_traffic.json")
+    try:
+        with open(path) as f:
+            table = json.load(f)
+    except (OSError, ValueError):
+        return None
+    rec = table.get(kernel)
+    if not rec or rec.get("n") != n or rec.get("nnz") != nnz:
+        return None
+    return rec.get("bytes_per_launch")
+
+
 def reorder_bytes(n, nnz, k, symmetric):
     b = 2 * (4 * (n + 1) + 4 * nnz) + 8 * n * k   # sketch: CSR + CSC reads, table write
     b += 8 * n * k + 4 * n                         # greedy: table read, order write
@@ -66,6 +83,9 @@ def main():
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="first run one device-to-device copy of BYTES (a kernel of known "
                          "traffic for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
+    ap.add_argument("--only-spmm", action="store_true",
+                    help="profiler pass: one reorder, then --spmm-iters SpMMs at N=128 on the "
+                         "reordered matrix; prints no JSON line")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -116,6 +136,14 @@ def main():
         p2, i2, v2 = sporder.reorder(ptr, ind, order, val=val, symmetric=True, ctx=ctx)
         sporder.spmm_csr(p2, i2, v2, B128, out=out128, ctx=ctx)
         return order, (p2, i2, v2)
+
+    if args.only_spmm:
+        order, (p2, i2, v2) = step()
+        for _ in range(args.spmm_iters):
+            sporder.spmm_csr(p2, i2, v2, B128, out=out128, ctx=ctx)
+        torch.cuda.synchronize()
+        log(f"only-spmm: {args.spmm_iters} SpMMs at N=128 on the reordered matrix")
+        return
 
     for _ in range(args.warmup):
         step()
@@ -180,6 +208,24 @@ def main():
         }
         log(f"spmm N={N}: orig {t_orig:.3f} ms, reordered {t_re:.3f} ms")
 
+    # Gather ceiling of the same kernel at the same shape (n rows, 16 nonzeros
+    # per row, N = 128): columns drawn uniformly from the first 8192 rows (the
+    # 4 MiB of B that one XCD's L2 holds) and from all n rows (C2's pattern:
+    # every B row gather misses L2).
+    ceiling = {}
+    gen = torch.Generator(device=dev).manual_seed(7)
+    cptr = torch.arange(0, nnz + 1, 16, dtype=torch.int32, device=dev)
+    cval = torch.rand(nnz, generator=gen, device=dev)
+    for label, col_span in (("l2_resident_cols", 8192), ("uniform_cols", n)):
+        cind = torch.randint(0, col_span, (nnz,), generator=gen, device=dev, dtype=torch.int32)
+        cind = cind.view(n, 16).sort(dim=1).values.reshape(-1).contiguous()
+        t_c = spmm_ms(cptr, cind, cval, B128)
+        ceiling[label] = {"ms": round(t_c, 4),
+                          "gbs": round(spmm_bytes(n, nnz, 128) / t_c / 1e6, 1),
+                          "gather_gbs": round(4.0 * nnz * 128 / t_c / 1e6, 1)}
+        del cind
+    log(f"spmm ceiling {ceiling}")
+
     k_used = stats["k_used"]
     # Dominant kernel of the step: compare the stage spans with the SpMM.
     stage = {
@@ -198,7 +244,8 @@ def main():
     achieved = algo_bytes[dom] / (stage[dom] * 1e-3) / 1e9
     roofline = {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 1),
                 "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "frac": round(achieved / HBM_PEAK_GBS, 4),
+                "traffic": pmc_traffic(dom, n, nnz),
                 "algorithmic_bytes": algo_bytes[dom], "avg_ms": round(stage[dom], 4)}
     spmm_ach = spmm["128"]["reordered_gbs"]
     roofline_spmm = {"kernel": "spmm_rowsplit_n128", "bound": "hbm", "achieved": spmm_ach,
@@ -259,6 +306,7 @@ def main():
         "csg_stats": stats,
         "roofline": roofline,
         "roofline_spmm": roofline_spmm,
+        "spmm_ceiling_n128": ceiling,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
