@@ -40,6 +40,7 @@ struct ChainCounters {
   int32_t restarts;
   int32_t links;
   double link_weight_sum;
+  double in_chunk_weight; // weight of table entries inside their row's chunk
 };
 
 // The visited bitmap of a chain is written by every lane of the wave with the
@@ -122,6 +123,7 @@ __global__ void __launch_bounds__(kGreedyBlock)
   int32_t cur = start, pos = start, low_word = 0;
   int32_t restarts = 0, links = 0;
   float link_w = 0.0f;
+  double in_w = 0.0; // per lane
 
   while (true) {
     mark_visited(bm, cur - start);
@@ -140,6 +142,7 @@ __global__ void __launch_bounds__(kGreedyBlock)
       int32_t cand = wi_index(e);
       if (cand < 0) break; // valid entries form a prefix
       if (cand < start || cand >= end) continue;
+      in_w += wi_weight(e);
       int32_t b = cand - start;
       if (bm[b >> 5] & (1u << (b & 31))) continue;
       float w = wi_weight(e);
@@ -161,18 +164,23 @@ __global__ void __launch_bounds__(kGreedyBlock)
     restarts += 1;
     cur = start + nxt;
   }
-  if (counters != nullptr && lane == 0) {
-    atomicAdd(&counters->restarts, restarts);
-    atomicAdd(&counters->links, links);
-    atomicAdd(&counters->link_weight_sum, static_cast<double>(link_w));
+  if (counters != nullptr) {
+    if (in_w != 0.0) atomicAdd(&counters->in_chunk_weight, in_w);
+    if (lane == 0) {
+      atomicAdd(&counters->restarts, restarts);
+      atomicAdd(&counters->links, links);
+      atomicAdd(&counters->link_weight_sum, static_cast<double>(link_w));
+    }
   }
 }
 
-// Compact greedy: chunks of at most kGreedyCompactRows rows.  Four waves
-// count each row's valid entries, scan them into per-row offsets and copy
-// the valid entries as (weight bits << 32 | local index) into LDS; then wave
-// 0 runs the chain on LDS alone.  A slice with more than `entry_cap` valid
-// entries keeps the offsets in LDS and reads the entries from global memory.
+// Compact greedy: chunks of at most kGreedyCompactRows rows.  One thread per
+// row counts the row's valid entries that fall inside the chunk (the only ones
+// the chain can follow; all of them for a chunk-restricted table, a few for
+// the global one), the counts are scanned into per-row offsets and the
+// entries copied as (weight bits << 32 | local index) into LDS; then wave 0
+// runs the chain on LDS alone.  A slice with more than `entry_cap` in-chunk
+// entries keeps the offsets in LDS and reads the rows from global memory.
 constexpr int kGreedyCompactRows = 4096;
 
 // Dynamic LDS layout: entries u64[entry_cap] | offsets i32[rows_cap + 1] |
@@ -205,21 +213,30 @@ __global__ void __launch_bounds__(kGreedyBlock)
   const uint64_t *slice = table + static_cast<size_t>(start) * k;
   const int64_t slice_len = static_cast<int64_t>(size) * k;
 
-  for (int32_t r = tid; r <= size; r += kGreedyBlock) s_off[r] = 0;
   for (int32_t w = tid; w < words; w += kGreedyBlock) s_bm[w] = 0u;
-  __syncthreads();
-  // Per-row valid counts (valid entries form a prefix of each row).
-  for (int64_t e0 = static_cast<int64_t>(tid) * 4; e0 < slice_len;
-       e0 += static_cast<int64_t>(kGreedyBlock) * 4) {
-    uint64_t v[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) v[u] = (e0 + u < slice_len) ? slice[e0 + u] : 0;
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      if (e0 + u < slice_len && wi_index(v[u]) >= 0) {
-        atomicAdd(&s_off[(e0 + u) / k + 1], 1);
+  if (tid == 0) s_off[0] = 0;
+  // Per-row count of valid entries inside the chunk (valid entries form a
+  // prefix of each row; only in-chunk entries can be followed).  With
+  // counters, the in-chunk weight is summed for the cut statistic.
+  double in_w = 0.0;
+  for (int32_t r = tid; r < size; r += kGreedyBlock) {
+    const uint64_t *row = slice + static_cast<size_t>(r) * k;
+    int32_t cnt = 0;
+    for (int32_t j = 0; j < k; ++j) {
+      const uint64_t v = row[j];
+      const int32_t c = wi_index(v);
+      if (c < 0) break;
+      if (c >= start && c < end) {
+        cnt += 1;
+        in_w += wi_weight(v);
       }
     }
+    s_off[r + 1] = cnt;
+  }
+  if (counters != nullptr) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) in_w += __shfl_xor(in_w, off, kWave);
+    if (lane == 0 && in_w != 0.0) atomicAdd(&counters->in_chunk_weight, in_w);
   }
   __syncthreads();
   // Inclusive scan of s_off[1..size] by wave 0 -> offsets.
@@ -238,14 +255,16 @@ __global__ void __launch_bounds__(kGreedyBlock)
   const int32_t total = s_total;
   const bool compact = total <= entry_cap;
   if (compact) {
-    for (int64_t e = tid; e < slice_len; e += kGreedyBlock) {
-      uint64_t v = slice[e];
-      int32_t c = wi_index(v);
-      if (c >= 0) {
-        int32_t r = static_cast<int32_t>(e / k), j = static_cast<int32_t>(e % k);
-        uint32_t local = (c >= start && c < end) ? static_cast<uint32_t>(c - start)
-                                                 : 0xFFFFFFFFu;
-        s_ent[s_off[r] + j] = (v & 0xFFFFFFFF00000000ull) | local;
+    for (int32_t r = tid; r < size; r += kGreedyBlock) {
+      const uint64_t *row = slice + static_cast<size_t>(r) * k;
+      int32_t at = s_off[r];
+      for (int32_t j = 0; j < k; ++j) {
+        const uint64_t v = row[j];
+        const int32_t c = wi_index(v);
+        if (c < 0) break;
+        if (c >= start && c < end) {
+          s_ent[at++] = (v & 0xFFFFFFFF00000000ull) | static_cast<uint32_t>(c - start);
+        }
       }
     }
   }
@@ -264,7 +283,10 @@ __global__ void __launch_bounds__(kGreedyBlock)
     float best_w = -1.0f;
     int32_t best_c = -1;
     if (d1 > d0) {
-      for (int32_t j = lane; j < d1 - d0; j += kWave) {
+      // Compacted: the row's in-chunk entries in LDS.  Otherwise the row's
+      // valid prefix from the table, filtered to the chunk.
+      const int32_t len = compact ? d1 - d0 : k;
+      for (int32_t j = lane; j < len; j += kWave) {
         int32_t cl;
         float w;
         if (compact) {
@@ -274,6 +296,7 @@ __global__ void __launch_bounds__(kGreedyBlock)
         } else {
           uint64_t e = slice[static_cast<size_t>(cur) * k + j];
           int32_t c = wi_index(e);
+          if (c < 0) break; // valid entries form a prefix
           cl = (c >= start && c < end) ? c - start : -1;
           w = wi_weight(e);
         }
@@ -488,6 +511,98 @@ void build_table(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
   }
 }
 
+
+// Shared body of csg and cg: the top-k table with `sketch_chunk` rows per
+// sketch chunk, then the greedy chain over chunks of `chain_chunk` rows.
+// Copies the chain counters and table totals to the host when `want_stats`
+// and reads the three stage spans when `want_timing`; ends in one
+// synchronize.
+struct SeriationOut {
+  ChainCounters hc{};
+  TopKTotals ht{};
+  float csr2csc_ms = 0.0f, similarity_ms = 0.0f, chunk_greedy_ms = 0.0f;
+};
+
+SeriationOut seriate(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
+                     const int32_t *d_ind, bool is_symmetric, int32_t k, int32_t m_cap,
+                     int32_t sketch_chunk, int32_t chain_chunk, int32_t *d_new_order,
+                     bool want_stats, bool want_timing) {
+  const int64_t num_chunks = ceil_div64(n, chain_chunk);
+  const int32_t rows_max = static_cast<int32_t>(std::min<int64_t>(chain_chunk, n));
+  const bool compact = rows_max <= kGreedyCompactRows;
+  const int32_t words = static_cast<int32_t>(ceil_div64(rows_max, 32));
+  // General greedy: bitmap in LDS when small enough, else in the workspace.
+  const size_t lds_need = static_cast<size_t>(words) * 4u;
+  const bool bitmap_lds = lds_need <= 64u * 1024u && lds_need <= ctx.lds_per_block;
+  const int general_wpb =
+      bitmap_lds ? static_cast<int>(std::max<size_t>(
+                       1, std::min<size_t>(kGreedyWaves, (64u * 1024u) / std::max<size_t>(lds_need, 1))))
+                 : kGreedyWaves;
+
+  size_t need = table_ws_bytes(n, nnz, k, sketch_chunk, is_symmetric) +
+                ws_bytes<ChainCounters>(1) + ws_bytes<TopKTotals>(1);
+  if (!compact && !bitmap_lds) need += ws_bytes<uint32_t>(static_cast<size_t>(num_chunks) * words);
+  ctx.reserve(need);
+  uint64_t *table = ctx.take<uint64_t>(static_cast<size_t>(n) * k);
+  ChainCounters *counters = ctx.take<ChainCounters>(1);
+  TopKTotals *totals = ctx.take<TopKTotals>(1);
+  uint32_t *gbitmap = (!compact && !bitmap_lds)
+                          ? ctx.take<uint32_t>(static_cast<size_t>(num_chunks) * words)
+                          : nullptr;
+
+  EventSpan t_csc, t_sim, t_greedy;
+  t_csc.create(want_timing);
+  t_sim.create(want_timing);
+  t_greedy.create(want_timing);
+
+  if (want_stats) {
+    zero_words(ctx, counters, sizeof(ChainCounters));
+    zero_words(ctx, totals, sizeof(TopKTotals));
+  }
+
+  build_table(ctx, n, nnz, d_ptr, d_ind, is_symmetric, k, m_cap, sketch_chunk, table, &t_csc,
+              &t_sim);
+  if (want_stats) top_k_stats(ctx, n, k, table, totals);
+
+  t_greedy.begin(ctx.stream);
+  if (compact) {
+    // About 20 KiB of LDS per chunk at chain_chunk 1024: several chunks per CU.
+    const int32_t entry_cap = 2048;
+    greedy_compact_kernel<<<dim3(static_cast<unsigned>(num_chunks)), kGreedyBlock,
+                            greedy_compact_lds(rows_max, entry_cap), ctx.stream>>>(
+        n, k, chain_chunk, table, d_new_order, want_stats ? counters : nullptr, rows_max,
+        entry_cap);
+    SP_LAUNCH_CHECK();
+  } else {
+    int64_t blocks = ceil_div64(num_chunks, general_wpb);
+    size_t lds = bitmap_lds ? static_cast<size_t>(general_wpb) * words * 4u : 0;
+    greedy_kernel<<<dim3(static_cast<unsigned>(blocks)), general_wpb * kWave, lds,
+                    ctx.stream>>>(n, k, chain_chunk, static_cast<int32_t>(num_chunks), table,
+                                  d_new_order, want_stats ? counters : nullptr, gbitmap, words,
+                                  bitmap_lds ? 1 : 0);
+    SP_LAUNCH_CHECK();
+  }
+  t_greedy.end(ctx.stream);
+
+  SeriationOut out;
+  if (want_stats) {
+    SP_HIP(hipMemcpyAsync(&out.hc, counters, sizeof(out.hc), hipMemcpyDeviceToHost,
+                          ctx.stream));
+    SP_HIP(hipMemcpyAsync(&out.ht, totals, sizeof(out.ht), hipMemcpyDeviceToHost,
+                          ctx.stream));
+  }
+  ctx.sync();
+  if (want_timing) {
+    out.csr2csc_ms = t_csc.ms();
+    out.similarity_ms = t_sim.ms();
+    out.chunk_greedy_ms = t_greedy.ms();
+  }
+  t_csc.destroy();
+  t_sim.destroy();
+  t_greedy.destroy();
+  return out;
+}
+
 } // namespace
 
 void top_k_stats(Context &ctx, int32_t n, int32_t k, const uint64_t *d_table,
@@ -525,95 +640,73 @@ void sporder_chunk_similarity_greedy(sporder_context_t h, int32_t n,
     stats->m_used = m_cap;
     stats->chunk_size_used = chunk_size;
   }
-  const int64_t num_chunks = ceil_div64(n, chunk_size);
-  const int32_t rows_max = static_cast<int32_t>(std::min<int64_t>(chunk_size, n));
-  const bool compact = rows_max <= kGreedyCompactRows;
-  const int32_t words = static_cast<int32_t>(ceil_div64(rows_max, 32));
-  // General greedy: bitmap in LDS when small enough, else in the workspace.
-  const size_t lds_need = static_cast<size_t>(words) * 4u;
-  const bool bitmap_lds = lds_need <= 64u * 1024u && lds_need <= ctx.lds_per_block;
-  const int general_wpb =
-      bitmap_lds ? static_cast<int>(std::max<size_t>(
-                       1, std::min<size_t>(kGreedyWaves, (64u * 1024u) / std::max<size_t>(lds_need, 1))))
-                 : kGreedyWaves;
-
-  size_t need = table_ws_bytes(n, nnz, k, chunk_size, is_symmetric) +
-                ws_bytes<ChainCounters>(1) + ws_bytes<TopKTotals>(1);
-  if (!compact && !bitmap_lds) need += ws_bytes<uint32_t>(static_cast<size_t>(num_chunks) * words);
-  ctx.reserve(need);
-  uint64_t *table = ctx.take<uint64_t>(static_cast<size_t>(n) * k);
-  ChainCounters *counters = ctx.take<ChainCounters>(1);
-  TopKTotals *totals = ctx.take<TopKTotals>(1);
-  uint32_t *gbitmap = (!compact && !bitmap_lds)
-                          ? ctx.take<uint32_t>(static_cast<size_t>(num_chunks) * words)
-                          : nullptr;
-
-  EventSpan t_csc, t_sim, t_greedy;
-  t_csc.create(timing != nullptr);
-  t_sim.create(timing != nullptr);
-  t_greedy.create(timing != nullptr);
-
-  if (stats) {
-    zero_words(ctx, counters, sizeof(ChainCounters));
-    zero_words(ctx, totals, sizeof(TopKTotals));
-  }
-
-  build_table(ctx, n, nnz, d_ptr, d_ind, is_symmetric, k, m_cap, chunk_size, table, &t_csc,
-              &t_sim);
-  if (stats) top_k_stats(ctx, n, k, table, totals);
-
-  t_greedy.begin(ctx.stream);
-  if (compact) {
-    // About 20 KiB of LDS per chunk at chunk_size 1024: several chunks per CU.
-    const int32_t entry_cap = 2048;
-    greedy_compact_kernel<<<dim3(static_cast<unsigned>(num_chunks)), kGreedyBlock,
-                            greedy_compact_lds(rows_max, entry_cap), ctx.stream>>>(
-        n, k, chunk_size, table, d_new_order, stats ? counters : nullptr, rows_max,
-        entry_cap);
-    SP_LAUNCH_CHECK();
-  } else {
-    int64_t blocks = ceil_div64(num_chunks, general_wpb);
-    size_t lds = bitmap_lds ? static_cast<size_t>(general_wpb) * words * 4u : 0;
-    greedy_kernel<<<dim3(static_cast<unsigned>(blocks)), general_wpb * kWave, lds,
-                    ctx.stream>>>(n, k, chunk_size, static_cast<int32_t>(num_chunks), table,
-                                  d_new_order, stats ? counters : nullptr, gbitmap, words,
-                                  bitmap_lds ? 1 : 0);
-    SP_LAUNCH_CHECK();
-  }
-  t_greedy.end(ctx.stream);
-
-  ChainCounters hc{};
-  TopKTotals ht{};
-  if (stats) {
-    SP_HIP(hipMemcpyAsync(&hc, counters, sizeof(hc), hipMemcpyDeviceToHost,
-                          ctx.stream));
-    SP_HIP(hipMemcpyAsync(&ht, totals, sizeof(ht), hipMemcpyDeviceToHost,
-                          ctx.stream));
-  }
-  ctx.sync();
-
+  const SeriationOut r = seriate(ctx, n, nnz, d_ptr, d_ind, is_symmetric, k, m_cap, chunk_size,
+                                 chunk_size, d_new_order, stats != nullptr, timing != nullptr);
   if (stats) {
     // Reference: sporder/src/csg/stats_collector.cu:43-63.
-    stats->avg_degree = static_cast<double>(ht.total_degree) / n;
+    stats->avg_degree = static_cast<double>(r.ht.total_degree) / n;
     stats->avg_edge_weight =
-        ht.total_degree > 0 ? ht.total_weight / static_cast<double>(ht.total_degree)
-                            : 0.0;
-    stats->zero_degree_rows = ht.zero_degree_rows;
-    stats->chain_restarts = hc.restarts;
-    stats->avg_followed_weight =
-        hc.links > 0 ? hc.link_weight_sum / hc.links : 0.0;
+        r.ht.total_degree > 0 ? r.ht.total_weight / static_cast<double>(r.ht.total_degree)
+                              : 0.0;
+    stats->zero_degree_rows = r.ht.zero_degree_rows;
+    stats->chain_restarts = r.hc.restarts;
+    stats->avg_followed_weight = r.hc.links > 0 ? r.hc.link_weight_sum / r.hc.links : 0.0;
   }
   if (timing) {
-    timing->csr2csc_ms = t_csc.ms();
-    timing->similarity_ms = t_sim.ms();
-    timing->chunk_greedy_ms = t_greedy.ms();
+    timing->csr2csc_ms = r.csr2csc_ms;
+    timing->similarity_ms = r.similarity_ms;
+    timing->chunk_greedy_ms = r.chunk_greedy_ms;
     timing->wall_ms = std::chrono::duration<double, std::milli>(
                           std::chrono::steady_clock::now() - wall0)
                           .count();
   }
-  t_csc.destroy();
-  t_sim.destroy();
-  t_greedy.destroy();
+}
+
+void sporder_chunk_greedy(sporder_context_t h, int32_t n, int32_t nnz, const int32_t *d_ptr,
+                          const int32_t *d_ind, bool is_symmetric, int32_t k,
+                          float oversampling, int32_t chunk_size, int32_t *d_new_order,
+                          sporder_cg_timing_t *timing, sporder_cg_stats_t *stats) {
+  auto wall0 = std::chrono::steady_clock::now();
+  SP_EXPECT(h != nullptr, "null context");
+  SP_EXPECT(n >= 1 && nnz >= 0, "expect n >= 1 and nnz >= 0");
+  Context &ctx = h->impl;
+  // Defaults: reference sporder/src/sporder.cpp:113-125.
+  if (k <= 0) k = std::min(256, std::max(16, 1 * (nnz / n)));
+  if (oversampling <= 0.0f) oversampling = 4.0f;
+  if (chunk_size <= 0) chunk_size = 1024;
+  // The global sketch is the chunked one with a single chunk of n rows
+  // (reference sporder/src/common/similarity_top_k.cu:10-51 scans every row
+  // of each column; the chunk filter [0, n) keeps them all).
+  validate_sketch_args(k, oversampling, n);
+  const int32_t m_cap = sketch_m(k, oversampling);
+  if (stats) {
+    stats->k_used = k;
+    stats->m_used = m_cap;
+    stats->chunk_size_used = chunk_size;
+  }
+  const SeriationOut r = seriate(ctx, n, nnz, d_ptr, d_ind, is_symmetric, k, m_cap, n,
+                                 chunk_size, d_new_order, stats != nullptr, timing != nullptr);
+  if (stats) {
+    // Reference: sporder/src/cg/stats_collector.cu:45-72.
+    stats->avg_degree = static_cast<double>(r.ht.total_degree) / n;
+    stats->avg_edge_weight =
+        r.ht.total_degree > 0 ? r.ht.total_weight / static_cast<double>(r.ht.total_degree)
+                              : 0.0;
+    stats->zero_degree_rows = r.ht.zero_degree_rows;
+    stats->chain_restarts = r.hc.restarts;
+    stats->avg_followed_weight = r.hc.links > 0 ? r.hc.link_weight_sum / r.hc.links : 0.0;
+    const double cut =
+        r.ht.total_weight > 0.0 ? 1.0 - r.hc.in_chunk_weight / r.ht.total_weight : 0.0;
+    stats->cut_weight_fraction = std::min(1.0, std::max(0.0, cut));
+  }
+  if (timing) {
+    timing->csr2csc_ms = r.csr2csc_ms;
+    timing->similarity_ms = r.similarity_ms;
+    timing->chunk_greedy_ms = r.chunk_greedy_ms;
+    timing->wall_ms = std::chrono::duration<double, std::milli>(
+                          std::chrono::steady_clock::now() - wall0)
+                          .count();
+  }
 }
 
 void sporder_chunk_similarity_top_k(sporder_context_t h, int32_t n, int32_t nnz,

@@ -1,7 +1,9 @@
 """Counterparts of the reference bench plugins that call the hot path.
 
-* Reorder plugin for ``sporder-csg``: ``reorder(csr, params) -> ReorderResult``
-  (reference bench/reorder/reorder_bench/methods/sporder_csg.py:25-70), with
+* Reorder plugins for ``sporder-csg`` and ``sporder-cg``:
+  ``reorder(csr, params)`` / ``reorder_cg(csr, params) -> ReorderResult``
+  (reference bench/reorder/reorder_bench/methods/sporder_csg.py:25-70 and
+  sporder_cg.py:25-70; ``REORDER_METHODS`` maps the method names), with
   ``prep_sporder_gpu`` (loader.py:63-93), ``flush_l2`` (timing.py:29-42),
   ``row_perm_from_order`` (loader.py:124-128), ``timed_ms`` (timing.py:8-15)
   and the ``ReorderResult`` record (types.py:9-17).  Device arrays are torch
@@ -93,11 +95,10 @@ def row_perm_from_order(order, nrows: int) -> np.ndarray:
     return perm
 
 
-def reorder(csr: scipy.sparse.csr_matrix, params: dict[str, Any]) -> ReorderResult:
-    """The ``sporder-csg`` reorder method: warmup call, cache flush, timed call;
-    reorder_time_ms is the library's wall_ms (reference sporder_csg.py:25-70)."""
-    from chunkedgreedy_amd import sporder
-
+def _reorder_with(entry, csr: scipy.sparse.csr_matrix, params: dict[str, Any]) -> ReorderResult:
+    """Warmup call, cache flush, timed call; reorder_time_ms is the library's
+    wall_ms (reference sporder_csg.py:25-70 and sporder_cg.py:25-70 share this
+    shape)."""
     auto_detect = bool(params.get("auto_detect_symmetric", True))
     ptr, ind, is_symmetric, prep_ms = prep_sporder_gpu(csr, detect_symmetric=auto_detect)
     nrows = csr.shape[0]
@@ -108,9 +109,9 @@ def reorder(csr: scipy.sparse.csr_matrix, params: dict[str, Any]) -> ReorderResu
         "chunk_size": int(params.get("chunk_size", 0)),
         "with_stats": False,
     }
-    sporder.chunk_similarity_greedy(ptr, ind, with_timing=False, **call_kwargs)
+    entry(ptr, ind, with_timing=False, **call_kwargs)
     flush_l2(ptr.device.index or 0)
-    order, timing = sporder.chunk_similarity_greedy(ptr, ind, with_timing=True, **call_kwargs)
+    order, timing = entry(ptr, ind, with_timing=True, **call_kwargs)
     breakdown = {
         "csr2csc_ms": float(timing.get("csr2csc_ms", 0.0)),
         "similarity_ms": float(timing.get("similarity_ms", 0.0)),
@@ -122,6 +123,24 @@ def reorder(csr: scipy.sparse.csr_matrix, params: dict[str, Any]) -> ReorderResu
                          prep_time_ms=prep_ms, perm_trans_ms=bucket[0],
                          timing_breakdown=breakdown,
                          effective_params={"is_symmetric": is_symmetric})
+
+
+def reorder(csr: scipy.sparse.csr_matrix, params: dict[str, Any]) -> ReorderResult:
+    """The ``sporder-csg`` reorder method (reference sporder_csg.py:25-70)."""
+    from chunkedgreedy_amd import sporder
+
+    return _reorder_with(sporder.chunk_similarity_greedy, csr, params)
+
+
+def reorder_cg(csr: scipy.sparse.csr_matrix, params: dict[str, Any]) -> ReorderResult:
+    """The ``sporder-cg`` reorder method, "CG w/o Stage 1" (reference
+    sporder_cg.py:25-70)."""
+    from chunkedgreedy_amd import sporder
+
+    return _reorder_with(sporder.chunk_greedy, csr, params)
+
+
+REORDER_METHODS = {"sporder-csg": reorder, "sporder-cg": reorder_cg}
 
 
 def apply_row_perm(csr: scipy.sparse.csr_matrix, row_perm) -> scipy.sparse.csr_matrix:

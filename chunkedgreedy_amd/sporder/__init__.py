@@ -6,10 +6,11 @@ defaults and return conventions, backed by libsporder_hip.so.  Arrays are
 torch tensors on a ROCm GPU (int32 CSR ``ptr``/``ind``); results come back
 as torch tensors on the same device.
 
-Provided: chunk_similarity_greedy (sporder-csg), reorder, similarity_graph,
-bench_cusparse_spmm, plus spmm_csr and chunk_similarity_top_k (new).
-hierarchical_matching, chunk_greedy, count_pillars and similarity_graph_exact
-exist for import compatibility and raise NotImplementedError.
+Provided: chunk_similarity_greedy (sporder-csg), chunk_greedy (sporder-cg),
+reorder, similarity_graph, bench_cusparse_spmm, plus spmm_csr and
+chunk_similarity_top_k (new).  hierarchical_matching, count_pillars and
+similarity_graph_exact exist for import compatibility and raise
+NotImplementedError.
 """
 
 from __future__ import annotations
@@ -165,8 +166,37 @@ def hierarchical_matching(ptr, ind, *, is_symmetric=False, num_levels=1, k=0,
 
 def chunk_greedy(ptr, ind, *, is_symmetric=False, k=0, oversampling=0.0, chunk_size=0,
                  with_timing=False, with_stats=False, ctx=None):
-    """Not part of this build yet (reference __init__.py:311-377)."""
-    return _chunk_greedy(ptr, ind)
+    """Chunked greedy seriation on the global similarity graph (sporder-cg,
+    "CG w/o Stage 1").
+
+    Every row gets its top-k Dice neighbours from a space-saving sketch over
+    the whole matrix (capacity 32*ceil(int(k*oversampling)/32)); rows are then
+    cut into aligned chunks of ``chunk_size`` and a greedy nearest-neighbour
+    chain, following only neighbours inside the chunk and restarting at the
+    lowest unvisited row, orders each chunk.
+
+    Arguments:
+        ptr, ind: int32 GPU arrays, CSR row pointers (n+1) and columns (nnz)
+        is_symmetric: the pattern equals its transpose (skips the transpose)
+        k: neighbours per row (0 = clamp(nnz // n, 16, 256))
+        oversampling: sketch oversampling (0 = 4.0); int(k*oversampling) <= 512
+        chunk_size: rows per chunk (0 = 1024)
+        with_timing: also return {wall_ms, csr2csc_ms, similarity_ms,
+            chunk_greedy_ms}
+        with_stats: also return {k_used, m_used, avg_degree, avg_edge_weight,
+            zero_degree_rows, chunk_size_used, chain_restarts,
+            avg_followed_weight, cut_weight_fraction}; cut_weight_fraction is
+            the top-k edge weight leaving its row's chunk over the total
+        ctx: Context, or None for the shared default context
+
+    Returns new_order (int32, new2old), followed by timing and/or stats when
+    requested.  Reference: sporder/python/sporder/__init__.py:311-377.
+    """
+    new_order, timing, stats = _chunk_greedy(
+        ptr, ind, is_symmetric=is_symmetric, k=k, oversampling=oversampling,
+        chunk_size=chunk_size, with_timing=with_timing, with_stats=with_stats, ctx=ctx)
+    result = _pack(_asarray_like(new_order, ptr), timing, stats, with_timing, with_stats)
+    return result if len(result) > 1 else result[0]
 
 
 def count_pillars(ptr, ind, height, *, ctx=None):

@@ -145,6 +145,39 @@ def chunk_similarity_greedy(ptr, ind, is_symmetric=False, k=0, oversampling=0.0,
     return new_order, timing_info, stats_info
 
 
+def chunk_greedy(ptr, ind, is_symmetric=False, k=0, oversampling=0.0, chunk_size=0,
+                 with_timing=False, with_stats=False, ctx=None):
+    """Reference bindings.cpp:258-312."""
+    ptr = _gpu_in(ptr, torch.int32, "ptr")
+    ind = _gpu_in(ind, torch.int32, "ind")
+    n, nnz = _sizes(ptr, ind)
+    c = _resolve(ctx, ptr)
+    new_order = torch.empty(n, dtype=torch.int32, device=ptr.device)
+    timing = _lib.CgTiming()
+    stats = _lib.CgStats()
+    c._lib.sporder_chunk_greedy(
+        c.handle, n, nnz, _addr(ptr), _addr(ind), bool(is_symmetric), int(k),
+        float(oversampling), int(chunk_size), _addr(new_order),
+        ctypes.byref(timing) if with_timing else None,
+        ctypes.byref(stats) if with_stats else None)
+    timing_info = None
+    if with_timing:
+        timing_info = {"wall_ms": timing.wall_ms, "csr2csc_ms": timing.csr2csc_ms,
+                       "similarity_ms": timing.similarity_ms,
+                       "chunk_greedy_ms": timing.chunk_greedy_ms}
+    stats_info = None
+    if with_stats:
+        stats_info = {"k_used": stats.k_used, "m_used": stats.m_used,
+                      "avg_degree": stats.avg_degree,
+                      "avg_edge_weight": stats.avg_edge_weight,
+                      "zero_degree_rows": stats.zero_degree_rows,
+                      "chunk_size_used": stats.chunk_size_used,
+                      "chain_restarts": stats.chain_restarts,
+                      "avg_followed_weight": stats.avg_followed_weight,
+                      "cut_weight_fraction": stats.cut_weight_fraction}
+    return new_order, timing_info, stats_info
+
+
 def reorder(ptr, ind, val=None, new_order=None, symmetric=False, ctx=None):
     """Reference bindings.cpp:151-202."""
     ptr = _gpu_in(ptr, torch.int32, "ptr")
@@ -293,6 +326,5 @@ def _not_built(name):
 # Entry points the reference imports at package load (reference
 # sporder/python/sporder/__init__.py:3-13) that this build does not provide.
 hierarchical_matching = _not_built("hierarchical_matching")
-chunk_greedy = _not_built("chunk_greedy")
 count_pillars = _not_built("count_pillars")
 similarity_graph_exact = _not_built("similarity_graph_exact")

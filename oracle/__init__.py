@@ -216,6 +216,40 @@ def chunk_similarity_greedy(ptr, ind, *, is_symmetric=False, k=0, oversampling=0
     return out
 
 
+def chunk_greedy(ptr, ind, *, is_symmetric=False, k=0, oversampling=0.0, chunk_size=0,
+                 return_table=False):
+    """Oracle of sporder_chunk_greedy (reference sporder/src/cg/chunk_greedy.cu:110-158):
+    the global sketch (sporder/src/common/similarity_top_k.cu:10-51, which is the
+    chunked sketch with one chunk of n rows), then the per-chunk chain of
+    oracle_greedy.  Stats follow sporder/src/cg/stats_collector.cu:45-72:
+    cut_weight_fraction = 1 - (weight of table entries inside their row's chunk)
+    / (weight of all table entries), clamped to [0, 1].  Returns
+    (new_order, stats[, table])."""
+    ptr, ind = _i32(ptr), _i32(ind)
+    n = ptr.shape[0] - 1
+    nnz = ind.shape[0]
+    k_used, ovs_used, chunk_used, m_used = csg_defaults(n, nnz, k, oversampling, chunk_size)
+    table = chunk_similarity_top_k(ptr, ind, k_used, n, ovs_used, is_symmetric)
+    order, ch = greedy(table, chunk_used)
+    deg, wsum, zeros = top_k_stats(table)
+    idx, w = unpack_table(table)
+    valid = idx >= 0
+    rows = np.broadcast_to(np.arange(n)[:, None], idx.shape)
+    same = valid & (idx // chunk_used == rows // chunk_used)
+    in_w = float(w[same].astype(np.float64).sum())
+    cut = 1.0 - in_w / wsum if wsum > 0 else 0.0
+    stats = {"k_used": k_used, "m_used": m_used,
+             "avg_degree": deg / n, "avg_edge_weight": wsum / deg if deg > 0 else 0.0,
+             "zero_degree_rows": zeros, "chunk_size_used": chunk_used,
+             "chain_restarts": ch["restarts"],
+             "avg_followed_weight": ch["link_weight_sum"] / ch["links"] if ch["links"] else 0.0,
+             "cut_weight_fraction": min(1.0, max(0.0, cut))}
+    out = (order, stats)
+    if return_table:
+        out += (table,)
+    return out
+
+
 def reorder(ptr, ind, new_order, val=None, symmetric=False):
     ptr, ind, new_order = _i32(ptr), _i32(ind), _i32(new_order)
     n = ptr.shape[0] - 1
@@ -266,7 +300,7 @@ def spmm_csr(ptr, ind, val, B, long_row=SPMM_LONG_ROW, seg_len=SPMM_SEGMENT) -> 
 __all__ = [
     "CsgStats", "build", "lib", "num_threads", "set_num_threads", "unpack_table",
     "pack_table", "csg_defaults", "csr2csc", "chunk_similarity_top_k", "sketch_stream",
-    "greedy", "top_k_stats", "chunk_similarity_greedy", "reorder", "spmm_csr",
+    "greedy", "top_k_stats", "chunk_similarity_greedy", "chunk_greedy", "reorder", "spmm_csr",
 ]
 
 if os.environ.get("SPORDER_ORACLE_THREADS"):

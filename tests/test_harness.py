@@ -69,6 +69,18 @@ def test_reorder_plugin_matches_oracle(sporder):
 
 
 @pytest.mark.gpu
+def test_cg_reorder_plugin_matches_oracle(sporder):
+    ptr, ind, val = synth.config1(10)
+    a = sp.csr_matrix((val, ind, ptr), shape=(20_000, 20_000))
+    res = harness.REORDER_METHODS["sporder-cg"](a, {"k": 0, "oversampling": 0.0,
+                                                   "chunk_size": 0,
+                                                   "auto_detect_symmetric": True})
+    o, _ = oracle.chunk_greedy(ptr, ind, is_symmetric=False)
+    assert np.array_equal(res.row_perm, o.astype(np.int64))
+    assert set(res.timing_breakdown) == {"csr2csc_ms", "similarity_ms", "chunk_greedy_ms"}
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("name", ["hip-csr-spmm", "hip-csr-spmm-merge"])
 def test_spmm_plugin(sporder, name):
     ptr, ind, val = synth.config1(9)
