@@ -59,6 +59,7 @@ struct Context {
   int max_threads_per_cu = 0;
   size_t lds_per_block = 0;
   Workspace ws;
+  Workspace aux; // second grow-only buffer, for temporaries sized mid-call
   hipEvent_t ev[8] = {};
 
   void init();
@@ -67,6 +68,10 @@ struct Context {
 
   // Grow the workspace to hold `bytes` (rounded), then reset the cursor.
   void reserve(size_t bytes);
+  // Base of the auxiliary buffer grown to at least `bytes`, for temporaries
+  // whose size is only known after part of a call has run (the main
+  // workspace's earlier takes stay valid).
+  void *aux_reserve(size_t bytes);
   template <typename T> T *take(size_t count) {
     size_t bytes = Workspace::align(count * sizeof(T) + (count == 0 ? 1 : 0));
     SP_EXPECT(ws.offset + bytes <= ws.capacity,

@@ -44,6 +44,10 @@ void Context::destroy() {
     SP_HIP(hipFree(ws.base));
     ws.base = nullptr;
   }
+  if (aux.base) {
+    SP_HIP(hipFree(aux.base));
+    aux.base = nullptr;
+  }
   SP_HIP(hipStreamDestroy(stream));
   SP_HIP(hipSetDevice(cur));
 }
@@ -65,6 +69,22 @@ void Context::reserve(size_t bytes) {
     ws.capacity = cap;
   }
   ws.offset = 0;
+}
+
+void *Context::aux_reserve(size_t bytes) {
+  bytes = Workspace::align(bytes + 256);
+  if (bytes > aux.capacity) {
+    SP_HIP(hipStreamSynchronize(stream));
+    if (aux.base) {
+      SP_HIP(hipFree(aux.base));
+      aux.base = nullptr;
+    }
+    size_t grown = aux.capacity + aux.capacity / 2;
+    size_t cap = bytes > grown ? bytes : grown;
+    SP_HIP(hipMalloc(&aux.base, cap));
+    aux.capacity = cap;
+  }
+  return aux.base;
 }
 
 namespace {

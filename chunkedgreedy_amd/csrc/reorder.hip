@@ -9,7 +9,8 @@
 // The reference sorts rows with cub::DeviceSegmentedSort.  Here rows are
 // sorted by size class: up to 64 entries in one wave (register bitonic network
 // over lanes), up to kBlockSortCap entries in one workgroup (LDS bitonic), and
-// longer rows with the library's stable radix sort, one row at a time.  Column
+// longer rows all together with the library's stable radix sort (by column,
+// then by row).  Column
 // keys of a valid permutation are distinct within a row, so every method gives
 // the same (unique) sorted result.
 #include "common.hpp"
@@ -214,6 +215,114 @@ __global__ void __launch_bounds__(kBlockSortThreads)
   }
 }
 
+// ---- rows longer than kBlockSortCap: one device-wide sort ------------------
+//
+// Their entries are gathered into one array and sorted by (row rank, column):
+// a stable radix sort by column, then a stable sort by rank, which keeps the
+// column order inside each rank.  Rank i's entries then occupy
+// [off[i], off[i+1]) in order and are scattered back to row i's range.
+
+__global__ void huge_lengths(const int32_t *__restrict__ ptr_new,
+                             const int32_t *__restrict__ huge_rows, int32_t hcount,
+                             int32_t *__restrict__ len) {
+  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+       i <= hcount; i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    if (i < hcount) {
+      const int32_t r = huge_rows[i];
+      len[i] = ptr_new[r + 1] - ptr_new[r];
+    } else {
+      len[i] = 0;
+    }
+  }
+}
+
+// One workgroup per huge row: column keys, gathered indices and ranks.
+__global__ void huge_gather(const int32_t *__restrict__ ptr_new,
+                            const int32_t *__restrict__ huge_rows, int32_t hcount,
+                            const int32_t *__restrict__ off,
+                            const int32_t *__restrict__ unsorted,
+                            uint32_t *__restrict__ keys, uint32_t *__restrict__ idx,
+                            uint32_t *__restrict__ rank) {
+  for (int32_t i = blockIdx.x; i < hcount; i += gridDim.x) {
+    const int32_t s = ptr_new[huge_rows[i]];
+    const int32_t g0 = off[i], len = off[i + 1] - g0;
+    for (int32_t t = threadIdx.x; t < len; t += blockDim.x) {
+      keys[g0 + t] = static_cast<uint32_t>(unsorted[s + t]);
+      idx[g0 + t] = static_cast<uint32_t>(g0 + t);
+      rank[g0 + t] = static_cast<uint32_t>(i);
+    }
+  }
+}
+
+__global__ void huge_rank_keys(int64_t count, const uint32_t *__restrict__ by_col,
+                               const uint32_t *__restrict__ rank,
+                               uint32_t *__restrict__ keys) {
+  for (int64_t q = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; q < count;
+       q += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    keys[q] = rank[by_col[q]];
+  }
+}
+
+// Sorted position q holds gathered entry g = order[q] of rank i = rank[g];
+// it goes to slot q - off[i] of row huge_rows[i].
+__global__ void huge_scatter(int64_t count, const int32_t *__restrict__ ptr_new,
+                             const int32_t *__restrict__ huge_rows,
+                             const int32_t *__restrict__ off,
+                             const uint32_t *__restrict__ order,
+                             const uint32_t *__restrict__ rank,
+                             const int32_t *__restrict__ unsorted,
+                             const float *__restrict__ val_unsorted,
+                             int32_t *__restrict__ ind_new, float *__restrict__ val_new) {
+  for (int64_t q = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; q < count;
+       q += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const uint32_t g = order[q];
+    const int32_t i = static_cast<int32_t>(rank[g]);
+    const int32_t s = ptr_new[huge_rows[i]];
+    const int32_t src = s + static_cast<int32_t>(g) - off[i];
+    const int32_t dst = s + static_cast<int32_t>(q) - off[i];
+    ind_new[dst] = unsorted[src];
+    if (val_new) val_new[dst] = val_unsorted[src];
+  }
+}
+
+// Sorts rows huge_rows[0 .. hcount) (entries unsorted in `unsorted`,
+// `val_unsorted`) into ind_new / val_new.  One host read of the total length.
+void sort_huge_rows(Context &ctx, int32_t n, const int32_t *ptr_new, const int32_t *huge_rows,
+                    int32_t hcount, const int32_t *unsorted, const float *val_unsorted,
+                    int32_t *ind_new, float *val_new, int32_t *off, int32_t *scan_tmp) {
+  const int g1 = ctx.grid_for(ceil_div64(static_cast<int64_t>(hcount) + 1, 256), 256, 4);
+  huge_lengths<<<g1, 256, 0, ctx.stream>>>(ptr_new, huge_rows, hcount, off);
+  SP_LAUNCH_CHECK();
+  scan_i32(ctx, off, off, static_cast<int64_t>(hcount) + 1, false, scan_tmp);
+  int32_t total = 0;
+  SP_HIP(hipMemcpyAsync(&total, off + hcount, sizeof(int32_t), hipMemcpyDeviceToHost,
+                        ctx.stream));
+  ctx.sync();
+  if (total == 0) return;
+  const size_t H = static_cast<size_t>(total);
+  const size_t tmp_elems = radix_tmp_elems(total);
+  auto *base = static_cast<uint32_t *>(ctx.aux_reserve((7 * H + tmp_elems) * 4 + 8 * 256));
+  auto carve = [&](size_t elems) {
+    uint32_t *p = base;
+    base += (elems + 63) & ~size_t(63);
+    return p;
+  };
+  uint32_t *keys = carve(H), *idx = carve(H), *rank = carve(H), *k1 = carve(H), *v1 = carve(H);
+  uint32_t *ka = carve(H), *va = carve(H);
+  int32_t *tmp = reinterpret_cast<int32_t *>(carve(tmp_elems));
+  huge_gather<<<std::min<int32_t>(hcount, ctx.num_cus * 8), 256, 0, ctx.stream>>>(
+      ptr_new, huge_rows, hcount, off, unsorted, keys, idx, rank);
+  SP_LAUNCH_CHECK();
+  radix_sort_pairs(ctx, keys, idx, k1, v1, ka, va, total, bits_for(n - 1), tmp);
+  const int gq = ctx.grid_for(ceil_div64(total, 256), 256, 4);
+  huge_rank_keys<<<gq, 256, 0, ctx.stream>>>(total, v1, rank, keys);
+  SP_LAUNCH_CHECK();
+  radix_sort_pairs(ctx, keys, v1, k1, idx, ka, va, total, bits_for(hcount - 1), tmp);
+  huge_scatter<<<gq, 256, 0, ctx.stream>>>(total, ptr_new, huge_rows, off, idx, rank, unsorted,
+                                           val_unsorted, ind_new, val_new);
+  SP_LAUNCH_CHECK();
+}
+
 template <int G>
 void launch_permute_g(Context &ctx, int32_t n, const int32_t *ptr_old, const int32_t *ind_old,
                       const float *val_old, const int32_t *new2old, const int32_t *col_map,
@@ -323,41 +432,9 @@ extern "C" void sporder_reorder(sporder_context_t h, int32_t n, int32_t nnz,
                         ctx.stream));
   ctx.sync();
   if (hcount > 0) {
-    // Rows longer than one workgroup's LDS: stable radix sort per row.
-    std::vector<int32_t> rows(hcount), bounds;
-    SP_HIP(hipMemcpy(rows.data(), huge_rows, sizeof(int32_t) * hcount,
-                     hipMemcpyDeviceToHost));
-    bounds.resize(2 * static_cast<size_t>(hcount));
-    int64_t max_len = 0;
-    for (int32_t i = 0; i < hcount; ++i) {
-      SP_HIP(hipMemcpy(&bounds[2 * i], d_ptr_new + rows[i], 2 * sizeof(int32_t),
-                       hipMemcpyDeviceToHost));
-      max_len = std::max<int64_t>(max_len, bounds[2 * i + 1] - bounds[2 * i]);
-    }
-    uint32_t *kalt = nullptr, *valt = nullptr, *zvals = nullptr;
-    int32_t *tmp = nullptr;
-    SP_HIP(hipMalloc(&kalt, max_len * 4));
-    SP_HIP(hipMalloc(&valt, max_len * 4));
-    SP_HIP(hipMalloc(&zvals, max_len * 4));
-    SP_HIP(hipMalloc(&tmp, radix_tmp_elems(max_len) * 4));
-    fill_u32(ctx, zvals, max_len, 0u);
-    uint32_t *vout = nullptr;
-    if (!with_vals) SP_HIP(hipMalloc(&vout, max_len * 4));
-    const int bits = bits_for(n - 1);
-    for (int32_t i = 0; i < hcount; ++i) {
-      int32_t s = bounds[2 * i], len = bounds[2 * i + 1] - s;
-      const uint32_t *vin = with_vals ? reinterpret_cast<const uint32_t *>(val_unsorted + s)
-                                      : zvals;
-      uint32_t *vo = with_vals ? reinterpret_cast<uint32_t *>(d_val_new + s) : vout;
-      radix_sort_pairs(ctx, reinterpret_cast<const uint32_t *>(unsorted + s), vin,
-                       reinterpret_cast<uint32_t *>(d_ind_new + s), vo, kalt, valt, len,
-                       bits, tmp);
-    }
-    ctx.sync();
-    SP_HIP(hipFree(kalt));
-    SP_HIP(hipFree(valt));
-    SP_HIP(hipFree(zvals));
-    SP_HIP(hipFree(tmp));
-    if (vout) SP_HIP(hipFree(vout));
+    sort_huge_rows(ctx, n, d_ptr_new, huge_rows, hcount, unsorted,
+                   with_vals ? val_unsorted : nullptr, d_ind_new,
+                   with_vals ? d_val_new : nullptr, list1, scan_tmp);
   }
+  ctx.sync();
 }

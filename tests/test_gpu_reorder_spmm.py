@@ -48,6 +48,19 @@ def hub_matrix(n=300_000, hub=250_000, seed=8):
     return ptr.astype(np.int32), ind.astype(np.int32), val
 
 
+def many_huge_matrix(n=60000, seed=9):
+    """40 rows of 4097..9000 entries (all sorted together past the LDS sort)
+    among rows of 0..10."""
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(0, 11, size=n)
+    lens[rng.choice(n, size=40, replace=False)] = rng.integers(4097, 9001, size=40)
+    ptr = np.zeros(n + 1, np.int64)
+    np.cumsum(lens, out=ptr[1:])
+    ind = np.concatenate([np.sort(rng.choice(n, size=L, replace=False)) for L in lens])
+    val = rng.standard_normal(ind.shape[0]).astype(np.float32)
+    return ptr.astype(np.int32), ind.astype(np.int32), val
+
+
 def mats():
     return {
         "C1": synth.config1(21),
@@ -55,6 +68,7 @@ def mats():
         "stencil16": synth.stencil7(16, 23),
         "longrows": long_row_matrix(),
         "hub": hub_matrix(),
+        "manyhuge": many_huge_matrix(),
     }
 
 
