@@ -4,7 +4,6 @@
 // links unchanged; calling one aborts with a diagnostic, the reference's
 // failure behaviour for invalid use (sporder/src/common/error_checking.h:55-61).
 //   sporder_hierarchical_matching   reference sporder.h:119-123 (hm/)
-//   sporder_count_pillars           reference sporder.h:276-279
 //   sporder_similarity_graph_exact  reference sporder.h:373-377
 #include "common.hpp"
 
@@ -17,11 +16,6 @@ void sporder_hierarchical_matching(sporder_context_t, int32_t, int32_t,
                                    const sporder_options_t *, int32_t *,
                                    sporder_hm_timing_t *, sporder_hm_stats_t *) {
   SP_EXPECT(false, "sporder_hierarchical_matching is not part of this build");
-}
-
-void sporder_count_pillars(sporder_context_t, int32_t, int32_t, const int32_t *,
-                           const int32_t *, int32_t, int32_t *) {
-  SP_EXPECT(false, "sporder_count_pillars is not part of this build yet");
 }
 
 void sporder_similarity_graph_exact(sporder_context_t, int32_t, int32_t,

@@ -7,8 +7,8 @@ torch tensors on a ROCm GPU (int32 CSR ``ptr``/``ind``); results come back
 as torch tensors on the same device.
 
 Provided: chunk_similarity_greedy (sporder-csg), chunk_greedy (sporder-cg),
-reorder, similarity_graph, bench_cusparse_spmm, plus spmm_csr and
-chunk_similarity_top_k (new).  hierarchical_matching, count_pillars and
+reorder, count_pillars, similarity_graph, bench_cusparse_spmm, plus spmm_csr
+and chunk_similarity_top_k (new).  hierarchical_matching and
 similarity_graph_exact exist for import compatibility and raise
 NotImplementedError.
 """
@@ -200,8 +200,23 @@ def chunk_greedy(ptr, ind, *, is_symmetric=False, k=0, oversampling=0.0, chunk_s
 
 
 def count_pillars(ptr, ind, height, *, ctx=None):
-    """Not part of this build yet (reference __init__.py:152-172)."""
-    return _count_pillars(ptr, ind, height)
+    """Count nonzero columns over consecutive row windows.
+
+    Rows are grouped into ceil(n / height) consecutive windows of ``height``
+    rows (the last may be shorter).  A pillar is a column holding at least one
+    nonzero inside a window; the total over all windows is the column-tile
+    count of a blocked SpMM with tile width 1, the quantity row reordering
+    tries to reduce.  Column indices need not be sorted or distinct.
+
+    Arguments:
+        ptr, ind: int32 GPU arrays, CSR row pointers (n+1) and columns (nnz)
+        height: row window height, >= 1
+        ctx: Context, or None for the shared default context
+
+    Returns the pillar total (int).  Reference:
+    sporder/python/sporder/__init__.py:152-172.
+    """
+    return _count_pillars(ptr, ind, height, ctx=ctx)
 
 
 def similarity_graph_exact(ptr, ind, *, is_symmetric=False, k=0, with_timing=False,

@@ -178,6 +178,22 @@ def chunk_greedy(ptr, ind, is_symmetric=False, k=0, oversampling=0.0, chunk_size
     return new_order, timing_info, stats_info
 
 
+def count_pillars(ptr, ind, height, ctx=None):
+    """Reference bindings.cpp:204-227."""
+    ptr = _gpu_in(ptr, torch.int32, "ptr")
+    ind = _gpu_in(ind, torch.int32, "ind")
+    if ptr.numel() < 2:
+        raise ValueError("ptr must have length n+1 (at least 2)")
+    if int(height) < 1:
+        raise ValueError("height must be >= 1")
+    n, nnz = _sizes(ptr, ind)
+    c = _resolve(ctx, ptr)
+    count = ctypes.c_int32()
+    c._lib.sporder_count_pillars(c.handle, n, nnz, _addr(ptr), _addr(ind), int(height),
+                                 ctypes.byref(count))
+    return int(count.value)
+
+
 def reorder(ptr, ind, val=None, new_order=None, symmetric=False, ctx=None):
     """Reference bindings.cpp:151-202."""
     ptr = _gpu_in(ptr, torch.int32, "ptr")
@@ -326,5 +342,4 @@ def _not_built(name):
 # Entry points the reference imports at package load (reference
 # sporder/python/sporder/__init__.py:3-13) that this build does not provide.
 hierarchical_matching = _not_built("hierarchical_matching")
-count_pillars = _not_built("count_pillars")
 similarity_graph_exact = _not_built("similarity_graph_exact")

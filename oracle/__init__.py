@@ -250,6 +250,51 @@ def chunk_greedy(ptr, ind, *, is_symmetric=False, k=0, oversampling=0.0, chunk_s
     return out
 
 
+def count_pillars(ptr, ind, height: int) -> int:
+    """Oracle of sporder_count_pillars (reference sporder/src/count_pillars.cu:11-85):
+    the number of distinct (row // height, column) pairs over all nonzeros.
+    Pinned by closed forms (height 1 with distinct columns per row gives nnz,
+    height >= n gives the number of distinct columns) and brute-force sets
+    (tests/test_oracle_quality.py)."""
+    ptr, ind = _i32(ptr), _i32(ind)
+    n = ptr.shape[0] - 1
+    if height < 1:
+        raise ValueError("height must be >= 1")
+    rows = np.repeat(np.arange(n, dtype=np.int64), np.diff(ptr))
+    keys = (rows // height) * np.int64(n) + ind.astype(np.int64)
+    return int(np.unique(keys).size)
+
+
+def quality_metrics(rows, cols, n: int, mu: int = 16, nu: int = 8) -> dict:
+    """Structural reordering-quality metrics of a pattern given as COO
+    (reference experiments/quality_metrics.py:36-57):
+      pillars   = distinct (row // mu, column) pairs;
+      tc_blocks = sum over row windows of ceil(pillars_in_window / nu);
+      bandwidth = max |i - j|;
+      profile   = sum over nonempty rows of max(0, i - min column);
+      log_gap   = mean over nonzeros of log2(gap + 1), gaps between consecutive
+                  sorted columns of a row, the first measured from the row index.
+    Pinned by closed forms on identity, band and dense-block patterns
+    (tests/test_oracle_quality.py)."""
+    rows = np.asarray(rows, np.int64)
+    cols = np.asarray(cols, np.int64)
+    order = np.lexsort((cols, rows))
+    r, c = rows[order], cols[order]
+    win = r // mu
+    uk = np.unique(win * n + c)
+    per_win = np.bincount(uk // n)
+    first = np.ones(r.size, dtype=bool)
+    first[1:] = r[1:] != r[:-1]
+    gaps = np.empty(r.size, dtype=np.int64)
+    gaps[1:] = c[1:] - c[:-1]
+    gaps[first] = np.abs(c[first] - r[first])
+    return {"pillars": int(uk.size),
+            "tc_blocks": int(np.sum((per_win + nu - 1) // nu)),
+            "bandwidth": int(np.max(np.abs(r - c))) if r.size else 0,
+            "profile": int(np.sum(np.maximum(0, r[first] - c[first]))),
+            "log_gap": float(np.log2(gaps + 1).sum() / r.size) if r.size else 0.0}
+
+
 def reorder(ptr, ind, new_order, val=None, symmetric=False):
     ptr, ind, new_order = _i32(ptr), _i32(ind), _i32(new_order)
     n = ptr.shape[0] - 1
@@ -301,6 +346,7 @@ __all__ = [
     "CsgStats", "build", "lib", "num_threads", "set_num_threads", "unpack_table",
     "pack_table", "csg_defaults", "csr2csc", "chunk_similarity_top_k", "sketch_stream",
     "greedy", "top_k_stats", "chunk_similarity_greedy", "chunk_greedy", "reorder", "spmm_csr",
+    "count_pillars", "quality_metrics",
 ]
 
 if os.environ.get("SPORDER_ORACLE_THREADS"):
