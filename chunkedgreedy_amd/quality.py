@@ -56,3 +56,39 @@ def structure_metrics(ptr, ind, new_order=None, *, mu: int = MU, nu: int = NU,
     log_gap = float(torch.log2(gaps.double() + 1.0).sum() / nnz)
     return {"pillars": pillars, "tc_blocks": tc_blocks, "bandwidth": bandwidth,
             "profile": profile, "log_gap": log_gap, "pillars_check": int(win_keys.numel())}
+
+
+def reorder_bench_metrics(ptr, ind, new_order=None, *, tc_h: int = 16, tc_w: int = 8,
+                          ctx=None) -> dict:
+    """The structure columns of the reorder-bench CSV for A or P A P^T
+    (spmatkit.py:1704-1717 and 1974-1995, 2037-2060):
+      bandwidth    = max over nonzeros of |i - j|
+      profile      = sum over nonempty rows of max_j |i - j|
+      tc_num       = sum over windows of tc_h rows of ceil(distinct columns / tc_w)
+      tc_fill_rate = nnz / (tc_num * tc_h * tc_w)."""
+    import torch
+
+    from chunkedgreedy_amd import sporder
+
+    if new_order is not None:
+        ptr, ind = sporder.reorder(ptr, ind, new_order, symmetric=True, ctx=ctx)
+    n = ptr.numel() - 1
+    nnz = ind.numel()
+    dev = ptr.device
+    out = {"tc_h": tc_h, "tc_w": tc_w}
+    if nnz == 0:
+        out.update(bandwidth=0, profile=0, tc_num=0, tc_fill_rate=float("nan"))
+        return out
+    deg = (ptr[1:] - ptr[:-1]).long()
+    rows = torch.repeat_interleave(torch.arange(n, device=dev), deg)
+    dist = (rows - ind.long()).abs()
+    row_max = torch.zeros(n, dtype=torch.int64, device=dev).scatter_reduce(
+        0, rows, dist, reduce="amax", include_self=True)
+    out["bandwidth"] = int(row_max.max())
+    out["profile"] = int(row_max.sum())
+    win_keys = torch.unique((rows // tc_h) * n + ind.long())
+    per_win = torch.bincount(win_keys // n)
+    tc_num = int(((per_win + tc_w - 1) // tc_w).sum())
+    out["tc_num"] = tc_num
+    out["tc_fill_rate"] = nnz / (tc_num * tc_h * tc_w) if tc_num else float("nan")
+    return out

@@ -295,6 +295,34 @@ def quality_metrics(rows, cols, n: int, mu: int = 16, nu: int = 8) -> dict:
             "log_gap": float(np.log2(gaps + 1).sum() / r.size) if r.size else 0.0}
 
 
+def reorder_bench_metrics(ptr, ind, tc_h: int = 16, tc_w: int = 8) -> dict:
+    """The structure columns of the reorder-bench CSV (reference
+    spmatkit/spmatkit.py:1704-1717 bandwidth/profile as the per-row maximum of
+    |i - j| (max and sum over nonempty rows), :1974-1995 windows of tc_h rows
+    and ceil(distinct columns / tc_w) tiles, :2052-2060 the fill rate).
+    Pinned by closed forms (tests/test_oracle_quality.py)."""
+    ptr, ind = _i32(ptr), _i32(ind)
+    n = ptr.shape[0] - 1
+    nnz = ind.shape[0]
+    out = {"tc_h": tc_h, "tc_w": tc_w}
+    if nnz == 0:
+        out.update(bandwidth=0, profile=0, tc_num=0, tc_fill_rate=float("nan"))
+        return out
+    rows = np.repeat(np.arange(n, dtype=np.int64), np.diff(ptr))
+    dist = np.abs(rows - ind.astype(np.int64))
+    row_max = np.zeros(n, np.int64)
+    np.maximum.at(row_max, rows, dist)
+    nonempty = np.diff(ptr) > 0
+    out["bandwidth"] = int(row_max.max())
+    out["profile"] = int(row_max[nonempty].sum())
+    uk = np.unique((rows // tc_h) * n + ind.astype(np.int64))
+    per_win = np.bincount(uk // n)
+    tc_num = int(np.sum((per_win + tc_w - 1) // tc_w))
+    out["tc_num"] = tc_num
+    out["tc_fill_rate"] = nnz / (tc_num * tc_h * tc_w) if tc_num else float("nan")
+    return out
+
+
 def reorder(ptr, ind, new_order, val=None, symmetric=False):
     ptr, ind, new_order = _i32(ptr), _i32(ind), _i32(new_order)
     n = ptr.shape[0] - 1
@@ -346,7 +374,7 @@ __all__ = [
     "CsgStats", "build", "lib", "num_threads", "set_num_threads", "unpack_table",
     "pack_table", "csg_defaults", "csr2csc", "chunk_similarity_top_k", "sketch_stream",
     "greedy", "top_k_stats", "chunk_similarity_greedy", "chunk_greedy", "reorder", "spmm_csr",
-    "count_pillars", "quality_metrics",
+    "count_pillars", "quality_metrics", "reorder_bench_metrics",
 ]
 
 if os.environ.get("SPORDER_ORACLE_THREADS"):

@@ -94,3 +94,35 @@ def test_spmm_plugin(sporder, name):
     assert np.abs(out.cpu().numpy() - ref).max() / np.abs(ref).max() < 1e-5
     assert ms > 0
     assert harness.time_run(m, prepared, B, warmup=2, iterations=3) > 0
+
+
+@pytest.mark.gpu
+def test_reorder_to_perm_npz_and_csv_row(sporder, tmp_path):
+    """The csg plugin's permutation flows into the reference formats: the
+    .perm.npz round trip, and a CSV row whose structure metrics (computed on
+    the GPU for P A P^T) equal the oracle's on scipy's A[p, :][:, p]."""
+    import csv
+
+    import torch
+
+    from chunkedgreedy_amd import formats, quality
+
+    ptr, ind, val = synth.config1(12)
+    a = sp.csr_matrix((val, ind, ptr), shape=(20_000, 20_000))
+    params = {"k": 0, "chunk_size": 0, "oversampling": 0, "auto_detect_symmetric": True}
+    res = harness.reorder(a, params)
+    path = formats.save_reorder_perm(tmp_path, "C1", "sporder-csg", params, res.row_perm)
+    perm = formats.load_reorder_perm(path, 20_000)
+    assert np.array_equal(perm, res.row_perm)
+    dptr = torch.from_numpy(ptr).cuda()
+    dind = torch.from_numpy(ind).cuda()
+    m = quality.reorder_bench_metrics(dptr, dind, torch.from_numpy(perm.astype(np.int32)).cuda())
+    b = a[perm, :][:, perm].tocsr()
+    b.sort_indices()
+    want = oracle.reorder_bench_metrics(b.indptr, b.indices)
+    assert {k: m[k] for k in want} == pytest.approx(want)
+    out = tmp_path / "reorder_bench.csv"
+    formats.write_result_row(out, formats.reorder_result_row("C1", "sporder-csg", params, res, m))
+    with out.open() as fh:
+        row = next(csv.DictReader(fh))
+    assert row["reorder_hash"] == "a609629886c6" and int(row["tc_num"]) == want["tc_num"]

@@ -61,3 +61,18 @@ def test_pillars_brute_force_with_duplicates(seed):
     for h in (1, 5, 16, 300):
         want = len({(r // h, int(c)) for r in range(n) for c in ind[ptr[r]:ptr[r + 1]]})
         assert oracle.count_pillars(ptr, ind, h) == want
+
+
+def test_reorder_bench_metrics_closed_forms():
+    n, hw = 64, 3
+    ptr, ind, _ = synth.band(n, hw)
+    m = oracle.reorder_bench_metrics(ptr, ind, tc_h=16, tc_w=8)
+    assert m["bandwidth"] == hw
+    # Row i reaches i+hw (or the last column) and i-hw (or column 0).
+    assert m["profile"] == sum(max(min(hw, i), min(hw, n - 1 - i)) for i in range(n))
+    # Window of 16 rows starting at a sees columns [a-hw, a+15+hw] clipped.
+    want_tc = sum(-(-(min(n, a + 16 + hw) - max(0, a - hw)) // 8) for a in range(0, n, 16))
+    assert m["tc_num"] == want_tc
+    assert m["tc_fill_rate"] == pytest.approx(ptr[-1] / (want_tc * 16 * 8))
+    empty = oracle.reorder_bench_metrics(np.zeros(5, np.int32), np.zeros(0, np.int32))
+    assert empty["tc_num"] == 0 and empty["bandwidth"] == 0
