@@ -174,12 +174,12 @@ __global__ void __launch_bounds__(kGreedyBlock)
   }
 }
 
-// Compact greedy: chunks of at most kGreedyCompactRows rows.  One thread per
-// row counts the row's valid entries that fall inside the chunk (the only ones
-// the chain can follow; all of them for a chunk-restricted table, a few for
-// the global one), the counts are scanned into per-row offsets and the
-// entries copied as (weight bits << 32 | local index) into LDS; then wave 0
-// runs the chain on LDS alone.  A slice with more than `entry_cap` in-chunk
+// Compact greedy: chunks of at most kGreedyCompactRows rows.  Four waves
+// count each row's valid entries that fall inside the chunk (the only ones the
+// chain can follow; all of them for a chunk-restricted table, a few for the
+// global one), the counts are scanned into per-row offsets and the entries
+// copied as (weight bits << 32 | local index) into LDS; then wave 0 runs the
+// chain on LDS alone.  A slice with more than `entry_cap` in-chunk
 // entries keeps the offsets in LDS and reads the rows from global memory.
 constexpr int kGreedyCompactRows = 4096;
 
@@ -213,25 +213,34 @@ __global__ void __launch_bounds__(kGreedyBlock)
   const uint64_t *slice = table + static_cast<size_t>(start) * k;
   const int64_t slice_len = static_cast<int64_t>(size) * k;
 
+  for (int32_t r = tid; r <= size; r += kGreedyBlock) s_off[r] = 0;
   for (int32_t w = tid; w < words; w += kGreedyBlock) s_bm[w] = 0u;
-  if (tid == 0) s_off[0] = 0;
+  __syncthreads();
   // Per-row count of valid entries inside the chunk (valid entries form a
-  // prefix of each row; only in-chunk entries can be followed).  With
-  // counters, the in-chunk weight is summed for the cut statistic.
+  // prefix of each row; only in-chunk entries can be followed), read as a
+  // coalesced sweep of the slice.  Rows that also hold out-of-chunk entries
+  // (global tables) are flagged in the bitmap, which the chain clears before
+  // it starts.  With counters, the in-chunk weight is summed for the cut
+  // statistic.
   double in_w = 0.0;
-  for (int32_t r = tid; r < size; r += kGreedyBlock) {
-    const uint64_t *row = slice + static_cast<size_t>(r) * k;
-    int32_t cnt = 0;
-    for (int32_t j = 0; j < k; ++j) {
-      const uint64_t v = row[j];
-      const int32_t c = wi_index(v);
-      if (c < 0) break;
-      if (c >= start && c < end) {
-        cnt += 1;
-        in_w += wi_weight(v);
+  for (int64_t e0 = static_cast<int64_t>(tid) * 4; e0 < slice_len;
+       e0 += static_cast<int64_t>(kGreedyBlock) * 4) {
+    uint64_t v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) v[u] = (e0 + u < slice_len) ? slice[e0 + u] : 0;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int32_t c = wi_index(v[u]);
+      if (e0 + u < slice_len && c >= 0) {
+        const int32_t r = static_cast<int32_t>((e0 + u) / k);
+        if (c >= start && c < end) {
+          atomicAdd(&s_off[r + 1], 1);
+          in_w += wi_weight(v[u]);
+        } else {
+          atomicOr(&s_bm[r >> 5], 1u << (r & 31));
+        }
       }
     }
-    s_off[r + 1] = cnt;
   }
   if (counters != nullptr) {
 #pragma unroll
@@ -255,19 +264,28 @@ __global__ void __launch_bounds__(kGreedyBlock)
   const int32_t total = s_total;
   const bool compact = total <= entry_cap;
   if (compact) {
-    for (int32_t r = tid; r < size; r += kGreedyBlock) {
-      const uint64_t *row = slice + static_cast<size_t>(r) * k;
-      int32_t at = s_off[r];
-      for (int32_t j = 0; j < k; ++j) {
-        const uint64_t v = row[j];
-        const int32_t c = wi_index(v);
-        if (c < 0) break;
-        if (c >= start && c < end) {
-          s_ent[at++] = (v & 0xFFFFFFFF00000000ull) | static_cast<uint32_t>(c - start);
+    // Entry j of row r lands at s_off[r] + (its rank among the row's in-chunk
+    // entries): j itself unless the row is flagged as mixed.
+    for (int64_t e = tid; e < slice_len; e += kGreedyBlock) {
+      const uint64_t v = slice[e];
+      const int32_t c = wi_index(v);
+      if (c >= start && c < end) {
+        const int32_t r = static_cast<int32_t>(e / k), j = static_cast<int32_t>(e % k);
+        int32_t rank = j;
+        if (s_bm[r >> 5] & (1u << (r & 31))) {
+          rank = 0;
+          const uint64_t *row = slice + static_cast<size_t>(r) * k;
+          for (int32_t t = 0; t < j; ++t) {
+            const int32_t ct = wi_index(row[t]);
+            rank += (ct >= start && ct < end);
+          }
         }
+        s_ent[s_off[r] + rank] = (v & 0xFFFFFFFF00000000ull) | static_cast<uint32_t>(c - start);
       }
     }
   }
+  __syncthreads();
+  for (int32_t w = tid; w < words; w += kGreedyBlock) s_bm[w] = 0u;
   __syncthreads();
   if (wave != 0) return;
 
