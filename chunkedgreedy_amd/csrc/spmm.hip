@@ -19,8 +19,8 @@
 //     start; each segment is such a chain from 0.0f, and
 //     C[i][j] = ((P_0 + P_1) + P_2) + ... left to right.
 // The segments of long rows are processed by many row groups of a second
-// launch (so one hub row does not serialise the whole SpMM); the group that
-// finishes a row's last segment adds the partials in the stated order.
+// launch (so one hub row does not serialise the whole SpMM), and a third
+// launch adds each long row's partials in the stated order.
 //
 // Merge-path: the nonzeros are cut into equal spans per wave (a row longer
 // than a span is split); each span's partial row sums are added into C with
@@ -38,17 +38,30 @@ constexpr int kSpmmDepth = 8; // B rows in flight per row group
 constexpr int kLongRow = SPORDER_SPMM_LONG_ROW;
 constexpr int kSegLen = SPORDER_SPMM_SEGMENT;
 
+
 // Long rows: descriptors appended by the row-split launch.
+// Rows past kLongRow nonzeros leave the row-split launch: each becomes nseg
+// segment units whose partials the fixup launch adds.
 struct LongRow {
   int32_t row;
-  int32_t base;  // first segment unit
+  int32_t base; // first unit (also its first partial row)
   int32_t nseg;
-  int32_t done;  // segments finished
+  int32_t pad;
 };
 struct LongCtl {
   int32_t rows;     // long rows registered
-  int32_t segments; // segment units allocated
+  int32_t segments; // units allocated
 };
+
+// Registers a row of `len` > kLongRow nonzeros (one lane per row).
+__device__ __forceinline__ void register_row(LongCtl *ctl, LongRow *longs, int32_t *owner,
+                                             int32_t row, int32_t len) {
+  const int32_t nseg = (len + kSegLen - 1) / kSegLen;
+  const int32_t id = atomicAdd(&ctl->rows, 1);
+  const int32_t base = atomicAdd(&ctl->segments, nseg);
+  longs[id] = LongRow{row, base, nseg, 0};
+  for (int32_t q = 0; q < nseg; ++q) owner[base + q] = id;
+}
 
 // A[s, e) x B on the group's float4 column slice col0 (col_ok false: lanes
 // past N).  Every lane of the wave calls it together; groups with different
@@ -134,13 +147,7 @@ __global__ void __launch_bounds__(kSpmmBlock)
   const int32_t e = row_ok ? ptr[row + 1] : 0;
   const bool is_long = longs != nullptr && e - s > kLongRow;
   if (is_long) {
-    if (gl == 0) {
-      const int32_t nseg = (e - s + kSegLen - 1) / kSegLen;
-      const int32_t id = atomicAdd(&ctl->rows, 1);
-      const int32_t base = atomicAdd(&ctl->segments, nseg);
-      longs[id] = LongRow{static_cast<int32_t>(row), base, nseg, 0};
-      for (int32_t q = 0; q < nseg; ++q) owner[base + q] = id;
-    }
+    if (gl == 0) register_row(ctl, longs, owner, static_cast<int32_t>(row), e - s);
     s = e; // the segment launch computes this row
   }
   for (int32_t col0 = gl * 4; col0 - gl * 4 < N; col0 += G * 4) {
@@ -150,17 +157,134 @@ __global__ void __launch_bounds__(kSpmmBlock)
   }
 }
 
+// Dynamic row-split for N <= 32 (one float4 column pass): a wave owns 64
+// consecutive rows and its 64/G row groups claim them in order, a group taking
+// the next unclaimed row as soon as its current one ends, so groups of one wave
+// do not wait for the longest row among them.  Each row is still one group's
+// fmaf chain in CSR order.  Row bounds come from one coalesced load of the
+// wave's 65 row pointers; rows longer than kLongRow are registered for the
+// segment launch as in spmm_rowsplit_v4.
+template <int G>
+__global__ void __launch_bounds__(kSpmmBlock)
+    spmm_rows_dyn(int32_t n, const int32_t *__restrict__ ptr, const int32_t *__restrict__ ind,
+                  const float *__restrict__ val, int32_t N, const float *__restrict__ B,
+                  float *__restrict__ C, LongCtl *ctl, LongRow *longs, int32_t *owner) {
+  constexpr int U = kSpmmDepth;
+  constexpr int RPW = kWave / G;
+  const int lane = lane_id();
+  const int sub = lane / G, gl = lane % G, gbase = sub * G;
+  const int64_t wave = static_cast<int64_t>(blockIdx.x) * kSpmmWaves + threadIdx.x / kWave;
+  const int64_t r0 = wave * kWave;
+  if (r0 >= n) return;
+  const int32_t nrows = static_cast<int32_t>(n - r0 < kWave ? n - r0 : kWave);
+  // Lane i holds ptr[r0 + i] (i <= nrows); ptr[r0 + 64] separately.
+  const int32_t pl = ptr[r0 + (lane < nrows ? lane : nrows)];
+  const int32_t p_last = ptr[r0 + nrows];
+  const int col0 = gl * 4;
+  const bool col_ok = col0 < N;
+
+  int32_t row = sub < nrows ? sub : -1; // local row of this group, -1 idle
+  int32_t next = RPW;                   // wave-uniform: next unclaimed local row
+  int32_t p = 0, e = 0;
+  bool is_long = false;
+  float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  // A claimed row longer than kLongRow goes to the segment launch and counts
+  // as finished at once.
+  auto take_long = [&]() {
+    if (row >= 0 && e - p > kLongRow) {
+      if (gl == 0) register_row(ctl, longs, owner, static_cast<int32_t>(r0 + row), e - p);
+      is_long = true;
+      p = e;
+    }
+  };
+  // Every lane takes part in each shuffle (a source lane that is inactive for
+  // a ds_bpermute reads as 0); the selects come after.
+  {
+    const int32_t a = __shfl(pl, row >= 0 ? row : 0, kWave);
+    const int32_t bi = row >= 0 ? row + 1 : 0;
+    const int32_t bs = __shfl(pl, bi < kWave ? bi : kWave - 1, kWave);
+    p = row >= 0 ? a : 0;
+    e = row >= 0 ? (bi < kWave ? bs : p_last) : 0;
+    take_long();
+  }
+  while (true) {
+    // Retire finished rows and claim new ones until every group has work or
+    // the wave's rows are used up.
+    while (true) {
+      const bool fin = row >= 0 && p >= e;
+      if (fin && !is_long && col_ok) store_nt(C + (r0 + row) * N + col0, acc);
+      const uint64_t fmask = ballot(fin && gl == 0);
+      if (fmask == 0) break;
+      const int32_t rank = __popcll(fmask & ((1ull << gbase) - 1ull));
+      const int32_t cand = next + rank;
+      const int32_t ci = cand < nrows ? cand : 0;
+      const int32_t a = __shfl(pl, ci, kWave);
+      const int32_t bi = ci + 1;
+      const int32_t bs = __shfl(pl, bi < kWave ? bi : kWave - 1, kWave);
+      const int32_t b = bi < kWave ? bs : p_last;
+      if (fin) {
+        row = cand < nrows ? cand : -1;
+        p = row >= 0 ? a : 0;
+        e = row >= 0 ? b : 0;
+        is_long = false;
+        acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        take_long();
+      }
+      next += __popcll(fmask);
+    }
+    if (ballot(row >= 0) == 0) break;
+    // One step: up to G nonzeros per group, U B rows in flight.
+    const int32_t rem = row >= 0 ? e - p : 0;
+    int32_t my_c = 0;
+    float my_v = 0.0f;
+    if (gl < rem) {
+      my_c = __builtin_nontemporal_load(ind + p + gl);
+      my_v = __builtin_nontemporal_load(val + p + gl);
+    }
+    const int32_t cnt = rem < G ? rem : G;
+    const int32_t cmax = static_cast<int32_t>(wave_max_u32(static_cast<uint32_t>(cnt)));
+    for (int32_t t = 0; t < cmax; t += U) {
+      int32_t c[U];
+      float v[U];
+      float4 bv[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        c[u] = __shfl(my_c, gbase + ((t + u) & (G - 1)), kWave);
+        v[u] = __shfl(my_v, gbase + ((t + u) & (G - 1)), kWave);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (t + u < cnt && col_ok) {
+          bv[u] = *reinterpret_cast<const float4 *>(B + static_cast<int64_t>(c[u]) * N + col0);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (t + u < cnt && col_ok) {
+          acc.x = fmaf(v[u], bv[u].x, acc.x);
+          acc.y = fmaf(v[u], bv[u].y, acc.y);
+          acc.z = fmaf(v[u], bv[u].z, acc.z);
+          acc.w = fmaf(v[u], bv[u].w, acc.w);
+        }
+      }
+    }
+    if (row >= 0) p += cnt;
+  }
+}
+
 // Segment units of the long rows: each row group computes one segment's
-// partial into `part` (unit-major, N floats per unit); the group that brings
-// a row's completion count to nseg adds the row's partials left to right into
-// C.  Grid-stride over the units registered by the row-split launch.
+// partial into `part` (unit-major, N floats per unit).  Grid-stride over the
+// units registered by the row-split launch.  The partials are added by the
+// next launch: handing them over inside this one would need a device-scope
+// release/acquire per unit, which on MI355X writes back and invalidates the
+// XCD's L2 and so evicts every other wave's B rows.
 template <int G>
 __global__ void __launch_bounds__(kSpmmBlock)
     spmm_long_segments(const int32_t *__restrict__ ptr, const int32_t *__restrict__ ind,
                        const float *__restrict__ val, int32_t N,
-                       const float *__restrict__ B, float *__restrict__ C,
-                       const LongCtl *__restrict__ ctl, LongRow *longs,
-                       const int32_t *__restrict__ owner, float *part) {
+                       const float *__restrict__ B, const LongCtl *__restrict__ ctl,
+                       const LongRow *__restrict__ longs, const int32_t *__restrict__ owner,
+                       float *__restrict__ part) {
   constexpr int kRowsPerWave = kWave / G;
   const int lane = lane_id();
   const int sub = lane / G, gl = lane % G, gbase = sub * G;
@@ -170,10 +294,9 @@ __global__ void __launch_bounds__(kSpmmBlock)
   for (int64_t ub = wave0 * kRowsPerWave; ub < units; ub += nwaves * kRowsPerWave) {
     const int64_t u = ub + sub;
     const bool ok = u < units;
-    LongRow lr{0, 0, 1, 0};
     int32_t s = 0, e = 0;
     if (ok) {
-      lr = longs[owner[u]];
+      const LongRow lr = longs[owner[u]];
       const int32_t rs = ptr[lr.row], re = ptr[lr.row + 1];
       s = rs + static_cast<int32_t>(u - lr.base) * kSegLen;
       e = s + kSegLen < re ? s + kSegLen : re;
@@ -183,40 +306,48 @@ __global__ void __launch_bounds__(kSpmmBlock)
       const float4 acc = group_dot<G>(s, e, ind, val, N, col0, col_ok, B, gl, gbase);
       if (ok && col_ok) *reinterpret_cast<float4 *>(part + u * N + col0) = acc;
     }
-    // Publish the partial, then count it; the last segment of a row sums.
-    __threadfence();
-    int32_t prev = 0;
-    if (ok && gl == 0) prev = atomicAdd(&longs[owner[u]].done, 1);
-    prev = __shfl(prev, gbase, kWave);
-    const bool last = ok && prev == lr.nseg - 1;
-    if (last) {
-      __threadfence();
-      const float *p0 = part + static_cast<int64_t>(lr.base) * N;
-      for (int32_t col0 = gl * 4; col0 < N; col0 += G * 4) {
-        float4 sum = *reinterpret_cast<const float4 *>(p0 + col0);
-        int32_t q = 1;
-        for (; q + 4 <= lr.nseg; q += 4) {
-          float4 t[4];
+  }
+}
+
+// C[row] = ((P_0 + P_1) + P_2) + ... for each long row, one row group per row,
+// eight partial rows in flight.
+template <int G>
+__global__ void __launch_bounds__(kSpmmBlock)
+    spmm_long_fixup(int32_t N, float *__restrict__ C, const LongCtl *__restrict__ ctl,
+                    const LongRow *__restrict__ longs, const float *__restrict__ part) {
+  constexpr int kRowsPerWave = kWave / G;
+  const int lane = lane_id();
+  const int sub = lane / G, gl = lane % G;
+  const int64_t wave0 = static_cast<int64_t>(blockIdx.x) * kSpmmWaves + threadIdx.x / kWave;
+  const int64_t nwaves = static_cast<int64_t>(gridDim.x) * kSpmmWaves;
+  const int32_t rows = ctl->rows;
+  for (int64_t t = wave0 * kRowsPerWave + sub; t < rows; t += nwaves * kRowsPerWave) {
+    const LongRow lr = longs[t];
+    const float *p0 = part + static_cast<int64_t>(lr.base) * N;
+    for (int32_t col0 = gl * 4; col0 < N; col0 += G * 4) {
+      float4 sum = *reinterpret_cast<const float4 *>(p0 + col0);
+      int32_t q = 1;
+      for (; q + 8 <= lr.nseg; q += 8) {
+        float4 v[8];
 #pragma unroll
-          for (int i = 0; i < 4; ++i)
-            t[i] = *reinterpret_cast<const float4 *>(p0 + static_cast<int64_t>(q + i) * N + col0);
+        for (int i = 0; i < 8; ++i)
+          v[i] = *reinterpret_cast<const float4 *>(p0 + static_cast<int64_t>(q + i) * N + col0);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            sum.x = sum.x + t[i].x;
-            sum.y = sum.y + t[i].y;
-            sum.z = sum.z + t[i].z;
-            sum.w = sum.w + t[i].w;
-          }
+        for (int i = 0; i < 8; ++i) {
+          sum.x = sum.x + v[i].x;
+          sum.y = sum.y + v[i].y;
+          sum.z = sum.z + v[i].z;
+          sum.w = sum.w + v[i].w;
         }
-        for (; q < lr.nseg; ++q) {
-          const float4 t = *reinterpret_cast<const float4 *>(p0 + static_cast<int64_t>(q) * N + col0);
-          sum.x = sum.x + t.x;
-          sum.y = sum.y + t.y;
-          sum.z = sum.z + t.z;
-          sum.w = sum.w + t.w;
-        }
-        store_nt(C + static_cast<int64_t>(lr.row) * N + col0, sum);
       }
+      for (; q < lr.nseg; ++q) {
+        const float4 v = *reinterpret_cast<const float4 *>(p0 + static_cast<int64_t>(q) * N + col0);
+        sum.x = sum.x + v.x;
+        sum.y = sum.y + v.y;
+        sum.z = sum.z + v.z;
+        sum.w = sum.w + v.w;
+      }
+      store_nt(C + static_cast<int64_t>(lr.row) * N + col0, sum);
     }
   }
 }
@@ -374,20 +505,42 @@ SpmmLongWs take_long_ws(Context &ctx, int32_t nnz, int32_t N) {
   return w;
 }
 
+// SPORDER_SPMM_STATIC_ROWS=1 selects the fixed row-per-group kernel for every
+// width (both compute the same stated order; the switch exists for A/B timing).
+bool static_rows() {
+  static const bool on = [] {
+    const char *v = std::getenv("SPORDER_SPMM_STATIC_ROWS");
+    return v != nullptr && v[0] == '1';
+  }();
+  return on;
+}
+
 template <int G>
 void launch_rowsplit_g(Context &ctx, int32_t n, int32_t nnz, const int32_t *ptr,
                        const int32_t *ind, const float *val, int32_t N, const float *B,
                        float *C, const SpmmLongWs &w) {
   constexpr int rpw = kWave / G;
-  const int64_t blocks = ceil_div64(ceil_div64(n, rpw), kSpmmWaves);
   fill_u32(ctx, w.ctl, sizeof(LongCtl) / 4, 0u);
-  spmm_rowsplit_v4<G><<<dim3(static_cast<unsigned>(blocks)), kSpmmBlock, 0, ctx.stream>>>(
-      n, ptr, ind, val, N, B, C, w.ctl, w.longs, w.owner);
+  // Narrow widths (G <= 8 lanes per row, 8+ rows per wave) lose most to
+  // row-length imbalance inside a wave: claim rows dynamically there.  With
+  // wider rows the fixed assignment keeps more waves in flight.
+  if (G <= 8 && N <= 4 * G && !static_rows()) {
+    const int64_t blocks = ceil_div64(ceil_div64(n, kWave), kSpmmWaves);
+    spmm_rows_dyn<G><<<dim3(static_cast<unsigned>(blocks)), kSpmmBlock, 0, ctx.stream>>>(
+        n, ptr, ind, val, N, B, C, w.ctl, w.longs, w.owner);
+  } else {
+    const int64_t blocks = ceil_div64(ceil_div64(n, rpw), kSpmmWaves);
+    spmm_rowsplit_v4<G><<<dim3(static_cast<unsigned>(blocks)), kSpmmBlock, 0, ctx.stream>>>(
+        n, ptr, ind, val, N, B, C, w.ctl, w.longs, w.owner);
+  }
   SP_LAUNCH_CHECK();
   // Persistent grid over the registered segment units (none: exits at once).
   const int g = ctx.grid_for(ceil_div64(max_segments(nnz), rpw * kSpmmWaves), kSpmmBlock, 2);
-  spmm_long_segments<G><<<g, kSpmmBlock, 0, ctx.stream>>>(ptr, ind, val, N, B, C, w.ctl,
+  spmm_long_segments<G><<<g, kSpmmBlock, 0, ctx.stream>>>(ptr, ind, val, N, B, w.ctl,
                                                             w.longs, w.owner, w.part);
+  SP_LAUNCH_CHECK();
+  const int gf = ctx.grid_for(ceil_div64(max_long_rows(nnz), rpw * kSpmmWaves), kSpmmBlock, 2);
+  spmm_long_fixup<G><<<gf, kSpmmBlock, 0, ctx.stream>>>(N, C, w.ctl, w.longs, w.part);
   SP_LAUNCH_CHECK();
 }
 
