@@ -16,13 +16,16 @@
 //      for small buckets, one wave per bucket (bitonic network in LDS) for
 //      large ones.  A column's keys are now one run, rows ascending;
 //   3. a row whose columns all occur once in the chunk has no candidates and
-//      gets the all-zero table row at once;
-//   4. the other rows (one wave each) binary-search each column's run inside
-//      its bucket and feed the run's rows, ascending, to the wave64 sketch.
+//      gets the all-zero table row;
+//   3b. the rows are counting-sorted by floor(log2(row size)), largest
+//      first, rows without candidates last;
+//   4. waves claim rows in that order; a row with candidates binary-searches
+//      each column's run inside its bucket and feeds the run's rows,
+//      ascending, to the wave64 sketch.
 //
 // The stream, and therefore the table, is identical to the reference's.
-// Two LDS tiers: up to 16384 nonzeros and 2048 rows per chunk (~78 KiB, two
-// workgroups per CU) and up to 32768 nonzeros and 4096 rows (~156 KiB).
+// Two LDS tiers: up to 16384 nonzeros and 1024 rows per chunk (~74 KiB, two
+// workgroups per CU) and up to 32768 nonzeros and 4096 rows (~157 KiB).
 // Larger chunks go to an overflow list for the global-CSC kernel.  Requires
 // ceil(log2 n) + ceil(log2 C) <= 32 (checked by the host).
 #include "common.hpp"
@@ -39,6 +42,10 @@ constexpr int kLocalThreads = 1024;
 constexpr int kLocalWaves = kLocalThreads / kWave;
 // Buckets up to this size are sorted by one thread.
 constexpr int kSmallBucket = 48;
+// Row classes of step 3b: clz(row size) in [0, 31] for rows with candidates,
+// kClasses for the others.
+constexpr int kClasses = 32;
+constexpr int kRowsPerThread = kLocalRowCap / kLocalThreads;
 
 __device__ __forceinline__ uint32_t bucket_of(uint32_t col, int nb_log2) {
   // Fibonacci hashing (Knuth, TAOCP vol. 3, 6.4): high bits of col * 2^32/phi.
@@ -87,7 +94,11 @@ __global__ void __launch_bounds__(kLocalThreads)
   __shared__ uint32_t s_keys[KEYCAP];
   __shared__ int32_t s_bend[NB];      // after the scatter: end of bucket b
   __shared__ int32_t s_size[ROWCAP];
-  __shared__ uint8_t s_multi[ROWCAP];
+  // Step 3: per-row "has a candidate" flags; from step 3b on: the chunk's
+  // rows in processing order.
+  __shared__ uint16_t s_order[ROWCAP];
+  __shared__ int32_t s_class[kClasses + 1]; // counts, then cursors, per class
+  __shared__ int32_t s_next_row;            // next entry of s_order to claim
 
   const int tid = threadIdx.x;
   const int lane = lane_id();
@@ -110,9 +121,11 @@ __global__ void __launch_bounds__(kLocalThreads)
 
     // 1. Bucket counts (coalesced column reads) and row sizes.
     for (int32_t b = tid; b < NB; b += kLocalThreads) s_bend[b] = 0;
+    if (tid <= kClasses) s_class[tid] = 0;
+    if (tid == 0) s_next_row = 0;
     for (int32_t r = tid; r < rows; r += kLocalThreads) {
       s_size[r] = row_ptr[cs + r + 1] - row_ptr[cs + r];
-      s_multi[r] = 0;
+      s_order[r] = 0;
     }
     __syncthreads();
     for (int32_t i = tid; i < E; i += kLocalThreads) {
@@ -172,17 +185,57 @@ __global__ void __launch_bounds__(kLocalThreads)
       const uint32_t c = key >> lb;
       const bool multi = (i > 0 && (s_keys[i - 1] >> lb) == c) ||
                          (i + 1 < E && (s_keys[i + 1] >> lb) == c);
-      if (multi) s_multi[key & rmask] = 1;
+      if (multi) s_order[key & rmask] = 1;
     }
     __syncthreads();
 
-    // 4. Sketch, one wave per row.
+    // 3b. Processing order: rows with candidates by floor(log2(row size)),
+    //     largest first (a longest-first schedule with the row size standing
+    //     in for the stream length), then the rows without candidates.  A
+    //     counting sort; the order inside a class does not matter, since each
+    //     row's table row depends on that row alone.
+    int32_t my_class[kRowsPerThread];
+#pragma unroll
+    for (int u = 0; u < kRowsPerThread; ++u) {
+      const int32_t r = tid + u * kLocalThreads;
+      my_class[u] = -1;
+      if (r < rows) {
+        const int32_t sz = s_size[r];
+        my_class[u] = (s_order[r] != 0 && sz > 0) ? __clz(sz) : kClasses;
+        atomicAdd(&s_class[my_class[u]], 1);
+      }
+    }
+    __syncthreads();
+    if (wave == 0) {
+      const int32_t v = lane <= kClasses ? s_class[lane] : 0;
+      const int32_t incl = wave_incl_scan(v);
+      if (lane <= kClasses) s_class[lane] = incl - v;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < kRowsPerThread; ++u) {
+      if (my_class[u] >= 0) {
+        const int32_t r = tid + u * kLocalThreads;
+        s_order[atomicAdd(&s_class[my_class[u]], 1)] = static_cast<uint16_t>(r);
+      }
+    }
+    __syncthreads();
+
+    // 4. Sketch, one wave per row.  Waves claim rows from a shared counter
+    //    in the order of step 3b: stream lengths vary by orders of magnitude
+    //    on skewed graphs, and a fixed row-to-wave assignment would leave the
+    //    workgroup waiting on its most loaded wave.
     WaveSketch<CELLS> store;
-    for (int32_t r = wave; r < rows; r += kLocalWaves) {
+    for (;;) {
+      int32_t claim = 0;
+      if (lane == 0) claim = atomicAdd(&s_next_row, 1);
+      const int32_t idx = readlane(claim, 0);
+      if (idx >= rows) break;
+      const int32_t r = s_order[idx];
       const int32_t row = cs + r;
       uint64_t *out = table + static_cast<size_t>(row) * k;
       const int32_t row_size = s_size[r];
-      if (row_size == 0 || s_multi[r] == 0) {
+      if (idx >= s_class[kClasses - 1]) { // no candidates (class kClasses)
         for (int32_t j = lane; j < k; j += kWave) out[j] = 0;
         continue;
       }
@@ -240,8 +293,8 @@ __global__ void __launch_bounds__(kLocalThreads)
 }
 
 // Tier parameters: (key capacity, row capacity, log2 buckets).
-constexpr int kT1Keys = 16384, kT1Rows = 2048, kT1Nb = 10;
-constexpr int kT2Keys = 32768, kT2Rows = 4096, kT2Nb = 11;
+constexpr int kT1Keys = 16384, kT1Rows = 1024, kT1Nb = 10;
+constexpr int kT2Keys = 32768, kT2Rows = 4096, kT2Nb = 10;
 
 template <int CELLS, int KEYCAP, int ROWCAP, int NB_LOG2>
 void launch_tier(Context &ctx, int32_t n, int32_t k, int32_t chunk_size, int32_t lb,
