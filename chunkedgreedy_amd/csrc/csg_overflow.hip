@@ -222,16 +222,22 @@ __global__ void __launch_bounds__(kOvfBlock)
                       const int32_t *__restrict__ row_ptr, const int2 *__restrict__ runs,
                       const int2 *__restrict__ pairs, uint64_t *__restrict__ table,
                       const int32_t *__restrict__ list,
-                      const int32_t *__restrict__ list_count) {
+                      const int32_t *__restrict__ list_count, uint32_t *__restrict__ claim) {
   __shared__ RunLookup s_lookup[kOvfWaves];
   const int lane = lane_id();
   RunLookup *lk = &s_lookup[threadIdx.x / kWave];
-  const int64_t wave0 = static_cast<int64_t>(blockIdx.x) * kOvfWaves + threadIdx.x / kWave;
-  const int64_t nwaves = static_cast<int64_t>(gridDim.x) * kOvfWaves;
+  // work < 2^32: list_len * chunk_size <= n + chunk_size - 1.
   const int64_t work = list_len(list, list_count, ceil_div64(n, chunk_size)) * chunk_size;
   WaveSketch<CELLS> store;
 
-  for (int64_t w = wave0; w < work; w += nwaves) {
+  // Waves claim rows one at a time from a device-wide counter (zeroed by the
+  // host before the launch): a few rows stream millions of items, and a
+  // fixed assignment would give one wave several of them.
+  for (;;) {
+    uint32_t claimed = 0;
+    if (lane == 0) claimed = atomicAdd(claim, 1u);
+    const int64_t w = static_cast<uint32_t>(readlane(static_cast<int32_t>(claimed), 0));
+    if (w >= work) break;
     int64_t row64 = w;
     if (list) row64 = static_cast<int64_t>(list[w / chunk_size]) * chunk_size + (w % chunk_size);
     if (row64 >= n) continue;
@@ -272,10 +278,13 @@ __global__ void __launch_bounds__(kOvfBlock)
 template <int CELLS>
 void launch_ovf_sketch(Context &ctx, int32_t n, int32_t k, int32_t chunk_size,
                        const int32_t *d_ptr, const int2 *runs, const int2 *pairs,
-                       uint64_t *d_table, const int32_t *list, const int32_t *list_count) {
+                       uint64_t *d_table, const int32_t *list, const int32_t *list_count,
+                       uint32_t *claim) {
   const int g = ctx.grid_for(ceil_div64(n, kOvfWaves), kOvfBlock, 4);
+  fill_u32(ctx, claim, 1, 0u);
   ovf_sketch_kernel<CELLS><<<g, kOvfBlock, 0, ctx.stream>>>(n, k, chunk_size, d_ptr, runs,
-                                                            pairs, d_table, list, list_count);
+                                                            pairs, d_table, list, list_count,
+                                                            claim);
   SP_LAUNCH_CHECK();
 }
 
@@ -283,7 +292,8 @@ void launch_ovf_sketch(Context &ctx, int32_t n, int32_t k, int32_t chunk_size,
 
 size_t chunk_sketch_ws_bytes(int32_t n, int32_t nnz, int32_t chunk_size) {
   return 2 * ws_bytes<int2>(static_cast<size_t>(nnz)) +
-         ws_bytes<int32_t>(static_cast<size_t>(ceil_div64(n, chunk_size)) + 1);
+         ws_bytes<int32_t>(static_cast<size_t>(ceil_div64(n, chunk_size)) + 1) +
+         ws_bytes<uint32_t>(1);
 }
 
 void chunk_sketch_top_k(Context &ctx, int32_t n, int32_t nnz, int32_t k, int32_t chunk_size,
@@ -298,6 +308,7 @@ void chunk_sketch_top_k(Context &ctx, int32_t n, int32_t nnz, int32_t k, int32_t
   int2 *runs = ctx.take<int2>(static_cast<size_t>(nnz));
   int2 *pairs = ctx.take<int2>(static_cast<size_t>(nnz));
   int32_t *task_off = ctx.take<int32_t>(static_cast<size_t>(chunks) + 1);
+  uint32_t *claim = ctx.take<uint32_t>(1);
 
   ovf_plan_kernel<<<1, kPlanBlock, 0, ctx.stream>>>(n, chunk_size, d_ptr, d_chunks,
                                                     d_chunk_count, task_off);
@@ -316,7 +327,7 @@ void chunk_sketch_top_k(Context &ctx, int32_t n, int32_t nnz, int32_t k, int32_t
 #define SP_CASE(C)                                                                       \
   case C:                                                                                \
     launch_ovf_sketch<C>(ctx, n, k, chunk_size, d_ptr, runs, pairs, d_table, d_chunks,   \
-                         d_chunk_count);                                                 \
+                         d_chunk_count, claim);                                          \
     break;
     SP_CASE(1) SP_CASE(2) SP_CASE(3) SP_CASE(4) SP_CASE(5) SP_CASE(6)
     SP_CASE(7) SP_CASE(8) SP_CASE(9) SP_CASE(10) SP_CASE(11) SP_CASE(12)
