@@ -379,11 +379,15 @@ __global__ void __launch_bounds__(kGreedyBlock)
 
 // ---- table statistics -------------------------------------------------------
 
-// One lane per row; each wave reads its 64 rows' entries as a coalesced
-// column sweep (entry j of 64 consecutive rows per step).
+// One lane per row.  The row's entries are loaded eight at a time with no
+// data-dependent branch between the loads (all k entries of a row exist), so
+// the loads of a batch are in flight together; the count and the float sum
+// then stop at the first empty entry, as the reference's loop does.  Block
+// totals are combined in LDS and added with one atomic per block.
 __global__ void __launch_bounds__(256)
     top_k_stats_kernel(int32_t n, int32_t k, const uint64_t *__restrict__ table,
                        TopKTotals *totals) {
+  constexpr int kBatch = 8;
   unsigned long long deg_sum = 0;
   double w_sum = 0.0;
   int32_t zeros = 0;
@@ -392,11 +396,19 @@ __global__ void __launch_bounds__(256)
     const uint64_t *r = table + static_cast<size_t>(row) * k;
     int32_t degree = 0;
     float rw = 0.0f;
-    for (int32_t j = 0; j < k; ++j) {
-      uint64_t e = r[j];
-      if (wi_index(e) == -1) break;
-      degree += 1;
-      rw += wi_weight(e);
+    bool open = true;
+    for (int32_t j0 = 0; j0 < k && open; j0 += kBatch) {
+      uint64_t e[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) e[u] = j0 + u < k ? r[j0 + u] : 0ull;
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        open = open && j0 + u < k && wi_index(e[u]) != -1;
+        if (open) {
+          degree += 1;
+          rw += wi_weight(e[u]);
+        }
+      }
     }
     deg_sum += degree;
     w_sum += rw;
@@ -408,7 +420,20 @@ __global__ void __launch_bounds__(256)
     w_sum += __shfl_xor(w_sum, off, kWave);
     zeros += __shfl_xor(zeros, off, kWave);
   }
+  __shared__ unsigned long long s_deg[4];
+  __shared__ double s_w[4];
+  __shared__ int32_t s_zero[4];
+  const int wave = threadIdx.x / kWave;
   if (lane_id() == 0) {
+    s_deg[wave] = deg_sum;
+    s_w[wave] = w_sum;
+    s_zero[wave] = zeros;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    deg_sum = s_deg[0] + s_deg[1] + s_deg[2] + s_deg[3];
+    w_sum = ((s_w[0] + s_w[1]) + s_w[2]) + s_w[3];
+    zeros = s_zero[0] + s_zero[1] + s_zero[2] + s_zero[3];
     if (deg_sum > 0) {
       atomicAdd(&totals->total_degree, deg_sum);
       atomicAdd(&totals->total_weight, w_sum);
