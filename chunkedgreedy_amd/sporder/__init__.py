@@ -151,9 +151,11 @@ def chunk_similarity_top_k(ptr, ind, *, k, oversampling, chunk_size, is_symmetri
 def spmm_csr(ptr, ind, val, B, *, out=None, algo="row_split", ctx=None):
     """(new) C = A @ B for CSR A (values ``val``) and row-major dense B.
 
-    algo "row_split" accumulates each output in CSR order with fmaf
-    (bit-reproducible); "merge_path" balances nonzeros across waves for skewed
-    rows.  Returns (C, kernel_ms)."""
+    algo "row_split" follows the stated order of include/sporder.h: a row of
+    at most 512 nonzeros is one fmaf chain in CSR order, a longer row is summed
+    in 512-nonzero segments added left to right (bit-reproducible);
+    "merge_path" splits the nonzeros evenly across waves and adds the partial
+    sums of cut rows with atomics.  Returns (C, kernel_ms)."""
     return _spmm_csr(ptr, ind, val, B, out=out, algo=algo, ctx=ctx)
 
 

@@ -1,0 +1,135 @@
+"""Measure the path on the five synthetic configurations (one GPU).
+
+For each configuration: the csg reorder (``chunk_similarity_greedy``, warmup,
+then a 1 GiB cache flush before each timed call, median wall of ``--repeats``
+calls with its stage spans and stats), the permutation apply P A P^T with
+values, and the CSR SpMM on the original and on the reordered matrix at the
+configuration's widths (warmup 5, median of 20 launch times, B = randn seed
+42, the same B for both matrices).  Prints one JSON record per configuration.
+
+Algorithmic bytes of an SpMM launch: 4(n+1) + 8 nnz + 8 n N (A once, B once,
+C once).
+
+Usage:  python -m chunkedgreedy_amd.sweep [--cfg C1,C2,C3,C4,C5] [--no-spmm]
+        [--algos row_split,merge_path] [--cg]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import statistics
+import sys
+import time
+
+import numpy as np
+
+WIDTHS = {"C1": [32], "C2": [32, 128], "C3": [32, 64, 256], "C4": [16, 32, 64, 128, 256],
+          "C5": [128]}
+
+
+def spmm_bytes(n: int, nnz: int, N: int) -> int:
+    return 4 * (n + 1) + 8 * nnz + 8 * n * N
+
+
+def _spmm_ms(sporder, ctx, ptr, ind, val, B, algo, iters=20):
+    import torch
+
+    out = torch.empty(B.shape, dtype=torch.float32, device=B.device)
+    for _ in range(5):
+        sporder.spmm_csr(ptr, ind, val, B, out=out, algo=algo, ctx=ctx)
+    return statistics.median(
+        sporder.spmm_csr(ptr, ind, val, B, out=out, algo=algo, ctx=ctx)[1] for _ in range(iters))
+
+
+def measure(name: str, *, spmm=True, algos=("row_split",), repeats=3, cg=False) -> dict:
+    import torch
+
+    from chunkedgreedy_amd import sporder, synth
+
+    gens = {"C1": synth.config1, "C2": synth.config2, "C3": synth.config3,
+            "C4": synth.config4, "C5": synth.config5}
+    dev = torch.device("cuda:0")
+    ctx = sporder.Context()
+    t0 = time.time()
+    ptr_h, ind_h, val_h = gens[name]()
+    n, nnz = ptr_h.shape[0] - 1, ind_h.shape[0]
+    sym = synth.is_pattern_symmetric(ptr_h, ind_h)
+    print(f"[{name}] generated n={n} nnz={nnz} symmetric={sym} in {time.time() - t0:.1f}s",
+          file=sys.stderr, flush=True)
+    ptr, ind, val = (torch.from_numpy(a).to(dev) for a in (ptr_h, ind_h, val_h))
+    rec = {"config": name, "n": n, "nnz": nnz, "symmetric": sym,
+           "max_row": int(np.diff(ptr_h).max())}
+
+    sporder.chunk_similarity_greedy(ptr, ind, is_symmetric=sym, ctx=ctx)  # warmup
+    flush = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    runs = []
+    for _ in range(repeats):
+        flush.zero_()
+        torch.cuda.synchronize()
+        order, timing = sporder.chunk_similarity_greedy(ptr, ind, is_symmetric=sym,
+                                                        with_timing=True, ctx=ctx)
+        runs.append(timing)
+    runs.sort(key=lambda t: t["wall_ms"])
+    rec["csg"] = runs[len(runs) // 2]
+    _, stats = sporder.chunk_similarity_greedy(ptr, ind, is_symmetric=sym, with_stats=True,
+                                               ctx=ctx)
+    rec["csg_stats"] = stats
+    print(f"[{name}] csg {rec['csg']}", file=sys.stderr, flush=True)
+    if cg:
+        flush.zero_()
+        torch.cuda.synchronize()
+        _, timing = sporder.chunk_greedy(ptr, ind, is_symmetric=sym, with_timing=True, ctx=ctx)
+        rec["cg"] = timing
+        print(f"[{name}] cg {timing}", file=sys.stderr, flush=True)
+    del flush
+
+    sporder.reorder(ptr, ind, order, val=val, symmetric=True, ctx=ctx)  # warmup
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    p2, i2, v2 = sporder.reorder(ptr, ind, order, val=val, symmetric=True, ctx=ctx)
+    torch.cuda.synchronize()
+    rec["permute_ms"] = (time.perf_counter() - t1) * 1e3
+
+    if spmm:
+        rec["spmm"] = {}
+        for N in WIDTHS[name]:
+            gen = torch.Generator(device=dev).manual_seed(42)
+            B = torch.randn((n, N), generator=gen, dtype=torch.float32, device=dev)
+            by = spmm_bytes(n, nnz, N)
+            for algo in algos:
+                to = _spmm_ms(sporder, ctx, ptr, ind, val, B, algo)
+                tr = _spmm_ms(sporder, ctx, p2, i2, v2, B, algo)
+                rec["spmm"][f"{N}/{algo}"] = {
+                    "orig_ms": round(to, 4), "reordered_ms": round(tr, 4),
+                    "orig_gbs": round(by / to / 1e6, 1), "reordered_gbs": round(by / tr / 1e6, 1)}
+                print(f"[{name}] N={N} {algo}: original {to:.4f} ms, reordered {tr:.4f} ms "
+                      f"({by / tr / 1e6:.0f} GB/s)", file=sys.stderr, flush=True)
+            del B
+    return rec
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--cfg", default="C1,C2,C3,C4,C5")
+    ap.add_argument("--no-spmm", action="store_true")
+    ap.add_argument("--algos", default="row_split,merge_path")
+    ap.add_argument("--repeats", type=int, default=3)
+    ap.add_argument("--cg", action="store_true", help="also time sporder-cg once")
+    args = ap.parse_args(argv)
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("sweep needs a ROCm GPU", file=sys.stderr)
+        return 1
+    for name in args.cfg.split(","):
+        rec = measure(name, spmm=not args.no_spmm, algos=tuple(args.algos.split(",")),
+                      repeats=args.repeats, cg=args.cg)
+        print(json.dumps(rec), flush=True)
+        torch.cuda.empty_cache()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
