@@ -177,16 +177,17 @@ __global__ void __launch_bounds__(kGreedyBlock)
 // Compact greedy: chunks of at most kGreedyCompactRows rows.  Four waves
 // count each row's valid entries that fall inside the chunk (the only ones the
 // chain can follow; all of them for a chunk-restricted table, a few for the
-// global one), the counts are scanned into per-row offsets and the entries
-// copied as (weight bits << 32 | local index) into LDS; then wave 0 runs the
-// chain on LDS alone.  A slice with more than `entry_cap` in-chunk
+// global one) and stage them, unordered, in LDS; the counts are scanned into
+// per-row offsets and the staged entries moved to their rows as
+// (weight bits << 32 | local index); then wave 0 runs the chain on LDS alone.
+// The table slice is read once.  A slice with more than `entry_cap` in-chunk
 // entries keeps the offsets in LDS and reads the rows from global memory.
 constexpr int kGreedyCompactRows = 4096;
 
-// Dynamic LDS layout: entries u64[entry_cap] | offsets i32[rows_cap + 1] |
-// bitmap u32[ceil(rows_cap / 32)].
+// Dynamic LDS layout: entries u64[entry_cap] | staged slice positions
+// i32[entry_cap] | offsets i32[rows_cap + 1] | bitmap u32[ceil(rows_cap / 32)].
 size_t greedy_compact_lds(int32_t rows_cap, int32_t entry_cap) {
-  return static_cast<size_t>(entry_cap) * 8u + static_cast<size_t>(rows_cap + 1) * 4u +
+  return static_cast<size_t>(entry_cap) * 12u + static_cast<size_t>(rows_cap + 1) * 4u +
          static_cast<size_t>((rows_cap + 31) / 32) * 4u;
 }
 
@@ -196,8 +197,10 @@ __global__ void __launch_bounds__(kGreedyBlock)
                           ChainCounters *counters, int32_t rows_cap, int32_t entry_cap) {
   extern __shared__ uint64_t smem_u64[];
   __shared__ int32_t s_total;
+  __shared__ int32_t s_staged;
   uint64_t *s_ent = smem_u64;
-  int32_t *s_off = reinterpret_cast<int32_t *>(smem_u64 + entry_cap);
+  int32_t *s_pos = reinterpret_cast<int32_t *>(smem_u64 + entry_cap);
+  int32_t *s_off = s_pos + entry_cap;
   uint32_t *s_bm = reinterpret_cast<uint32_t *>(s_off + rows_cap + 1);
 
   const int tid = threadIdx.x;
@@ -215,6 +218,7 @@ __global__ void __launch_bounds__(kGreedyBlock)
 
   for (int32_t r = tid; r <= size; r += kGreedyBlock) s_off[r] = 0;
   for (int32_t w = tid; w < words; w += kGreedyBlock) s_bm[w] = 0u;
+  if (tid == 0) s_staged = 0;
   __syncthreads();
   // Per-row count of valid entries inside the chunk (valid entries form a
   // prefix of each row; only in-chunk entries can be followed), read as a
@@ -236,6 +240,11 @@ __global__ void __launch_bounds__(kGreedyBlock)
         if (c >= start && c < end) {
           atomicAdd(&s_off[r + 1], 1);
           in_w += wi_weight(v[u]);
+          const int32_t si = atomicAdd(&s_staged, 1);
+          if (si < entry_cap) {
+            s_ent[si] = v[u];
+            s_pos[si] = static_cast<int32_t>(e0 + u);
+          }
         } else {
           atomicOr(&s_bm[r >> 5], 1u << (r & 31));
         }
@@ -264,13 +273,29 @@ __global__ void __launch_bounds__(kGreedyBlock)
   const int32_t total = s_total;
   const bool compact = total <= entry_cap;
   if (compact) {
-    // Entry j of row r lands at s_off[r] + (its rank among the row's in-chunk
-    // entries): j itself unless the row is flagged as mixed.
-    for (int64_t e = tid; e < slice_len; e += kGreedyBlock) {
-      const uint64_t v = slice[e];
-      const int32_t c = wi_index(v);
-      if (c >= start && c < end) {
-        const int32_t r = static_cast<int32_t>(e / k), j = static_cast<int32_t>(e % k);
+    // Entry j of row r moves from its staging slot to s_off[r] + (its rank
+    // among the row's in-chunk entries): j itself unless the row is flagged as
+    // mixed.  Every thread takes its staged entries into registers before any
+    // is overwritten.
+    constexpr int kPerThread = 8; // entry_cap <= kPerThread * kGreedyBlock
+    uint64_t sv[kPerThread];
+    int32_t sp[kPerThread];
+#pragma unroll
+    for (int q = 0; q < kPerThread; ++q) {
+      const int32_t i = tid + q * kGreedyBlock;
+      sp[q] = -1;
+      if (i < total) {
+        sv[q] = s_ent[i];
+        sp[q] = s_pos[i];
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < kPerThread; ++q) {
+      if (sp[q] >= 0) {
+        const uint64_t v = sv[q];
+        const int32_t c = wi_index(v);
+        const int32_t r = sp[q] / k, j = sp[q] % k;
         int32_t rank = j;
         if (s_bm[r >> 5] & (1u << (r & 31))) {
           rank = 0;
@@ -610,7 +635,7 @@ SeriationOut seriate(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
   t_greedy.begin(ctx.stream);
   if (compact) {
     // About 20 KiB of LDS per chunk at chain_chunk 1024: several chunks per CU.
-    const int32_t entry_cap = 2048;
+    const int32_t entry_cap = 2048; // at most 8 staged entries per thread
     greedy_compact_kernel<<<dim3(static_cast<unsigned>(num_chunks)), kGreedyBlock,
                             greedy_compact_lds(rows_max, entry_cap), ctx.stream>>>(
         n, k, chain_chunk, table, d_new_order, want_stats ? counters : nullptr, rows_max,

@@ -19,9 +19,9 @@
 //      gets the all-zero table row;
 //   3b. the rows are counting-sorted by floor(log2(row size)), largest
 //      first, rows without candidates last;
-//   4. waves claim rows in that order; a row with candidates binary-searches
-//      each column's run inside its bucket and feeds the run's rows,
-//      ascending, to the wave64 sketch.
+//   4. the workgroup writes the zero rows; waves claim the other rows in
+//      order, and each binary-searches each column's run inside its bucket
+//      and feeds the run's rows, ascending, to the wave64 sketch.
 //
 // The stream, and therefore the table, is identical to the reference's.
 // Two LDS tiers: up to 16384 nonzeros and 1024 rows per chunk (~74 KiB, two
@@ -221,24 +221,27 @@ __global__ void __launch_bounds__(kLocalThreads)
     }
     __syncthreads();
 
-    // 4. Sketch, one wave per row.  Waves claim rows from a shared counter
-    //    in the order of step 3b: stream lengths vary by orders of magnitude
-    //    on skewed graphs, and a fixed row-to-wave assignment would leave the
-    //    workgroup waiting on its most loaded wave.
+    // 4a. Rows without candidates (the tail of the order) get all-zero table
+    //     rows from the whole workgroup, 16 lanes per row.
+    const int32_t zero_start = s_class[kClasses - 1];
+    for (int32_t zi = zero_start + tid / 16; zi < rows; zi += kLocalThreads / 16) {
+      uint64_t *out = table + static_cast<size_t>(cs + s_order[zi]) * k;
+      for (int32_t j = tid % 16; j < k; j += 16) out[j] = 0;
+    }
+    // 4b. Sketch, one wave per row.  Waves claim rows from a shared counter
+    //     in the order of step 3b: stream lengths vary by orders of magnitude
+    //     on skewed graphs, and a fixed row-to-wave assignment would leave the
+    //     workgroup waiting on its most loaded wave.
     WaveSketch<CELLS> store;
     for (;;) {
       int32_t claim = 0;
       if (lane == 0) claim = atomicAdd(&s_next_row, 1);
       const int32_t idx = readlane(claim, 0);
-      if (idx >= rows) break;
+      if (idx >= zero_start) break;
       const int32_t r = s_order[idx];
       const int32_t row = cs + r;
       uint64_t *out = table + static_cast<size_t>(row) * k;
       const int32_t row_size = s_size[r];
-      if (idx >= s_class[kClasses - 1]) { // no candidates (class kClasses)
-        for (int32_t j = lane; j < k; j += kWave) out[j] = 0;
-        continue;
-      }
       store.clear();
       const int32_t rb = row_ptr[row], re = rb + row_size;
       for (int32_t pb = rb; pb < re; pb += kWave) {
