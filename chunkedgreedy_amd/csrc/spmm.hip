@@ -20,7 +20,9 @@
 //     C[i][j] = ((P_0 + P_1) + P_2) + ... left to right.
 // The segments of long rows are processed by many row groups of a second
 // launch (so one hub row does not serialise the whole SpMM), and a third
-// launch adds each long row's partials in the stated order.
+// launch adds each long row's partials in the stated order.  For N <= 32
+// (8 or more rows per wave) the row groups of a wave claim its 64 rows
+// dynamically, so short rows do not wait for a long neighbour.
 //
 // Merge-path: the nonzeros are cut into equal spans per wave (a row longer
 // than a span is split); each span's partial row sums are added into C with
@@ -38,10 +40,9 @@ constexpr int kSpmmDepth = 8; // B rows in flight per row group
 constexpr int kLongRow = SPORDER_SPMM_LONG_ROW;
 constexpr int kSegLen = SPORDER_SPMM_SEGMENT;
 
-
-// Long rows: descriptors appended by the row-split launch.
-// Rows past kLongRow nonzeros leave the row-split launch: each becomes nseg
-// segment units whose partials the fixup launch adds.
+// Long rows: rows past kLongRow nonzeros leave the row-split launch, which
+// appends a descriptor; each becomes nseg segment units whose partials the
+// fixup launch adds.
 struct LongRow {
   int32_t row;
   int32_t base; // first unit (also its first partial row)
