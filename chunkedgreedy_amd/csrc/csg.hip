@@ -184,10 +184,12 @@ __global__ void __launch_bounds__(kGreedyBlock)
 // entries keeps the offsets in LDS and reads the rows from global memory.
 constexpr int kGreedyCompactRows = 4096;
 
-// Dynamic LDS layout: entries u64[entry_cap] | staged slice positions
-// i32[entry_cap] | offsets i32[rows_cap + 1] | bitmap u32[ceil(rows_cap / 32)].
+// Dynamic LDS layout: entries u64[entry_cap] | offsets i32[rows_cap + 1] |
+// bitmap u32[ceil(rows_cap / 32)].  A staged entry is (weight bits << 32) |
+// (slice position << 12) | local index: positions are below 4096 * 256 = 2^20
+// and local indices below 4096.
 size_t greedy_compact_lds(int32_t rows_cap, int32_t entry_cap) {
-  return static_cast<size_t>(entry_cap) * 12u + static_cast<size_t>(rows_cap + 1) * 4u +
+  return static_cast<size_t>(entry_cap) * 8u + static_cast<size_t>(rows_cap + 1) * 4u +
          static_cast<size_t>((rows_cap + 31) / 32) * 4u;
 }
 
@@ -199,8 +201,7 @@ __global__ void __launch_bounds__(kGreedyBlock)
   __shared__ int32_t s_total;
   __shared__ int32_t s_staged;
   uint64_t *s_ent = smem_u64;
-  int32_t *s_pos = reinterpret_cast<int32_t *>(smem_u64 + entry_cap);
-  int32_t *s_off = s_pos + entry_cap;
+  int32_t *s_off = reinterpret_cast<int32_t *>(smem_u64 + entry_cap);
   uint32_t *s_bm = reinterpret_cast<uint32_t *>(s_off + rows_cap + 1);
 
   const int tid = threadIdx.x;
@@ -235,15 +236,24 @@ __global__ void __launch_bounds__(kGreedyBlock)
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int32_t c = wi_index(v[u]);
-      if (e0 + u < slice_len && c >= 0) {
+      const bool valid = e0 + u < slice_len && c >= 0;
+      const bool inside = valid && c >= start && c < end;
+      // Staging slots for the wave's in-chunk entries: one LDS atomic per
+      // wave, ranks from the ballot.
+      const uint64_t m = ballot(inside);
+      int32_t base = 0;
+      if (m != 0 && lane == 0) base = atomicAdd(&s_staged, __popcll(m));
+      base = readlane(base, 0);
+      if (valid) {
         const int32_t r = static_cast<int32_t>((e0 + u) / k);
-        if (c >= start && c < end) {
+        if (inside) {
           atomicAdd(&s_off[r + 1], 1);
           in_w += wi_weight(v[u]);
-          const int32_t si = atomicAdd(&s_staged, 1);
+          const int32_t si = base + __popcll(m & ((1ull << lane) - 1ull));
           if (si < entry_cap) {
-            s_ent[si] = v[u];
-            s_pos[si] = static_cast<int32_t>(e0 + u);
+            s_ent[si] = (v[u] & 0xFFFFFFFF00000000ull) |
+                        (static_cast<uint64_t>(e0 + u) << 12) |
+                        static_cast<uint32_t>(c - start);
           }
         } else {
           atomicOr(&s_bm[r >> 5], 1u << (r & 31));
@@ -279,23 +289,19 @@ __global__ void __launch_bounds__(kGreedyBlock)
     // is overwritten.
     constexpr int kPerThread = 8; // entry_cap <= kPerThread * kGreedyBlock
     uint64_t sv[kPerThread];
-    int32_t sp[kPerThread];
 #pragma unroll
     for (int q = 0; q < kPerThread; ++q) {
       const int32_t i = tid + q * kGreedyBlock;
-      sp[q] = -1;
-      if (i < total) {
-        sv[q] = s_ent[i];
-        sp[q] = s_pos[i];
-      }
+      sv[q] = i < total ? s_ent[i] : ~0ull;
     }
     __syncthreads();
 #pragma unroll
     for (int q = 0; q < kPerThread; ++q) {
-      if (sp[q] >= 0) {
+      if (sv[q] != ~0ull) {
         const uint64_t v = sv[q];
-        const int32_t c = wi_index(v);
-        const int32_t r = sp[q] / k, j = sp[q] % k;
+        const int32_t pos = static_cast<int32_t>((v >> 12) & 0xFFFFFu);
+        const int32_t local = static_cast<int32_t>(v & 0xFFFu);
+        const int32_t r = pos / k, j = pos % k;
         int32_t rank = j;
         if (s_bm[r >> 5] & (1u << (r & 31))) {
           rank = 0;
@@ -305,7 +311,7 @@ __global__ void __launch_bounds__(kGreedyBlock)
             rank += (ct >= start && ct < end);
           }
         }
-        s_ent[s_off[r] + rank] = (v & 0xFFFFFFFF00000000ull) | static_cast<uint32_t>(c - start);
+        s_ent[s_off[r] + rank] = (v & 0xFFFFFFFF00000000ull) | static_cast<uint32_t>(local);
       }
     }
   }
@@ -636,6 +642,9 @@ SeriationOut seriate(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
   if (compact) {
     // About 20 KiB of LDS per chunk at chain_chunk 1024: several chunks per CU.
     const int32_t entry_cap = 2048; // at most 8 staged entries per thread
+    // Staged entries pack the slice position in 20 bits.
+    SP_EXPECT(static_cast<int64_t>(rows_max) * k <= (int64_t{1} << 20),
+              "compact chain slice exceeds 2^20 entries");
     greedy_compact_kernel<<<dim3(static_cast<unsigned>(num_chunks)), kGreedyBlock,
                             greedy_compact_lds(rows_max, entry_cap), ctx.stream>>>(
         n, k, chain_chunk, table, d_new_order, want_stats ? counters : nullptr, rows_max,

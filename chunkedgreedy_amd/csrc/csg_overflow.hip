@@ -113,7 +113,8 @@ __global__ void __launch_bounds__(kRunsBlock)
       const int32_t c = col_ind[p];
       const int32_t b0 = col_ptr[c], b1 = col_ptr[c + 1];
       const int32_t a = lower_bound_dev(row_ind, b0, b1, cs);
-      const int32_t b = lower_bound_dev(row_ind, a, b1, ce);
+      // The run of chunk rows is short next to the column: gallop from a.
+      const int32_t b = gallop_lower_bound(row_ind, a, b1, ce);
       runs[p] = make_int2(a, b - a);
     }
   }

@@ -33,6 +33,17 @@ __device__ __forceinline__ int32_t lower_bound_dev(const int32_t *a, int32_t lo,
   return lo;
 }
 
+// lower_bound_dev for an answer expected near `lo`: probe lo, lo+1, lo+3,
+// lo+7, ... until an element >= t (or hi) is passed, then search the last
+// doubling interval.  log2(distance) probes instead of log2(hi - lo).
+__device__ __forceinline__ int32_t gallop_lower_bound(const int32_t *a, int32_t lo,
+                                                      int32_t hi, int32_t t) {
+  int32_t b = 1;
+  while (lo + b < hi && a[lo + b - 1] < t) b <<= 1;
+  // a[lo + b/2 - 1] < t when b > 1, and a[lo + b - 1] >= t unless lo + b >= hi.
+  return lower_bound_dev(a, lo + (b >> 1), lo + b < hi ? lo + b : hi, t);
+}
+
 // Space-saving sketch of capacity 32*CELLS spread over one wave64.
 template <int CELLS> struct WaveSketch {
   static constexpr int LC = (CELLS + 1) / 2; // cells held per physical lane
