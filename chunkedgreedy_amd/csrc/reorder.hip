@@ -24,6 +24,24 @@ namespace {
 
 constexpr int kBlockSortCap = 4096;
 constexpr int kBlockSortThreads = 256;
+// Rows longer than kBigRow entries are copied by copy_big_rows in units of
+// kCopyUnit entries spread over the whole GPU, not by one lane group.
+constexpr int kBigRow = 1024;
+constexpr int kCopyUnit = 4096;
+
+struct BigRow {
+  int32_t src;  // first old entry
+  int32_t len;
+  int32_t dst;  // first new entry
+  int32_t base; // first copy unit
+};
+struct BigCtl {
+  int32_t rows;
+  int32_t units;
+};
+
+int64_t max_big_rows(int32_t nnz) { return nnz / (kBigRow + 1) + 1; }
+int64_t max_copy_units(int32_t nnz) { return nnz / kCopyUnit + max_big_rows(nnz) + 1; }
 
 __global__ void gather_row_lengths(int32_t n, const int32_t *__restrict__ ptr_old,
                                    const int32_t *__restrict__ new2old,
@@ -49,9 +67,10 @@ __global__ void invert_perm(int32_t n, const int32_t *__restrict__ src,
 // row of at most G entries is also sorted in registers (bitonic network over
 // the group's lanes) and written in final order; a longer row is written
 // unsorted to key_tmp/val_tmp and appended to `long_rows`.  Without col_map
-// (ROWS) rows are copied verbatim at any length.  With val_new set and
-// val_old NULL the values written are 0.0f, as in the reference's gather_rows
-// (reorder.cu:37-45).
+// (ROWS) rows are copied verbatim.  Rows past kBigRow entries are registered
+// for copy_big_rows instead of copied here (still appended to `long_rows`
+// with col_map).  With val_new set and val_old NULL the values written are
+// 0.0f, as in the reference's gather_rows (reorder.cu:37-45).
 template <int G>
 __global__ void __launch_bounds__(256)
     permute_rows(int32_t n, const int32_t *__restrict__ ptr_old,
@@ -60,7 +79,8 @@ __global__ void __launch_bounds__(256)
                  const int32_t *__restrict__ ptr_new, int32_t *__restrict__ ind_new,
                  float *__restrict__ val_new, int32_t *__restrict__ key_tmp,
                  float *__restrict__ val_tmp, int32_t *__restrict__ long_rows,
-                 int32_t *__restrict__ long_count) {
+                 int32_t *__restrict__ long_count, BigCtl *big_ctl, BigRow *big_rows,
+                 int32_t *big_owner) {
   constexpr int kRowsPerWave = kWave / G;
   const int lane = lane_id();
   const int gl = lane % G;
@@ -100,14 +120,45 @@ __global__ void __launch_bounds__(256)
         if (val_new) val_new[dst + gl] = v;
       }
     } else if (row_ok) {
-      int32_t *ki = col_map ? key_tmp : ind_new;
-      float *vo = col_map ? val_tmp : val_new;
-      for (int32_t q = gl; q < len; q += G) {
-        const int32_t c = ind_old[src + q];
-        ki[dst + q] = col_map ? col_map[c] : c;
-        if (vo) vo[dst + q] = val_old ? val_old[src + q] : 0.0f;
+      if (len > kBigRow) {
+        if (gl == 0) {
+          const int32_t units = (len + kCopyUnit - 1) / kCopyUnit;
+          const int32_t id = atomicAdd(&big_ctl->rows, 1);
+          const int32_t base = atomicAdd(&big_ctl->units, units);
+          big_rows[id] = BigRow{src, len, dst, base};
+          for (int32_t u = 0; u < units; ++u) big_owner[base + u] = id;
+        }
+      } else {
+        int32_t *ki = col_map ? key_tmp : ind_new;
+        float *vo = col_map ? val_tmp : val_new;
+        for (int32_t q = gl; q < len; q += G) {
+          const int32_t c = ind_old[src + q];
+          ki[dst + q] = col_map ? col_map[c] : c;
+          if (vo) vo[dst + q] = val_old ? val_old[src + q] : 0.0f;
+        }
       }
       if (col_map && gl == 0) long_rows[atomicAdd(long_count, 1)] = static_cast<int32_t>(p);
+    }
+  }
+}
+
+// Copy units of the rows registered by permute_rows: a workgroup copies
+// kCopyUnit consecutive entries of one row (columns mapped through col_map
+// when given), grid-striding over the units.
+__global__ void __launch_bounds__(256)
+    copy_big_rows(const int32_t *__restrict__ ind_old, const float *__restrict__ val_old,
+                  const int32_t *__restrict__ col_map, const BigCtl *__restrict__ big_ctl,
+                  const BigRow *__restrict__ big_rows, const int32_t *__restrict__ big_owner,
+                  int32_t *__restrict__ ind_out, float *__restrict__ val_out) {
+  const int32_t units = big_ctl->units;
+  for (int32_t u = blockIdx.x; u < units; u += gridDim.x) {
+    const BigRow b = big_rows[big_owner[u]];
+    const int32_t q0 = (u - b.base) * kCopyUnit;
+    const int32_t q1 = q0 + kCopyUnit < b.len ? q0 + kCopyUnit : b.len;
+    for (int32_t q = q0 + static_cast<int32_t>(threadIdx.x); q < q1; q += 256) {
+      const int32_t c = ind_old[b.src + q];
+      ind_out[b.dst + q] = col_map ? col_map[c] : c;
+      if (val_out) val_out[b.dst + q] = val_old ? val_old[b.src + q] : 0.0f;
     }
   }
 }
@@ -328,12 +379,14 @@ void launch_permute_g(Context &ctx, int32_t n, const int32_t *ptr_old, const int
                       const float *val_old, const int32_t *new2old, const int32_t *col_map,
                       const int32_t *ptr_new, int32_t *ind_new, float *val_new,
                       int32_t *key_tmp, float *val_tmp, int32_t *long_rows,
-                      int32_t *long_count) {
+                      int32_t *long_count, BigCtl *big_ctl, BigRow *big_rows,
+                      int32_t *big_owner) {
   constexpr int rows_per_block = 4 * (kWave / G);
   const int g = ctx.grid_for(ceil_div64(n, rows_per_block), 256, 4);
   permute_rows<G><<<g, 256, 0, ctx.stream>>>(n, ptr_old, ind_old, val_old, new2old, col_map,
                                             ptr_new, ind_new, val_new, key_tmp, val_tmp,
-                                            long_rows, long_count);
+                                            long_rows, long_count, big_ctl, big_rows,
+                                            big_owner);
   SP_LAUNCH_CHECK();
 }
 
@@ -341,18 +394,27 @@ void launch_permute(Context &ctx, int G, int32_t n, const int32_t *ptr_old,
                     const int32_t *ind_old, const float *val_old, const int32_t *new2old,
                     const int32_t *col_map, const int32_t *ptr_new, int32_t *ind_new,
                     float *val_new, int32_t *key_tmp, float *val_tmp, int32_t *long_rows,
-                    int32_t *long_count) {
+                    int32_t *long_count, int32_t nnz, BigCtl *big_ctl, BigRow *big_rows,
+                    int32_t *big_owner) {
+  fill_u32(ctx, big_ctl, sizeof(BigCtl) / 4, 0u);
   switch (G) {
 #define SP_CASE(V)                                                                       \
   case V:                                                                                \
     launch_permute_g<V>(ctx, n, ptr_old, ind_old, val_old, new2old, col_map, ptr_new,    \
-                        ind_new, val_new, key_tmp, val_tmp, long_rows, long_count);      \
+                        ind_new, val_new, key_tmp, val_tmp, long_rows, long_count,       \
+                        big_ctl, big_rows, big_owner);                                   \
     break;
     SP_CASE(4) SP_CASE(8) SP_CASE(16) SP_CASE(32) SP_CASE(64)
 #undef SP_CASE
   default:
     SP_EXPECT(false, "internal: bad group width");
   }
+  // Big rows' units (none registered: every workgroup exits at once).
+  const int gb = ctx.grid_for(max_copy_units(nnz), 256, 4);
+  copy_big_rows<<<gb, 256, 0, ctx.stream>>>(ind_old, val_old, col_map, big_ctl, big_rows,
+                                            big_owner, col_map ? key_tmp : ind_new,
+                                            col_map ? val_tmp : val_new);
+  SP_LAUNCH_CHECK();
 }
 
 } // namespace
@@ -374,13 +436,18 @@ extern "C" void sporder_reorder(sporder_context_t h, int32_t n, int32_t nnz,
   const bool symmetric = mode == SPORDER_REORDER_SYMMETRIC;
   const bool with_vals = d_val_old != nullptr && d_val_new != nullptr;
 
-  size_t need = ws_bytes<int32_t>(scan_tmp_elems(static_cast<int64_t>(n) + 1));
+  size_t need = ws_bytes<int32_t>(scan_tmp_elems(static_cast<int64_t>(n) + 1)) +
+                ws_bytes<BigCtl>(1) + ws_bytes<BigRow>(static_cast<size_t>(max_big_rows(nnz))) +
+                ws_bytes<int32_t>(static_cast<size_t>(max_copy_units(nnz)));
   if (symmetric) {
     need += ws_bytes<int32_t>(n) + ws_bytes<int32_t>(nnz) + ws_bytes<float>(nnz) +
             3 * ws_bytes<int32_t>(static_cast<size_t>(n) + 2) + ws_bytes<int32_t>(3);
   }
   ctx.reserve(need);
   int32_t *scan_tmp = ctx.take<int32_t>(scan_tmp_elems(static_cast<int64_t>(n) + 1));
+  BigCtl *big_ctl = ctx.take<BigCtl>(1);
+  BigRow *big_rows = ctx.take<BigRow>(static_cast<size_t>(max_big_rows(nnz)));
+  int32_t *big_owner = ctx.take<int32_t>(static_cast<size_t>(max_copy_units(nnz)));
 
   const int row_grid = ctx.grid_for(ceil_div64(n, 256), 256, 4);
   const int wave_grid = ctx.grid_for(ceil_div64(n, 4), 256, 4);
@@ -397,7 +464,8 @@ extern "C" void sporder_reorder(sporder_context_t h, int32_t n, int32_t nnz,
 
   if (!symmetric) {
     launch_permute(ctx, G, n, d_ptr_old, d_ind_old, d_val_old, d_new_order, nullptr,
-                   d_ptr_new, d_ind_new, d_val_new, nullptr, nullptr, nullptr, nullptr);
+                   d_ptr_new, d_ind_new, d_val_new, nullptr, nullptr, nullptr, nullptr, nnz,
+                   big_ctl, big_rows, big_owner);
     ctx.sync();
     return;
   }
@@ -417,7 +485,8 @@ extern "C" void sporder_reorder(sporder_context_t h, int32_t n, int32_t nnz,
   // longer rows go to list1 (unsorted in the temporaries).
   launch_permute(ctx, G, n, d_ptr_old, d_ind_old, d_val_old, d_new_order, old2new,
                  d_ptr_new, d_ind_new, with_vals ? d_val_new : nullptr, unsorted,
-                 with_vals ? val_unsorted : nullptr, list1, counts);
+                 with_vals ? val_unsorted : nullptr, list1, counts, nnz, big_ctl, big_rows,
+                 big_owner);
   sort_rows_wave<<<wave_grid, 256, 0, ctx.stream>>>(
       list1, counts, d_ptr_new, unsorted, with_vals ? val_unsorted : nullptr, d_ind_new,
       with_vals ? d_val_new : nullptr, long_rows, counts + 1);
