@@ -220,6 +220,43 @@ __device__ __forceinline__ uint32_t dpp_u32(uint32_t v, uint32_t ident) {
       static_cast<int>(ident), static_cast<int>(v), CTRL, ROWS, 0xf, false));
 }
 
+// v of lane (lane ^ j) for j in {1, 2, 4, 8, 16, 32}, inside the VALU:
+// quad_perm for 1 and 2, row_shl:4 / row_shr:4 restricted to alternate banks
+// of 4 lanes for 4, row_ror:8 for 8, and the gfx950 lane swaps for 16 and 32
+// (permlane16_swap exchanges rows 0<->1 and 2<->3, permlane32_swap the two
+// halves; of the pair returned for (v, v), element 0 holds the partner value
+// in the upper row / half and element 1 in the lower).  j is a compile-time
+// constant after unrolling at every call site.
+__device__ __forceinline__ uint32_t lane_xor_u32(uint32_t v, int j) {
+  const int x = static_cast<int>(v);
+  switch (j) {
+  case 1:
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(x, x, 0xB1, 0xf, 0xf, false));
+  case 2:
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(x, x, 0x4E, 0xf, 0xf, false));
+  case 4: {
+    const int t = __builtin_amdgcn_update_dpp(x, x, 0x104, 0xf, 0x5, false);
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(t, x, 0x114, 0xf, 0xA, false));
+  }
+  case 8:
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(x, x, 0x128, 0xf, 0xf, false));
+  case 16: {
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return (__lane_id() & 16) ? r[0] : r[1];
+  }
+  default: {
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return (__lane_id() & 32) ? r[0] : r[1];
+  }
+  }
+}
+__device__ __forceinline__ int32_t lane_xor_i32(int32_t v, int j) {
+  return static_cast<int32_t>(lane_xor_u32(static_cast<uint32_t>(v), j));
+}
+__device__ __forceinline__ float lane_xor_f32(float v, int j) {
+  return __uint_as_float(lane_xor_u32(__float_as_uint(v), j));
+}
+
 // Minimum / maximum over the wave, returned wave-uniform.
 __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
   constexpr uint32_t I = 0xFFFFFFFFu;

@@ -22,6 +22,7 @@ namespace sporder_hip {
 
 namespace {
 
+constexpr int kWaveSortCap = 8 * kWave; // rows sorted in one wave's registers
 constexpr int kBlockSortCap = 4096;
 constexpr int kBlockSortThreads = 256;
 // Rows longer than kBigRow entries are copied by copy_big_rows in units of
@@ -62,15 +63,31 @@ __global__ void invert_perm(int32_t n, const int32_t *__restrict__ src,
   }
 }
 
+// Appends `value` for every lane with `take` to list[*count ...]: one atomic
+// per wave, slots in lane order.  Every lane of the wave must call it.
+__device__ __forceinline__ void wave_append(bool take, int32_t value, int32_t *list,
+                                            int32_t *count) {
+  const uint64_t m = ballot(take);
+  if (m == 0) return;
+  const int leader = __builtin_ctzll(m);
+  int32_t base = 0;
+  if (lane_id() == leader) base = atomicAdd(count, __popcll(m));
+  base = readlane(base, leader);
+  if (take) list[base + __popcll(m & ((1ull << lane_id()) - 1ull))] = value;
+}
+
 // G lanes per new row (64/G rows per wave).  Copies old row new2old[p] to row
 // p, mapping columns through col_map when given.  With col_map (SYMMETRIC) a
 // row of at most G entries is also sorted in registers (bitonic network over
 // the group's lanes) and written in final order; a longer row is written
-// unsorted to key_tmp/val_tmp and appended to `long_rows`.  Without col_map
-// (ROWS) rows are copied verbatim.  Rows past kBigRow entries are registered
-// for copy_big_rows instead of copied here (still appended to `long_rows`
-// with col_map).  With val_new set and val_old NULL the values written are
-// 0.0f, as in the reference's gather_rows (reorder.cu:37-45).
+// unsorted to key_tmp/val_tmp and appended to the list of the stage that
+// sorts it: lists[0] (up to kWaveSortCap entries, sort_rows_wave), lists[1]
+// (up to kBlockSortCap, sort_rows_block), lists[2] (longer, the device-wide
+// sort), with counts in counts[0..2].  Without col_map (ROWS) rows are copied
+// verbatim.  Rows past kBigRow entries are registered for copy_big_rows
+// instead of copied here.  All list and registry appends take one atomic per
+// wave.  With val_new set and val_old NULL the values written are 0.0f, as in
+// the reference's gather_rows (reorder.cu:37-45).
 template <int G>
 __global__ void __launch_bounds__(256)
     permute_rows(int32_t n, const int32_t *__restrict__ ptr_old,
@@ -78,9 +95,9 @@ __global__ void __launch_bounds__(256)
                  const int32_t *__restrict__ new2old, const int32_t *__restrict__ col_map,
                  const int32_t *__restrict__ ptr_new, int32_t *__restrict__ ind_new,
                  float *__restrict__ val_new, int32_t *__restrict__ key_tmp,
-                 float *__restrict__ val_tmp, int32_t *__restrict__ long_rows,
-                 int32_t *__restrict__ long_count, BigCtl *big_ctl, BigRow *big_rows,
-                 int32_t *big_owner) {
+                 float *__restrict__ val_tmp, int32_t *__restrict__ lists,
+                 int32_t *__restrict__ counts, int32_t list_stride, BigCtl *big_ctl,
+                 BigRow *big_rows, int32_t *big_owner) {
   constexpr int kRowsPerWave = kWave / G;
   const int lane = lane_id();
   const int gl = lane % G;
@@ -105,8 +122,8 @@ __global__ void __launch_bounds__(256)
       for (int kk = 2; kk <= G; kk <<= 1) {
 #pragma unroll
         for (int j = kk >> 1; j > 0; j >>= 1) {
-          const int32_t ok = __shfl_xor(key, j, G);
-          const float ov = __shfl_xor(v, j, G);
+          const int32_t ok = lane_xor_i32(key, j);
+          const float ov = lane_xor_f32(v, j);
           const bool ascending = (gl & kk) == 0;
           const bool lower = (gl & j) == 0;
           if ((ascending == lower) ? (ok < key) : (ok > key)) {
@@ -119,25 +136,63 @@ __global__ void __launch_bounds__(256)
         ind_new[dst + gl] = key;
         if (val_new) val_new[dst + gl] = v;
       }
-    } else if (row_ok) {
-      if (len > kBigRow) {
-        if (gl == 0) {
-          const int32_t units = (len + kCopyUnit - 1) / kCopyUnit;
-          const int32_t id = atomicAdd(&big_ctl->rows, 1);
-          const int32_t base = atomicAdd(&big_ctl->units, units);
-          big_rows[id] = BigRow{src, len, dst, base};
-          for (int32_t u = 0; u < units; ++u) big_owner[base + u] = id;
+    } else if (row_ok && len <= kBigRow) {
+      int32_t *ki = col_map ? key_tmp : ind_new;
+      float *vo = col_map ? val_tmp : val_new;
+      // Four entries per lane in flight: the column gather depends on the
+      // index load, so one at a time would serialise two latencies per entry.
+      for (int32_t q0 = gl; q0 < len; q0 += 4 * G) {
+        int32_t c[4];
+        float v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int32_t q = q0 + u * G;
+          c[u] = q < len ? ind_old[src + q] : 0;
+          v[u] = (q < len && val_old) ? val_old[src + q] : 0.0f;
         }
-      } else {
-        int32_t *ki = col_map ? key_tmp : ind_new;
-        float *vo = col_map ? val_tmp : val_new;
-        for (int32_t q = gl; q < len; q += G) {
-          const int32_t c = ind_old[src + q];
-          ki[dst + q] = col_map ? col_map[c] : c;
-          if (vo) vo[dst + q] = val_old ? val_old[src + q] : 0.0f;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int32_t q = q0 + u * G;
+          if (q < len) c[u] = col_map ? col_map[c[u]] : c[u];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int32_t q = q0 + u * G;
+          if (q < len) {
+            ki[dst + q] = c[u];
+            if (vo) vo[dst + q] = v[u];
+          }
         }
       }
-      if (col_map && gl == 0) long_rows[atomicAdd(long_count, 1)] = static_cast<int32_t>(p);
+    }
+    // Registry of big rows for copy_big_rows: unit bases from a wave scan.
+    const bool big = row_ok && gl == 0 && len > kBigRow;
+    const uint64_t mb = ballot(big);
+    if (mb != 0) {
+      const int32_t units = big ? (len + kCopyUnit - 1) / kCopyUnit : 0;
+      const int32_t incl = wave_incl_scan(units);
+      const int leader = __builtin_ctzll(mb);
+      int32_t rbase = 0, ubase = 0;
+      if (lane == leader) {
+        rbase = atomicAdd(&big_ctl->rows, __popcll(mb));
+        ubase = atomicAdd(&big_ctl->units, readlane(incl, kWave - 1));
+      }
+      rbase = readlane(rbase, leader);
+      ubase = readlane(ubase, leader);
+      if (big) {
+        const int32_t id = rbase + __popcll(mb & ((1ull << lane) - 1ull));
+        const int32_t base = ubase + incl - units;
+        big_rows[id] = BigRow{src, len, dst, base};
+        for (int32_t u = 0; u < units; ++u) big_owner[base + u] = id;
+      }
+    }
+    if (col_map != nullptr) {
+      const bool listed = row_ok && gl == 0 && !sort_here;
+      const int32_t row = static_cast<int32_t>(p);
+      wave_append(listed && len <= kWaveSortCap, row, lists, counts);
+      wave_append(listed && len > kWaveSortCap && len <= kBlockSortCap, row,
+                  lists + list_stride, counts + 1);
+      wave_append(listed && len > kBlockSortCap, row, lists + 2 * list_stride, counts + 2);
     }
   }
 }
@@ -163,74 +218,112 @@ __global__ void __launch_bounds__(256)
   }
 }
 
-// Listed rows of up to 64 entries: bitonic network across the lanes of one
-// wave.  Longer rows are appended to `long_rows` for the next stage.
-__global__ void sort_rows_wave(const int32_t *__restrict__ rows,
-                               const int32_t *__restrict__ row_count,
-                               const int32_t *__restrict__ ptr,
-                               const int32_t *__restrict__ key_in,
-                               const float *__restrict__ val_in,
-                               int32_t *__restrict__ key_out,
-                               float *__restrict__ val_out,
-                               int32_t *__restrict__ long_rows,
-                               int32_t *__restrict__ long_count) {
+// Bitonic sort of one row of at most 64*P entries held in a wave's registers:
+// entry e sits in lane e % 64, register e / 64 (padding keys 0x7fffffff sort
+// last; a row's columns are distinct).  Exchanges at distance j < 64 cross
+// lanes (lane_xor), longer ones pair registers of the same lane.
+template <int P>
+__device__ __forceinline__ void wave_sort_row(int32_t s, int32_t len,
+                                              const int32_t *__restrict__ key_in,
+                                              const float *__restrict__ val_in,
+                                              int32_t *__restrict__ key_out,
+                                              float *__restrict__ val_out) {
   const int lane = lane_id();
+  int32_t key[P];
+  float val[P];
+#pragma unroll
+  for (int r = 0; r < P; ++r) {
+    const int32_t e = lane + kWave * r;
+    const bool in = e < len;
+    key[r] = in ? key_in[s + e] : 0x7fffffff;
+    val[r] = (in && val_in) ? val_in[s + e] : 0.0f;
+  }
+#pragma unroll
+  for (int kk = 2; kk <= kWave * P; kk <<= 1) {
+#pragma unroll
+    for (int j = kk >> 1; j > 0; j >>= 1) {
+      if (j >= kWave) {
+        const int jr = j / kWave;
+#pragma unroll
+        for (int r = 0; r < P; ++r) {
+          if ((r & jr) == 0) {
+            const int q = r | jr;
+            const bool asc = ((kWave * r) & kk) == 0; // kk >= 128: lane bits do not matter
+            const bool swap = asc ? key[r] > key[q] : key[r] < key[q];
+            const int32_t tk = key[r];
+            const float tv = val[r];
+            key[r] = swap ? key[q] : key[r];
+            val[r] = swap ? val[q] : val[r];
+            key[q] = swap ? tk : key[q];
+            val[q] = swap ? tv : val[q];
+          }
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < P; ++r) {
+          const int32_t ok = lane_xor_i32(key[r], j);
+          const float ov = lane_xor_f32(val[r], j);
+          const bool asc = ((lane + kWave * r) & kk) == 0;
+          const bool lower = (lane & j) == 0;
+          if ((asc == lower) ? (ok < key[r]) : (ok > key[r])) {
+            key[r] = ok;
+            val[r] = ov;
+          }
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < P; ++r) {
+    const int32_t e = lane + kWave * r;
+    if (e < len) {
+      key_out[s + e] = key[r];
+      if (val_out) val_out[s + e] = val[r];
+    }
+  }
+}
+
+// Listed rows of up to kWaveSortCap entries, one wave per row, sorted in
+// registers (64, 128, 256 or 512 slots by the row's length; longer rows sort
+// faster in a workgroup's LDS).
+__global__ void __launch_bounds__(256)
+    sort_rows_wave(const int32_t *__restrict__ rows, const int32_t *__restrict__ row_count,
+                   const int32_t *__restrict__ ptr, const int32_t *__restrict__ key_in,
+                   const float *__restrict__ val_in, int32_t *__restrict__ key_out,
+                   float *__restrict__ val_out) {
   const int64_t wave0 = (blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x) / kWave;
   const int64_t nwaves = static_cast<int64_t>(gridDim.x) * blockDim.x / kWave;
   const int64_t count = *row_count;
   for (int64_t t = wave0; t < count; t += nwaves) {
     const int32_t r = rows[t];
-    int32_t s = ptr[r], e = ptr[r + 1], len = e - s;
-    if (len > kWave) {
-      if (lane == 0) long_rows[atomicAdd(long_count, 1)] = static_cast<int32_t>(r);
-      continue;
-    }
-    if (len == 0) continue;
-    bool in = lane < len;
-    int32_t key = in ? key_in[s + lane] : 0x7fffffff;
-    float val = (in && val_in) ? val_in[s + lane] : 0.0f;
-#pragma unroll
-    for (int kk = 2; kk <= kWave; kk <<= 1) {
-#pragma unroll
-      for (int j = kk >> 1; j > 0; j >>= 1) {
-        int32_t ok = __shfl_xor(key, j, kWave);
-        float ov = __shfl_xor(val, j, kWave);
-        bool ascending = (lane & kk) == 0;
-        bool lower = (lane & j) == 0;
-        bool take = (ascending == lower) ? (ok < key) : (ok > key);
-        if (take) {
-          key = ok;
-          val = ov;
-        }
-      }
-    }
-    if (in) {
-      key_out[s + lane] = key;
-      if (val_out) val_out[s + lane] = val;
+    const int32_t s = ptr[r], len = ptr[r + 1] - s;
+    if (len <= kWave) {
+      wave_sort_row<1>(s, len, key_in, val_in, key_out, val_out);
+    } else if (len <= 2 * kWave) {
+      wave_sort_row<2>(s, len, key_in, val_in, key_out, val_out);
+    } else if (len <= 4 * kWave) {
+      wave_sort_row<4>(s, len, key_in, val_in, key_out, val_out);
+    } else {
+      wave_sort_row<8>(s, len, key_in, val_in, key_out, val_out);
     }
   }
 }
 
-// Rows of 65..kBlockSortCap entries: LDS bitonic sort, one workgroup per row.
-// Rows beyond the cap are appended to `huge_rows`.
+// Listed rows of kWaveSortCap+1 .. kBlockSortCap entries: LDS bitonic sort,
+// one workgroup per row.
 __global__ void __launch_bounds__(kBlockSortThreads)
     sort_rows_block(const int32_t *__restrict__ ptr,
                     const int32_t *__restrict__ long_rows,
                     const int32_t *__restrict__ long_count,
                     const int32_t *__restrict__ key_in,
                     const float *__restrict__ val_in, int32_t *__restrict__ key_out,
-                    float *__restrict__ val_out, int32_t *__restrict__ huge_rows,
-                    int32_t *__restrict__ huge_count) {
+                    float *__restrict__ val_out) {
   __shared__ int32_t sk[kBlockSortCap];
   __shared__ float sv[kBlockSortCap];
   const int32_t count = *long_count;
   for (int32_t t = blockIdx.x; t < count; t += gridDim.x) {
     int32_t r = long_rows[t];
     int32_t s = ptr[r], e = ptr[r + 1], len = e - s;
-    if (len > kBlockSortCap) {
-      if (threadIdx.x == 0) huge_rows[atomicAdd(huge_count, 1)] = r;
-      continue;
-    }
     int32_t pow2 = 1;
     while (pow2 < len) pow2 <<= 1;
     for (int32_t i = threadIdx.x; i < pow2; i += blockDim.x) {
@@ -378,14 +471,14 @@ template <int G>
 void launch_permute_g(Context &ctx, int32_t n, const int32_t *ptr_old, const int32_t *ind_old,
                       const float *val_old, const int32_t *new2old, const int32_t *col_map,
                       const int32_t *ptr_new, int32_t *ind_new, float *val_new,
-                      int32_t *key_tmp, float *val_tmp, int32_t *long_rows,
-                      int32_t *long_count, BigCtl *big_ctl, BigRow *big_rows,
+                      int32_t *key_tmp, float *val_tmp, int32_t *lists, int32_t *counts,
+                      int32_t list_stride, BigCtl *big_ctl, BigRow *big_rows,
                       int32_t *big_owner) {
   constexpr int rows_per_block = 4 * (kWave / G);
   const int g = ctx.grid_for(ceil_div64(n, rows_per_block), 256, 4);
   permute_rows<G><<<g, 256, 0, ctx.stream>>>(n, ptr_old, ind_old, val_old, new2old, col_map,
                                             ptr_new, ind_new, val_new, key_tmp, val_tmp,
-                                            long_rows, long_count, big_ctl, big_rows,
+                                            lists, counts, list_stride, big_ctl, big_rows,
                                             big_owner);
   SP_LAUNCH_CHECK();
 }
@@ -393,15 +486,15 @@ void launch_permute_g(Context &ctx, int32_t n, const int32_t *ptr_old, const int
 void launch_permute(Context &ctx, int G, int32_t n, const int32_t *ptr_old,
                     const int32_t *ind_old, const float *val_old, const int32_t *new2old,
                     const int32_t *col_map, const int32_t *ptr_new, int32_t *ind_new,
-                    float *val_new, int32_t *key_tmp, float *val_tmp, int32_t *long_rows,
-                    int32_t *long_count, int32_t nnz, BigCtl *big_ctl, BigRow *big_rows,
-                    int32_t *big_owner) {
+                    float *val_new, int32_t *key_tmp, float *val_tmp, int32_t *lists,
+                    int32_t *counts, int32_t list_stride, int32_t nnz, BigCtl *big_ctl,
+                    BigRow *big_rows, int32_t *big_owner) {
   fill_u32(ctx, big_ctl, sizeof(BigCtl) / 4, 0u);
   switch (G) {
 #define SP_CASE(V)                                                                       \
   case V:                                                                                \
     launch_permute_g<V>(ctx, n, ptr_old, ind_old, val_old, new2old, col_map, ptr_new,    \
-                        ind_new, val_new, key_tmp, val_tmp, long_rows, long_count,       \
+                        ind_new, val_new, key_tmp, val_tmp, lists, counts, list_stride,  \
                         big_ctl, big_rows, big_owner);                                   \
     break;
     SP_CASE(4) SP_CASE(8) SP_CASE(16) SP_CASE(32) SP_CASE(64)
@@ -441,7 +534,7 @@ extern "C" void sporder_reorder(sporder_context_t h, int32_t n, int32_t nnz,
                 ws_bytes<int32_t>(static_cast<size_t>(max_copy_units(nnz)));
   if (symmetric) {
     need += ws_bytes<int32_t>(n) + ws_bytes<int32_t>(nnz) + ws_bytes<float>(nnz) +
-            3 * ws_bytes<int32_t>(static_cast<size_t>(n) + 2) + ws_bytes<int32_t>(3);
+            ws_bytes<int32_t>(3 * (static_cast<size_t>(n) + 2)) + ws_bytes<int32_t>(3);
   }
   ctx.reserve(need);
   int32_t *scan_tmp = ctx.take<int32_t>(scan_tmp_elems(static_cast<int64_t>(n) + 1));
@@ -464,7 +557,7 @@ extern "C" void sporder_reorder(sporder_context_t h, int32_t n, int32_t nnz,
 
   if (!symmetric) {
     launch_permute(ctx, G, n, d_ptr_old, d_ind_old, d_val_old, d_new_order, nullptr,
-                   d_ptr_new, d_ind_new, d_val_new, nullptr, nullptr, nullptr, nullptr, nnz,
+                   d_ptr_new, d_ind_new, d_val_new, nullptr, nullptr, nullptr, nullptr, 0, nnz,
                    big_ctl, big_rows, big_owner);
     ctx.sync();
     return;
@@ -473,27 +566,29 @@ extern "C" void sporder_reorder(sporder_context_t h, int32_t n, int32_t nnz,
   int32_t *old2new = ctx.take<int32_t>(n);
   int32_t *unsorted = ctx.take<int32_t>(nnz);
   float *val_unsorted = ctx.take<float>(nnz);
-  int32_t *list1 = ctx.take<int32_t>(static_cast<size_t>(n) + 2);
-  int32_t *long_rows = ctx.take<int32_t>(static_cast<size_t>(n) + 2);
-  int32_t *huge_rows = ctx.take<int32_t>(static_cast<size_t>(n) + 2);
+  // Row lists of the three sort stages, one array with stride n + 2.
+  const int32_t stride = n + 2;
+  int32_t *lists = ctx.take<int32_t>(3 * static_cast<size_t>(stride));
+  int32_t *list1 = lists, *long_rows = lists + stride, *huge_rows = lists + 2 * stride;
   int32_t *counts = ctx.take<int32_t>(3);
 
   invert_perm<<<row_grid, 256, 0, ctx.stream>>>(n, d_new_order, old2new);
   SP_LAUNCH_CHECK();
   fill_u32(ctx, counts, 3, 0u);
   // Rows of at most G entries are remapped, sorted and written in one pass;
-  // longer rows go to list1 (unsorted in the temporaries).
+  // longer rows are written unsorted to the temporaries and listed by length
+  // for the stage that sorts them.
   launch_permute(ctx, G, n, d_ptr_old, d_ind_old, d_val_old, d_new_order, old2new,
                  d_ptr_new, d_ind_new, with_vals ? d_val_new : nullptr, unsorted,
-                 with_vals ? val_unsorted : nullptr, list1, counts, nnz, big_ctl, big_rows,
-                 big_owner);
+                 with_vals ? val_unsorted : nullptr, lists, counts, stride, nnz, big_ctl,
+                 big_rows, big_owner);
   sort_rows_wave<<<wave_grid, 256, 0, ctx.stream>>>(
       list1, counts, d_ptr_new, unsorted, with_vals ? val_unsorted : nullptr, d_ind_new,
-      with_vals ? d_val_new : nullptr, long_rows, counts + 1);
+      with_vals ? d_val_new : nullptr);
   SP_LAUNCH_CHECK();
   sort_rows_block<<<ctx.num_cus * 4, kBlockSortThreads, 0, ctx.stream>>>(
       d_ptr_new, long_rows, counts + 1, unsorted, with_vals ? val_unsorted : nullptr,
-      d_ind_new, with_vals ? d_val_new : nullptr, huge_rows, counts + 2);
+      d_ind_new, with_vals ? d_val_new : nullptr);
   SP_LAUNCH_CHECK();
 
   int32_t hcount = 0;
