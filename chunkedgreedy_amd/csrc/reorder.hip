@@ -165,6 +165,8 @@ __global__ void __launch_bounds__(256)
         }
       }
     }
+    // Rows sorted here need no bookkeeping; most waves have only those.
+    if (ballot(row_ok && !sort_here) == 0) continue;
     // Registry of big rows for copy_big_rows: unit bases from a wave scan.
     const bool big = row_ok && gl == 0 && len > kBigRow;
     const uint64_t mb = ballot(big);
