@@ -506,16 +506,6 @@ SpmmLongWs take_long_ws(Context &ctx, int32_t nnz, int32_t N) {
   return w;
 }
 
-// SPORDER_SPMM_STATIC_ROWS=1 selects the fixed row-per-group kernel for every
-// width (both compute the same stated order; the switch exists for A/B timing).
-bool static_rows() {
-  static const bool on = [] {
-    const char *v = std::getenv("SPORDER_SPMM_STATIC_ROWS");
-    return v != nullptr && v[0] == '1';
-  }();
-  return on;
-}
-
 template <int G>
 void launch_rowsplit_g(Context &ctx, int32_t n, int32_t nnz, const int32_t *ptr,
                        const int32_t *ind, const float *val, int32_t N, const float *B,
@@ -525,7 +515,7 @@ void launch_rowsplit_g(Context &ctx, int32_t n, int32_t nnz, const int32_t *ptr,
   // Narrow widths (G <= 8 lanes per row, 8+ rows per wave) lose most to
   // row-length imbalance inside a wave: claim rows dynamically there.  With
   // wider rows the fixed assignment keeps more waves in flight.
-  if (G <= 8 && N <= 4 * G && !static_rows()) {
+  if (G <= 8 && N <= 4 * G) {
     const int64_t blocks = ceil_div64(ceil_div64(n, kWave), kSpmmWaves);
     spmm_rows_dyn<G><<<dim3(static_cast<unsigned>(blocks)), kSpmmBlock, 0, ctx.stream>>>(
         n, ptr, ind, val, N, B, C, w.ctl, w.longs, w.owner);
