@@ -433,19 +433,153 @@ __global__ void __launch_bounds__(kSpmmBlock)
   }
 }
 
+// Merge-path on row groups: group g (G lanes, one float4 column slice each)
+// owns the nonzeros [g*span, (g+1)*span) and walks the pieces of the rows
+// they cover, in row order, with the pipelined gathers of the row-split
+// kernels.  A row lying wholly inside the span is stored; the piece of a row
+// cut by a span edge is added into C with float atomics (those rows are
+// zeroed first), so a cut row's value depends on the order of the atomics:
+// within 1e-5 of the row-split result, not bit-identical.  Row ends come from
+// a window of G row pointers held in the group's lanes.  N > 4G is covered by
+// repeating the walk per column slice.
+template <int G>
+__global__ void __launch_bounds__(kSpmmBlock)
+    spmm_merge_v4(int32_t n, int32_t nnz, const int32_t *__restrict__ ptr,
+                  const int32_t *__restrict__ ind, const float *__restrict__ val, int32_t N,
+                  const float *__restrict__ B, float *__restrict__ C, int32_t span,
+                  const int32_t *__restrict__ start_row) {
+  constexpr int U = kSpmmDepth;
+  const int lane = lane_id();
+  const int sub = lane / G, gl = lane % G, gbase = sub * G;
+  const int64_t wave = static_cast<int64_t>(blockIdx.x) * kSpmmWaves + threadIdx.x / kWave;
+  const int64_t grp = wave * (kWave / G) + sub;
+  const int64_t p0_64 = grp * static_cast<int64_t>(span);
+  const bool has = p0_64 < nnz;
+  const int32_t p0 = has ? static_cast<int32_t>(p0_64) : nnz;
+  const int32_t p1 =
+      has ? static_cast<int32_t>(p0_64 + span < nnz ? p0_64 + span : nnz) : nnz;
+  // First row of the span: the row holding nonzero p0 (from the prepare launch).
+  const int32_t first = has ? start_row[grp] : -1;
+  for (int32_t cb = 0; cb < N; cb += 4 * G) {
+    const int32_t col0 = cb + gl * 4;
+    const bool col_ok = col0 < N;
+    int32_t row = first;
+    int32_t wbase = first >= 0 ? first : 0;
+    int32_t win = ptr[wbase + 1 + gl < n ? wbase + 1 + gl : n]; // ptr[wbase + 1 + gl]
+    const int32_t w0 = __shfl(win, gbase, kWave);               // every lane shuffles
+    int32_t rs = row >= 0 ? ptr[row] : 0;
+    int32_t re = row >= 0 ? w0 : 0;
+    int32_t p = row >= 0 ? (rs > p0 ? rs : p0) : 0;
+    int32_t e = row >= 0 ? (re < p1 ? re : p1) : 0;
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    while (true) {
+      // Retire finished pieces and move each such group to its span's next
+      // row, until every group has work or is done.
+      while (true) {
+        const bool fin = row >= 0 && p >= e;
+        if (fin && col_ok) {
+          float *dst = C + static_cast<int64_t>(row) * N + col0;
+          if (rs >= p0 && re <= p1) {
+            store_nt(dst, acc);
+          } else {
+            atomicAdd(dst + 0, acc.x);
+            atomicAdd(dst + 1, acc.y);
+            atomicAdd(dst + 2, acc.z);
+            atomicAdd(dst + 3, acc.w);
+          }
+        }
+        if (ballot(fin) == 0) break;
+        const int32_t nrow = row + 1;
+        const bool next_ok = fin && re < p1 && nrow < n;
+        if (next_ok && nrow - wbase >= G) {
+          wbase = nrow;
+          win = ptr[wbase + 1 + gl < n ? wbase + 1 + gl : n];
+        }
+        const int32_t idx = next_ok ? gbase + (nrow - wbase) : gbase;
+        const int32_t wend = __shfl(win, idx, kWave);
+        if (fin) {
+          if (next_ok) {
+            rs = re;
+            re = wend;
+            row = nrow;
+            p = rs;
+            e = re < p1 ? re : p1;
+            acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+          } else {
+            row = -1;
+          }
+        }
+      }
+      if (ballot(row >= 0) == 0) break;
+      // One step: up to G nonzeros per group, U B rows in flight.
+      const int32_t rem = row >= 0 ? e - p : 0;
+      int32_t my_c = 0;
+      float my_v = 0.0f;
+      if (gl < rem) {
+        my_c = __builtin_nontemporal_load(ind + p + gl);
+        my_v = __builtin_nontemporal_load(val + p + gl);
+      }
+      const int32_t cnt = rem < G ? rem : G;
+      const int32_t cmax = static_cast<int32_t>(wave_max_u32(static_cast<uint32_t>(cnt)));
+      for (int32_t t = 0; t < cmax; t += U) {
+        int32_t c[U];
+        float v[U];
+        float4 bv[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          c[u] = __shfl(my_c, gbase + ((t + u) & (G - 1)), kWave);
+          v[u] = __shfl(my_v, gbase + ((t + u) & (G - 1)), kWave);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          if (t + u < cnt && col_ok) {
+            bv[u] = *reinterpret_cast<const float4 *>(B + static_cast<int64_t>(c[u]) * N + col0);
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          if (t + u < cnt && col_ok) {
+            acc.x = fmaf(v[u], bv[u].x, acc.x);
+            acc.y = fmaf(v[u], bv[u].y, acc.y);
+            acc.z = fmaf(v[u], bv[u].z, acc.z);
+            acc.w = fmaf(v[u], bv[u].w, acc.w);
+          }
+        }
+      }
+      if (row >= 0) p += cnt;
+    }
+  }
+}
+
 // Zero C rows that the merge-path kernel will accumulate into (rows crossing
-// a span boundary) and rows with no nonzeros (no span writes them).
+// a span boundary) and rows with no nonzeros (no span writes them).  With
+// start_row, also record for every span the row holding its first nonzero.
+// One lane per row for the bounds, the wave for each row it zeroes.
 __global__ void spmm_merge_prepare(int32_t n, const int32_t *__restrict__ ptr,
-                                   int32_t N, float *__restrict__ C, int32_t span) {
+                                   int32_t N, float *__restrict__ C, int32_t span,
+                                   int32_t *__restrict__ start_row) {
   const int lane = lane_id();
   const int64_t wave0 =
       (blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x) / kWave;
   const int64_t nwaves = static_cast<int64_t>(gridDim.x) * blockDim.x / kWave;
-  for (int64_t row = wave0; row < n; row += nwaves) {
-    const int32_t rs = ptr[row], re = ptr[row + 1];
-    const bool empty = rs == re;
-    const bool split = !empty && (rs / span) != ((re - 1) / span);
-    if (empty || split) {
+  for (int64_t rb = wave0 * kWave; rb < n; rb += nwaves * kWave) {
+    const int64_t r = rb + lane;
+    int32_t rs = 0, re = 0;
+    if (r < n) {
+      rs = ptr[r];
+      re = ptr[r + 1];
+    }
+    const bool empty = r < n && rs == re;
+    const bool split = r < n && !empty && (rs / span) != ((re - 1) / span);
+    if (start_row != nullptr && r < n && !empty) {
+      for (int64_t sp = (static_cast<int64_t>(rs) + span - 1) / span; sp * span < re; ++sp) {
+        start_row[sp] = static_cast<int32_t>(r);
+      }
+    }
+    uint64_t m = ballot(empty || split);
+    while (m) {
+      const int64_t row = rb + __builtin_ctzll(m);
+      m &= m - 1;
       for (int32_t j = lane; j < N; j += kWave) C[row * N + j] = 0.0f;
     }
   }
@@ -573,16 +707,62 @@ void spmm_rowsplit(Context &ctx, int32_t n, int32_t nnz, const int32_t *ptr,
   }
 }
 
+template <int G>
+void launch_merge_g(Context &ctx, int32_t n, int32_t nnz, const int32_t *ptr,
+                    const int32_t *ind, const float *val, int32_t N, const float *B, float *C) {
+  constexpr int gpw = kWave / G; // row groups per wave
+  // Span: about two groups per resident group slot, at least G * kSpmmDepth
+  // nonzeros (one full gather pipeline per group).
+  const int64_t groups = static_cast<int64_t>(ctx.num_cus) *
+                         (ctx.max_threads_per_cu / kWave) * gpw * 2;
+  int64_t span64 = ceil_div64(nnz > 0 ? nnz : 1, groups);
+  if (span64 < G * kSpmmDepth) span64 = G * kSpmmDepth;
+  const int32_t span = static_cast<int32_t>(span64);
+  const int64_t spans = ceil_div64(nnz, span);
+  ctx.reserve(ws_bytes<int32_t>(static_cast<size_t>(spans) + 1));
+  int32_t *start_row = ctx.take<int32_t>(static_cast<size_t>(spans) + 1);
+  const int gp = ctx.grid_for(ceil_div64(n, kSpmmBlock), kSpmmBlock, 4);
+  spmm_merge_prepare<<<gp, kSpmmBlock, 0, ctx.stream>>>(n, ptr, N, C, span, start_row);
+  SP_LAUNCH_CHECK();
+  if (nnz == 0) return;
+  const int64_t blocks = ceil_div64(spans, gpw * kSpmmWaves);
+  spmm_merge_v4<G><<<dim3(static_cast<unsigned>(blocks)), kSpmmBlock, 0, ctx.stream>>>(
+      n, nnz, ptr, ind, val, N, B, C, span, start_row);
+  SP_LAUNCH_CHECK();
+}
+
 void spmm_merge(Context &ctx, int32_t n, int32_t nnz, const int32_t *ptr,
                 const int32_t *ind, const float *val, int32_t N, const float *B,
                 float *C) {
-  // Span: about 2 waves per CU slot of work, at least 32 nonzeros.
+  const bool aligned = (N % 4 == 0) && (reinterpret_cast<uintptr_t>(B) % 16 == 0) &&
+                       (reinterpret_cast<uintptr_t>(C) % 16 == 0);
+  if (aligned) {
+    const int32_t q = N / 4; // float4 columns
+    if (q <= 1) {
+      launch_merge_g<1>(ctx, n, nnz, ptr, ind, val, N, B, C);
+    } else if (q <= 2) {
+      launch_merge_g<2>(ctx, n, nnz, ptr, ind, val, N, B, C);
+    } else if (q <= 4) {
+      launch_merge_g<4>(ctx, n, nnz, ptr, ind, val, N, B, C);
+    } else if (q <= 8) {
+      launch_merge_g<8>(ctx, n, nnz, ptr, ind, val, N, B, C);
+    } else if (q <= 16) {
+      launch_merge_g<16>(ctx, n, nnz, ptr, ind, val, N, B, C);
+    } else if (q <= 32) {
+      launch_merge_g<32>(ctx, n, nnz, ptr, ind, val, N, B, C);
+    } else {
+      launch_merge_g<64>(ctx, n, nnz, ptr, ind, val, N, B, C);
+    }
+    return;
+  }
+  // Widths that are not a multiple of 4 (or unaligned operands): one wave per
+  // span, lanes over columns.
   int64_t slots = static_cast<int64_t>(ctx.num_cus) * (ctx.max_threads_per_cu / kWave) * 2;
   int64_t span64 = ceil_div64(nnz > 0 ? nnz : 1, slots);
   if (span64 < 32) span64 = 32;
   int32_t span = static_cast<int32_t>(span64);
-  int gp = ctx.grid_for(ceil_div64(n, kSpmmBlock / kWave), kSpmmBlock, 4);
-  spmm_merge_prepare<<<gp, kSpmmBlock, 0, ctx.stream>>>(n, ptr, N, C, span);
+  int gp = ctx.grid_for(ceil_div64(n, kSpmmBlock), kSpmmBlock, 4);
+  spmm_merge_prepare<<<gp, kSpmmBlock, 0, ctx.stream>>>(n, ptr, N, C, span, nullptr);
   SP_LAUNCH_CHECK();
   if (nnz == 0) return;
   int64_t waves = ceil_div64(nnz, span);
