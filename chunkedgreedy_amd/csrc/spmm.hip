@@ -440,8 +440,9 @@ __global__ void __launch_bounds__(kSpmmBlock)
 // cut by a span edge is added into C with float atomics (those rows are
 // zeroed first), so a cut row's value depends on the order of the atomics:
 // within 1e-5 of the row-split result, not bit-identical.  Row ends come from
-// a window of G row pointers held in the group's lanes.  N > 4G is covered by
-// repeating the walk per column slice.
+// a window of G row pointers held in the group's lanes; empty rows are
+// skipped (the prepare launch zeroes them).  N > 4G is covered by repeating
+// the walk per column slice.
 template <int G>
 __global__ void __launch_bounds__(kSpmmBlock)
     spmm_merge_v4(int32_t n, int32_t nnz, const int32_t *__restrict__ ptr,
@@ -449,6 +450,7 @@ __global__ void __launch_bounds__(kSpmmBlock)
                   const float *__restrict__ B, float *__restrict__ C, int32_t span,
                   const int32_t *__restrict__ start_row) {
   constexpr int U = kSpmmDepth;
+  constexpr uint64_t kGroupMask = G == kWave ? ~0ull : ((1ull << G) - 1ull);
   const int lane = lane_id();
   const int sub = lane / G, gl = lane % G, gbase = sub * G;
   const int64_t wave = static_cast<int64_t>(blockIdx.x) * kSpmmWaves + threadIdx.x / kWave;
@@ -489,19 +491,37 @@ __global__ void __launch_bounds__(kSpmmBlock)
           }
         }
         if (ballot(fin) == 0) break;
-        const int32_t nrow = row + 1;
-        const bool next_ok = fin && re < p1 && nrow < n;
-        if (next_ok && nrow - wbase >= G) {
-          wbase = nrow;
-          win = ptr[wbase + 1 + gl < n ? wbase + 1 + gl : n];
+        // Next row of the span with nonzeros: the first row after `row` whose
+        // end passes re (empty rows in between were zeroed by the prepare
+        // launch).  The window moves on while it holds only empty rows; the
+        // span's nonzeros past re guarantee such a row before n.
+        bool seek = fin && re < p1;
+        int32_t after = row; // rows up to `after` are done
+        int32_t next = -1, nend = 0;
+        while (ballot(seek) != 0) {
+          if (seek && after + 1 - wbase >= G) {
+            wbase = after + 1;
+            win = ptr[wbase + 1 + gl < n ? wbase + 1 + gl : n];
+          }
+          const bool c = seek && gl >= after + 1 - wbase && win > re;
+          const uint64_t gm = (ballot(c) >> gbase) & kGroupMask;
+          const int32_t off = gm != 0 ? static_cast<int32_t>(__builtin_ctzll(gm)) : 0;
+          const int32_t wend = __shfl(win, gbase + off, kWave);
+          if (seek) {
+            if (gm != 0) {
+              next = wbase + off;
+              nend = wend;
+              seek = false;
+            } else {
+              after = wbase + G - 1;
+            }
+          }
         }
-        const int32_t idx = next_ok ? gbase + (nrow - wbase) : gbase;
-        const int32_t wend = __shfl(win, idx, kWave);
         if (fin) {
-          if (next_ok) {
-            rs = re;
-            re = wend;
-            row = nrow;
+          if (next >= 0) {
+            rs = re; // empty rows in between start and end there too
+            re = nend;
+            row = next;
             p = rs;
             e = re < p1 ? re : p1;
             acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
