@@ -10,11 +10,13 @@
 // chunk's row block alone, in LDS:
 //
 //   1. every nonzero (c, local row) becomes the key (c << lb) | local_row and is
-//      counting-sorted into NB buckets by a multiplicative hash of c (keys of
-//      one column share a bucket);
-//   2. each bucket is sorted by key: one thread per bucket (insertion sort)
-//      for small buckets, one wave per bucket (bitonic network in LDS) for
-//      large ones.  A column's keys are now one run, rows ascending;
+//      counting-sorted into buckets by a multiplicative hash of c (keys of one
+//      column share a bucket; about 8 keys per bucket, up to the tier's
+//      bucket capacity);
+//   2. each bucket is sorted by key: one thread per bucket for small buckets
+//      (a register bitonic network up to 16 keys, insertion sort up to 48),
+//      one wave per bucket (bitonic network in LDS) for large ones.  A
+//      column's keys are now one run, rows ascending;
 //   3. a row whose columns all occur once in the chunk has no candidates and
 //      gets the all-zero table row;
 //   3b. the rows are counting-sorted by floor(log2(row size)), largest
@@ -24,8 +26,9 @@
 //      and feeds the run's rows, ascending, to the wave64 sketch.
 //
 // The stream, and therefore the table, is identical to the reference's.
-// Two LDS tiers: up to 16384 nonzeros and 1024 rows per chunk (~74 KiB, two
-// workgroups per CU) and up to 32768 nonzeros and 4096 rows (~157 KiB).
+// Two LDS tiers: up to 16384 nonzeros, 1024 rows and 2048 buckets per chunk
+// (~78 KiB, two workgroups per CU) and up to 32768 nonzeros, 4096 rows and
+// 1024 buckets (~157 KiB).
 // Larger chunks go to an overflow list for the global-CSC kernel.  Requires
 // ceil(log2 n) + ceil(log2 C) <= 32 (checked by the host).
 #include "common.hpp"
@@ -80,6 +83,36 @@ __device__ __forceinline__ int32_t lds_upper_bound(const uint32_t *keys, int32_t
   return lo;
 }
 
+// Sorts keys[lo, lo + sz) (sz <= S) in one thread's registers with a bitonic
+// network over S slots, padding with the largest key (equal keys are
+// interchangeable, so a real key equal to the padding is still placed right).
+template <int S>
+__device__ __forceinline__ void register_sort_keys(uint32_t *keys, int32_t lo, int32_t sz) {
+  uint32_t v[S];
+#pragma unroll
+  for (int i = 0; i < S; ++i) v[i] = i < sz ? keys[lo + i] : 0xFFFFFFFFu;
+#pragma unroll
+  for (int k = 2; k <= S; k <<= 1) {
+#pragma unroll
+    for (int j = k >> 1; j > 0; j >>= 1) {
+#pragma unroll
+      for (int i = 0; i < S; ++i) {
+        const int l = i ^ j;
+        if (l > i) {
+          const uint32_t a = v[i], c = v[l];
+          const bool asc = (i & k) == 0;
+          v[i] = asc ? min(a, c) : max(a, c);
+          v[l] = asc ? max(a, c) : min(a, c);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < S; ++i) {
+    if (i < sz) keys[lo + i] = v[i];
+  }
+}
+
 template <int CELLS, int KEYCAP, int ROWCAP, int NB_LOG2>
 __global__ void __launch_bounds__(kLocalThreads)
     chunk_local_sketch_kernel(int32_t n, int32_t k, int32_t chunk_size, int32_t lb,
@@ -118,9 +151,13 @@ __global__ void __launch_bounds__(kLocalThreads)
       if (tid == 0) overflow[atomicAdd(overflow_count, 1)] = chunk;
       continue; // uniform across the workgroup
     }
+    // Buckets for about 8 keys each (at most NB, at least 64).
+    int nbl = 6;
+    while (nbl < NB_LOG2 && (E >> (nbl + 3)) > 0) ++nbl;
+    const int32_t nb = 1 << nbl;
 
     // 1. Bucket counts (coalesced column reads) and row sizes.
-    for (int32_t b = tid; b < NB; b += kLocalThreads) s_bend[b] = 0;
+    for (int32_t b = tid; b < nb; b += kLocalThreads) s_bend[b] = 0;
     if (tid <= kClasses) s_class[tid] = 0;
     if (tid == 0) s_next_row = 0;
     for (int32_t r = tid; r < rows; r += kLocalThreads) {
@@ -129,13 +166,13 @@ __global__ void __launch_bounds__(kLocalThreads)
     }
     __syncthreads();
     for (int32_t i = tid; i < E; i += kLocalThreads) {
-      atomicAdd(&s_bend[bucket_of(static_cast<uint32_t>(col_ind[e0 + i]), NB_LOG2)], 1);
+      atomicAdd(&s_bend[bucket_of(static_cast<uint32_t>(col_ind[e0 + i]), nbl)], 1);
     }
     __syncthreads();
     // Exclusive scan of the counts (wave 0): s_bend[b] = start of bucket b.
     if (wave == 0) {
       int32_t carry = 0;
-      for (int32_t base = 0; base < NB; base += kWave) {
+      for (int32_t base = 0; base < nb; base += kWave) {
         const int32_t v = s_bend[base + lane];
         const int32_t incl = wave_incl_scan(v);
         s_bend[base + lane] = carry + incl - v;
@@ -151,15 +188,22 @@ __global__ void __launch_bounds__(kLocalThreads)
 #pragma unroll 4
       for (int32_t q = 0; q < len; ++q) {
         const uint32_t c = static_cast<uint32_t>(col_ind[rb + q]);
-        const int32_t slot = atomicAdd(&s_bend[bucket_of(c, NB_LOG2)], 1);
+        const int32_t slot = atomicAdd(&s_bend[bucket_of(c, nbl)], 1);
         s_keys[slot] = (c << lb) | static_cast<uint32_t>(r);
       }
     }
     __syncthreads();
-    // 2b. Sort each bucket: small ones by one thread (insertion sort) ...
-    for (int32_t b = tid; b < NB; b += kLocalThreads) {
-      const int32_t lo = b ? s_bend[b - 1] : 0, hi = s_bend[b];
-      if (hi - lo <= kSmallBucket) {
+    // 2b. Sort each bucket: up to 16 keys by one thread in registers (a
+    //     16-slot bitonic network), up to kSmallBucket by one thread in LDS
+    //     (insertion sort) ...
+    for (int32_t b0 = 0; b0 < nb; b0 += kLocalThreads) {
+      const int32_t b = b0 + tid;
+      const int32_t lo = (b < nb && b) ? s_bend[b - 1] : 0;
+      const int32_t hi = b < nb ? s_bend[b] : 0;
+      const int32_t sz = hi - lo;
+      if (sz <= 16) {
+        register_sort_keys<16>(s_keys, lo, sz);
+      } else if (sz <= kSmallBucket) {
         for (int32_t i = lo + 1; i < hi; ++i) {
           const uint32_t x = s_keys[i];
           int32_t j = i - 1;
@@ -172,7 +216,7 @@ __global__ void __launch_bounds__(kLocalThreads)
       }
     }
     // ... large ones by one wave each.
-    for (int32_t b = wave; b < NB; b += kLocalWaves) {
+    for (int32_t b = wave; b < nb; b += kLocalWaves) {
       const int32_t lo = b ? s_bend[b - 1] : 0, hi = s_bend[b];
       if (hi - lo > kSmallBucket) wave_sort_lds(s_keys + lo, hi - lo);
     }
@@ -249,7 +293,7 @@ __global__ void __launch_bounds__(kLocalThreads)
         int32_t a = 0, bnd = 0;
         if (p < re) {
           const uint32_t c = static_cast<uint32_t>(col_ind[p]);
-          const uint32_t bk = bucket_of(c, NB_LOG2);
+          const uint32_t bk = bucket_of(c, nbl);
           const int32_t blo = bk ? s_bend[bk - 1] : 0, bhi = s_bend[bk];
           const uint32_t base = c << lb;
           a = lds_lower_bound(s_keys, blo, bhi, base);
@@ -296,7 +340,7 @@ __global__ void __launch_bounds__(kLocalThreads)
 }
 
 // Tier parameters: (key capacity, row capacity, log2 buckets).
-constexpr int kT1Keys = 16384, kT1Rows = 1024, kT1Nb = 10;
+constexpr int kT1Keys = 16384, kT1Rows = 1024, kT1Nb = 11;
 constexpr int kT2Keys = 32768, kT2Rows = 4096, kT2Nb = 10;
 
 template <int CELLS, int KEYCAP, int ROWCAP, int NB_LOG2>
