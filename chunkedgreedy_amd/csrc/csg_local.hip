@@ -48,6 +48,8 @@ constexpr int kSmallBucket = 48;
 // Row classes of step 3b: clz(row size) in [0, 31] for rows with candidates,
 // kClasses for the others.
 constexpr int kClasses = 32;
+// Step 3's mark: larger than any bucket id (< 2048) or row index (< 4096).
+constexpr uint16_t kMultiMark = 0xFFFF;
 constexpr int kRowsPerThread = kLocalRowCap / kLocalThreads;
 
 __device__ __forceinline__ uint32_t bucket_of(uint32_t col, int nb_log2) {
@@ -124,12 +126,16 @@ __global__ void __launch_bounds__(kLocalThreads)
                               int32_t *__restrict__ overflow,
                               int32_t *__restrict__ overflow_count) {
   constexpr int NB = 1 << NB_LOG2;
+  static_assert(KEYCAP / (kSmallBucket + 1) <= ROWCAP, "large-bucket list must fit s_order");
+  static_assert(NB <= kMultiMark && ROWCAP <= kMultiMark, "kMultiMark must be unused");
   __shared__ uint32_t s_keys[KEYCAP];
   __shared__ int32_t s_bend[NB];      // after the scatter: end of bucket b
   __shared__ int32_t s_size[ROWCAP];
-  // Step 3: per-row "has a candidate" flags; from step 3b on: the chunk's
-  // rows in processing order.
+  // Step 2b: the buckets too large for one thread; step 3: per-row "has a
+  // candidate" marks (kMultiMark, a value no bucket id or row index takes);
+  // from step 3b on: the chunk's rows in processing order.
   __shared__ uint16_t s_order[ROWCAP];
+  __shared__ int32_t s_big_count;
   __shared__ int32_t s_class[kClasses + 1]; // counts, then cursors, per class
   __shared__ int32_t s_next_row;            // next entry of s_order to claim
 
@@ -140,6 +146,8 @@ __global__ void __launch_bounds__(kLocalThreads)
   const int64_t num_chunks = ceil_div64(n, chunk_size);
   const int64_t work = chunk_list ? *chunk_list_count : num_chunks;
 
+  for (int32_t r = threadIdx.x; r < ROWCAP; r += kLocalThreads) s_order[r] = 0;
+  __syncthreads();
   for (int64_t t = blockIdx.x; t < work; t += gridDim.x) {
     const int32_t chunk = chunk_list ? chunk_list[t] : static_cast<int32_t>(t);
     const int32_t cs = chunk * chunk_size;
@@ -159,10 +167,12 @@ __global__ void __launch_bounds__(kLocalThreads)
     // 1. Bucket counts (coalesced column reads) and row sizes.
     for (int32_t b = tid; b < nb; b += kLocalThreads) s_bend[b] = 0;
     if (tid <= kClasses) s_class[tid] = 0;
-    if (tid == 0) s_next_row = 0;
+    if (tid == 0) {
+      s_next_row = 0;
+      s_big_count = 0;
+    }
     for (int32_t r = tid; r < rows; r += kLocalThreads) {
       s_size[r] = row_ptr[cs + r + 1] - row_ptr[cs + r];
-      s_order[r] = 0;
     }
     __syncthreads();
     for (int32_t i = tid; i < E; i += kLocalThreads) {
@@ -213,12 +223,17 @@ __global__ void __launch_bounds__(kLocalThreads)
           }
           s_keys[j + 1] = x;
         }
+      } else {
+        // At most KEYCAP / (kSmallBucket + 1) such buckets: fits s_order.
+        s_order[atomicAdd(&s_big_count, 1)] = static_cast<uint16_t>(b);
       }
     }
-    // ... large ones by one wave each.
-    for (int32_t b = wave; b < nb; b += kLocalWaves) {
+    __syncthreads();
+    // ... large ones by one wave each, from the list.
+    for (int32_t i = wave; i < s_big_count; i += kLocalWaves) {
+      const int32_t b = s_order[i];
       const int32_t lo = b ? s_bend[b - 1] : 0, hi = s_bend[b];
-      if (hi - lo > kSmallBucket) wave_sort_lds(s_keys + lo, hi - lo);
+      wave_sort_lds(s_keys + lo, hi - lo);
     }
     __syncthreads();
 
@@ -229,7 +244,7 @@ __global__ void __launch_bounds__(kLocalThreads)
       const uint32_t c = key >> lb;
       const bool multi = (i > 0 && (s_keys[i - 1] >> lb) == c) ||
                          (i + 1 < E && (s_keys[i + 1] >> lb) == c);
-      if (multi) s_order[key & rmask] = 1;
+      if (multi) s_order[key & rmask] = kMultiMark;
     }
     __syncthreads();
 
@@ -245,7 +260,7 @@ __global__ void __launch_bounds__(kLocalThreads)
       my_class[u] = -1;
       if (r < rows) {
         const int32_t sz = s_size[r];
-        my_class[u] = (s_order[r] != 0 && sz > 0) ? __clz(sz) : kClasses;
+        my_class[u] = (s_order[r] == kMultiMark && sz > 0) ? __clz(sz) : kClasses;
         atomicAdd(&s_class[my_class[u]], 1);
       }
     }
