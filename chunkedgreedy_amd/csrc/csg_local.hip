@@ -136,6 +136,7 @@ __global__ void __launch_bounds__(kLocalThreads)
   // from step 3b on: the chunk's rows in processing order.
   __shared__ uint16_t s_order[ROWCAP];
   __shared__ int32_t s_big_count;
+  __shared__ int32_t s_slice_total[kLocalWaves]; // step 1's scan
   __shared__ int32_t s_class[kClasses + 1]; // counts, then cursors, per class
   __shared__ int32_t s_next_row;            // next entry of s_order to claim
 
@@ -179,14 +180,29 @@ __global__ void __launch_bounds__(kLocalThreads)
       atomicAdd(&s_bend[bucket_of(static_cast<uint32_t>(col_ind[e0 + i]), nbl)], 1);
     }
     __syncthreads();
-    // Exclusive scan of the counts (wave 0): s_bend[b] = start of bucket b.
-    if (wave == 0) {
+    // Exclusive scan of the counts: s_bend[b] = start of bucket b.  Up to 16
+    // waves scan slices of 64 or more buckets, then add the totals of the
+    // slices before theirs.
+    {
+      const int32_t nw = nb / kWave < kLocalWaves ? nb / kWave : kLocalWaves;
+      const int32_t slice = nb / nw;
       int32_t carry = 0;
-      for (int32_t base = 0; base < nb; base += kWave) {
-        const int32_t v = s_bend[base + lane];
-        const int32_t incl = wave_incl_scan(v);
-        s_bend[base + lane] = carry + incl - v;
-        carry += readlane(incl, kWave - 1);
+      if (wave < nw) {
+        for (int32_t base = wave * slice; base < (wave + 1) * slice; base += kWave) {
+          const int32_t v = s_bend[base + lane];
+          const int32_t incl = wave_incl_scan(v);
+          s_bend[base + lane] = carry + incl - v;
+          carry += readlane(incl, kWave - 1);
+        }
+        if (lane == 0) s_slice_total[wave] = carry;
+      }
+      __syncthreads();
+      if (wave > 0 && wave < nw) {
+        int32_t before = 0;
+        for (int32_t w = 0; w < wave; ++w) before += s_slice_total[w];
+        for (int32_t base = wave * slice; base < (wave + 1) * slice; base += kWave) {
+          s_bend[base + lane] += before;
+        }
       }
     }
     __syncthreads();
