@@ -61,8 +61,23 @@ def many_huge_matrix(n=60000, seed=9):
     return ptr.astype(np.int32), ind.astype(np.int32), val
 
 
+def skewed_matrix(n=50000, seed=10):
+    """80 % of rows with 0..4 entries, 20 % with 60..120: a mean past 16, so
+    rows of at most 4 entries take the one-lane pass of the permutation."""
+    rng = np.random.default_rng(seed)
+    lens = np.where(rng.random(n) < 0.8, rng.integers(0, 5, size=n),
+                    rng.integers(60, 121, size=n))
+    ptr = np.zeros(n + 1, np.int64)
+    np.cumsum(lens, out=ptr[1:])
+    assert ptr[-1] / n >= 17
+    ind = np.concatenate([np.sort(rng.choice(n, size=L, replace=False)) for L in lens])
+    val = rng.standard_normal(ind.shape[0]).astype(np.float32)
+    return ptr.astype(np.int32), ind.astype(np.int32), val
+
+
 def mats():
     return {
+        "skewed": skewed_matrix(),
         "C1": synth.config1(21),
         "rmat12": synth.rmat(12, 16, 22),
         "stencil16": synth.stencil7(16, 23),
