@@ -224,8 +224,8 @@ __global__ void __launch_bounds__(kGreedyBlock)
   // Per-row count of valid entries inside the chunk (valid entries form a
   // prefix of each row; only in-chunk entries can be followed), read as a
   // coalesced sweep of the slice.  Rows that also hold out-of-chunk entries
-  // (global tables) are flagged in the bitmap, which the chain clears before
-  // it starts.  With counters, the in-chunk weight is summed for the cut
+  // (global tables) are flagged in the LDS bitmap; the chain keeps its own
+  // visited bitmap in registers.  With counters, the in-chunk weight is summed for the cut
   // statistic.
   double in_w = 0.0;
   for (int64_t e0 = static_cast<int64_t>(tid) * 4; e0 < slice_len;
@@ -316,16 +316,26 @@ __global__ void __launch_bounds__(kGreedyBlock)
     }
   }
   __syncthreads();
-  for (int32_t w = tid; w < words; w += kGreedyBlock) s_bm[w] = 0u;
-  __syncthreads();
   if (wave != 0) return;
 
+  // The chain runs on wave 0 with the visited bitmap in registers: lane l
+  // holds words l and 64 + l (chunks of at most kGreedyCompactRows = 4096
+  // rows need 128 words).  Cross-lane reads are shuffles issued by every lane
+  // (an inactive source lane would read as 0).
   const uint32_t tail_mask = (size & 31) ? ((1u << (size & 31)) - 1u) : 0xFFFFFFFFu;
+  uint32_t bm0 = 0u, bm1 = 0u;
+  auto full_bits = [&](int32_t w) { return w == words - 1 ? tail_mask : 0xFFFFFFFFu; };
+  // Branch-free so that bm0 and bm1 stay registers (a selected reference
+  // would turn them into a scratch array).
+  auto mark_bits = [&](int32_t w, uint32_t bits) {
+    bm0 |= lane == w ? bits : 0u;
+    bm1 |= lane + kWave == w ? bits : 0u;
+  };
   int32_t cur = 0, pos = start, low_word = 0;
   int32_t restarts = 0, links = 0;
   float link_w = 0.0f;
   while (true) {
-    mark_visited(s_bm, cur);
+    mark_bits(cur >> 5, 1u << (cur & 31));
     if (lane == 0) order[pos] = start + cur;
     pos += 1;
     const int32_t d0 = s_off[cur], d1 = s_off[cur + 1];
@@ -335,29 +345,49 @@ __global__ void __launch_bounds__(kGreedyBlock)
       // Compacted: the row's in-chunk entries in LDS.  Otherwise the row's
       // valid prefix from the table, filtered to the chunk.
       const int32_t len = compact ? d1 - d0 : k;
-      for (int32_t j = lane; j < len; j += kWave) {
-        int32_t cl;
-        float w;
-        if (compact) {
-          uint64_t e = s_ent[d0 + j];
-          cl = static_cast<int32_t>(static_cast<uint32_t>(e));
-          w = wi_weight(e);
-        } else {
-          uint64_t e = slice[static_cast<size_t>(cur) * k + j];
-          int32_t c = wi_index(e);
-          if (c < 0) break; // valid entries form a prefix
-          cl = (c >= start && c < end) ? c - start : -1;
-          w = wi_weight(e);
+      bool open = true; // valid prefix not yet ended (table reads)
+      for (int32_t j0 = 0; j0 < len; j0 += kWave) {
+        const int32_t j = j0 + lane;
+        int32_t cl = -1;
+        float w = 0.0f;
+        if (j < len) {
+          if (compact) {
+            const uint64_t e = s_ent[d0 + j];
+            cl = static_cast<int32_t>(static_cast<uint32_t>(e));
+            w = wi_weight(e);
+          } else {
+            const uint64_t e = slice[static_cast<size_t>(cur) * k + j];
+            const int32_t c = wi_index(e);
+            if (c < 0) open = false; // valid entries form a prefix
+            cl = (open && c >= start && c < end) ? c - start : -1;
+            w = wi_weight(e);
+          }
         }
-        if (cl < 0) continue; // outside the chunk
-        if (s_bm[cl >> 5] & (1u << (cl & 31))) continue;
-        if (w > best_w || (w == best_w && cl < best_c)) {
+        const int32_t wi = cl >= 0 ? cl >> 5 : 0;
+        uint32_t word =
+            static_cast<uint32_t>(__shfl(static_cast<int32_t>(bm0), wi & (kWave - 1), kWave));
+        if (words > kWave) { // wave-uniform
+          const uint32_t v1 =
+              static_cast<uint32_t>(__shfl(static_cast<int32_t>(bm1), wi & (kWave - 1), kWave));
+          word = wi < kWave ? word : v1;
+        }
+        const bool cand = cl >= 0 && !((word >> (cl & 31)) & 1u);
+        if (cand && (w > best_w || (w == best_w && cl < best_c))) {
           best_w = w;
           best_c = cl;
         }
+        if (!compact && ballot(open) != ~0ull) break; // some lane passed the prefix
       }
-      wave_argmax(&best_w, &best_c);
-      best_c = __builtin_amdgcn_readfirstlane(best_c);
+      const uint64_t m = ballot(best_c >= 0);
+      if (m != 0 && (m & (m - 1)) == 0) {
+        // One lane holds a candidate: it is the best.
+        const int l = __builtin_ctzll(m);
+        best_w = readlane_f(best_w, l);
+        best_c = readlane(best_c, l);
+      } else {
+        wave_argmax(&best_w, &best_c);
+        best_c = __builtin_amdgcn_readfirstlane(best_c);
+      }
     }
     if (best_c >= 0) {
       links += 1;
@@ -371,11 +401,24 @@ __global__ void __launch_bounds__(kGreedyBlock)
     // restarts, in index order: emit them in one step.
     int32_t nxt = -1;
     while (true) {
-      nxt = next_unvisited(s_bm, words, tail_mask, &low_word);
-      if (nxt < 0) break;
-      const int32_t w = nxt >> 5;
-      const uint32_t free_bits =
-          ~s_bm[w] & (w == words - 1 ? tail_mask : 0xFFFFFFFFu);
+      // Lowest word at or after low_word with a free bit.
+      const uint32_t f0 =
+          (lane < words && lane >= low_word) ? (~bm0 & full_bits(lane)) : 0u;
+      const uint32_t f1 = (kWave + lane < words && kWave + lane >= low_word)
+                              ? (~bm1 & full_bits(kWave + lane))
+                              : 0u;
+      const uint64_t m0 = ballot(f0 != 0u), m1 = ballot(f1 != 0u);
+      int32_t w = -1;
+      uint32_t free_bits = 0u;
+      if (m0 != 0) {
+        w = __builtin_ctzll(m0);
+        free_bits = static_cast<uint32_t>(readlane(static_cast<int32_t>(f0), w));
+      } else if (m1 != 0) {
+        w = kWave + __builtin_ctzll(m1);
+        free_bits = static_cast<uint32_t>(readlane(static_cast<int32_t>(f1), w - kWave));
+      }
+      if (w < 0) break;
+      low_word = w;
       const int32_t r = w * 32 + (lane & 31);
       const bool free_here = lane < 32 && ((free_bits >> (lane & 31)) & 1u);
       const bool has_entries = free_here && s_off[r + 1] > s_off[r];
@@ -387,7 +430,7 @@ __global__ void __launch_bounds__(kGreedyBlock)
         if (lane < 32 && ((emit >> lane) & 1u)) {
           order[pos + __popc(emit & ((1u << lane) - 1u))] = start + r;
         }
-        s_bm[w] |= emit; // every lane writes the same value
+        mark_bits(w, emit);
         const int32_t m = __popc(emit);
         pos += m;
         restarts += m;
