@@ -60,7 +60,15 @@ struct Context {
   size_t lds_per_block = 0;
   Workspace ws;
   Workspace aux; // second grow-only buffer, for temporaries sized mid-call
-  hipEvent_t ev[8] = {};
+  // Two more streams (default priority) for independent kernels of one call,
+  // forked from and joined back into `stream` with the events below, so a
+  // synchronize of `stream` also waits for their work.
+  hipStream_t side[2] = {};
+  hipEvent_t fork_ev = nullptr;
+  hipEvent_t join_ev[2] = {};
+  // Pinned host words for small device-to-host readbacks.
+  int32_t *host_words = nullptr;
+  static constexpr int kHostWords = 16;
 
   void init();
   void destroy();
@@ -89,6 +97,22 @@ struct Context {
     int64_t g = work_blocks < cap ? work_blocks : cap;
     return static_cast<int>(g < 1 ? 1 : g);
   }
+};
+
+// Makes the work already queued on ctx.stream a prerequisite of side[i]
+// (fork) and the work queued on side[i] a prerequisite of ctx.stream (join).
+void fork_side(Context &ctx, int i);
+void join_side(Context &ctx, int i);
+
+// Routes the context's launches (which use ctx.stream) to `s` for the guard's
+// lifetime.  Code run under it must not synchronize or grow the workspace.
+struct OnStream {
+  Context &ctx;
+  hipStream_t saved;
+  OnStream(Context &c, hipStream_t s) : ctx(c), saved(c.stream) { c.stream = s; }
+  ~OnStream() { ctx.stream = saved; }
+  OnStream(const OnStream &) = delete;
+  OnStream &operator=(const OnStream &) = delete;
 };
 
 // Bytes a workspace request of `count` T's occupies (for reserve sums).
@@ -164,16 +188,22 @@ void chunk_sketch_top_k(Context &ctx, int32_t n, int32_t nnz, int32_t k, int32_t
                         const int32_t *d_chunk_count = nullptr);
 
 // Chunk-local variant: one workgroup per chunk with the chunk's transpose in
-// LDS.  Applicable when chunk_local_supported(n, chunk_size).  d_lists holds
-// 2*num_chunks int32 and d_counts 2 int32 (zeroed by the caller).  Chunks too
-// large for LDS are left unwritten and listed in *d_overflow[0 ..
-// **d_overflow_count) for the global-CSC kernel.
+// LDS.  Applicable when chunk_local_supported(n, chunk_size).
+// chunk_local_classify fills d_lists (2*num_chunks int32) and d_counts (2
+// int32): the chunks of LDS tier 2 in d_lists[0 .. d_counts[0]) and the chunks
+// too large for LDS in d_lists[num_chunks .. num_chunks + d_counts[1]), the
+// latter for chunk_sketch_top_k over the global CSC.  chunk_local_sketch_top_k
+// then writes the rows of tier-1 chunks (tiers & 1; chunk_size <= 1024) and of
+// the listed tier-2 chunks (tiers & 2); the two launches are independent and
+// may run on different streams.
 constexpr int kLocalRowCap = 4096;
 bool chunk_local_supported(int32_t n, int32_t chunk_size);
+void chunk_local_classify(Context &ctx, int32_t n, int32_t chunk_size, const int32_t *d_ptr,
+                          int32_t *d_lists, int32_t *d_counts);
 void chunk_local_sketch_top_k(Context &ctx, int32_t n, int32_t k, int32_t chunk_size,
                               int32_t m_capacity, const int32_t *d_ptr, const int32_t *d_ind,
-                              uint64_t *d_table, int32_t *d_lists, int32_t *d_counts,
-                              int32_t **d_overflow, int32_t **d_overflow_count);
+                              uint64_t *d_table, const int32_t *d_lists,
+                              const int32_t *d_counts, int tiers);
 
 // Degree / weight totals of a top-k table (reference
 // sporder/src/common/similarity_top_k.cu:120-172).

@@ -24,6 +24,11 @@ void fail_expect(const char *msg, const char *file, int line) {
 void Context::init() {
   SP_HIP(hipGetDevice(&device));
   SP_HIP(hipStreamCreate(&stream));
+  for (auto &s : side) SP_HIP(hipStreamCreate(&s));
+  SP_HIP(hipEventCreateWithFlags(&fork_ev, hipEventDisableTiming));
+  for (auto &e : join_ev) SP_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+  SP_HIP(hipHostMalloc(reinterpret_cast<void **>(&host_words), kHostWords * sizeof(int32_t),
+                       hipHostMallocDefault));
   SP_HIP(hipDeviceGetAttribute(&num_cus, hipDeviceAttributeMultiprocessorCount,
                                device));
   SP_HIP(hipDeviceGetAttribute(&max_threads_per_cu,
@@ -40,6 +45,7 @@ void Context::destroy() {
   SP_HIP(hipGetDevice(&cur));
   SP_HIP(hipSetDevice(device));
   SP_HIP(hipStreamSynchronize(stream));
+  for (auto &s : side) SP_HIP(hipStreamSynchronize(s));
   if (ws.base) {
     SP_HIP(hipFree(ws.base));
     ws.base = nullptr;
@@ -48,6 +54,10 @@ void Context::destroy() {
     SP_HIP(hipFree(aux.base));
     aux.base = nullptr;
   }
+  SP_HIP(hipHostFree(host_words));
+  for (auto &e : join_ev) SP_HIP(hipEventDestroy(e));
+  SP_HIP(hipEventDestroy(fork_ev));
+  for (auto &s : side) SP_HIP(hipStreamDestroy(s));
   SP_HIP(hipStreamDestroy(stream));
   SP_HIP(hipSetDevice(cur));
 }
@@ -102,6 +112,16 @@ void fill_u32(Context &ctx, void *p, int64_t count, uint32_t value) {
   fill_u32_kernel<<<g, 256, 0, ctx.stream>>>(static_cast<uint32_t *>(p), count,
                                              value);
   SP_LAUNCH_CHECK();
+}
+
+void fork_side(Context &ctx, int i) {
+  SP_HIP(hipEventRecord(ctx.fork_ev, ctx.stream));
+  SP_HIP(hipStreamWaitEvent(ctx.side[i], ctx.fork_ev, 0));
+}
+
+void join_side(Context &ctx, int i) {
+  SP_HIP(hipEventRecord(ctx.join_ev[i], ctx.side[i]));
+  SP_HIP(hipStreamWaitEvent(ctx.stream, ctx.join_ev[i], 0));
 }
 
 int bits_for(int64_t max_value) {

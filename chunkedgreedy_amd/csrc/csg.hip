@@ -569,7 +569,6 @@ void build_table(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
   const int64_t chunks = ceil_div64(n, chunk_size);
   int32_t *lists = ctx.take<int32_t>(2 * static_cast<size_t>(chunks));
   int32_t *counts = ctx.take<int32_t>(2);
-  int32_t *overflow = nullptr, *overflow_count = nullptr;
   const bool local = chunk_local_supported(n, chunk_size);
 
   auto global_csc = [&](const int32_t **cp, const int32_t **ri) {
@@ -597,35 +596,44 @@ void build_table(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
     return;
   }
 
-  fill_u32(ctx, counts, 2, 0u);
+  // Chunks are classified and the two list lengths read back; then the
+  // sketch paths that have work, which write disjoint table rows, run
+  // concurrently: tier 2 (mid-size chunks) on side stream 1, the global-CSC
+  // path (large chunks, whose hub rows set the critical path on power-law
+  // inputs) on side stream 0, tier 1 on the library stream.  Tier 2 is
+  // launched first so that its workgroups, which need a whole CU's LDS, are
+  // placed before tier 1 fills the CUs.  The transpose of a non-symmetric
+  // matrix is built only when the global path has chunks.
   t_sim->begin(ctx.stream);
-  chunk_local_sketch_top_k(ctx, n, k, chunk_size, m_cap, d_ptr, d_ind, table, lists, counts,
-                           &overflow, &overflow_count);
-  if (is_symmetric) {
-    // The CSR is its own transpose: run the fallback over the overflow list
-    // without waiting for its length (an empty list exits at once).
-    chunk_sketch_top_k(ctx, n, nnz, k, chunk_size, m_cap, d_ptr, d_ind, d_ptr, d_ind, table,
-                       overflow, overflow_count);
-    t_sim->end(ctx.stream);
-    t_csc->begin(ctx.stream);
-    t_csc->end(ctx.stream);
-    return;
-  }
-  t_sim->end(ctx.stream);
-  int32_t h_overflow = 0;
-  SP_HIP(hipMemcpyAsync(&h_overflow, overflow_count, sizeof(int32_t), hipMemcpyDeviceToHost,
+  chunk_local_classify(ctx, n, chunk_size, d_ptr, lists, counts);
+  int32_t *h_counts = ctx.host_words;
+  SP_HIP(hipMemcpyAsync(h_counts, counts, 2 * sizeof(int32_t), hipMemcpyDeviceToHost,
                         ctx.stream));
   ctx.sync();
-  t_csc->begin(ctx.stream);
-  if (h_overflow > 0) {
+  const bool run_t2 = h_counts[0] > 0, run_global = h_counts[1] > 0;
+  if (run_t2) {
+    fork_side(ctx, 1);
+    OnStream on(ctx, ctx.side[1]);
+    chunk_local_sketch_top_k(ctx, n, k, chunk_size, m_cap, d_ptr, d_ind, table, lists, counts,
+                             2);
+  }
+  if (run_global) {
+    fork_side(ctx, 0);
+    OnStream on(ctx, ctx.side[0]);
     const int32_t *cp, *ri;
+    t_csc->begin(ctx.stream);
     global_csc(&cp, &ri);
     t_csc->end(ctx.stream);
-    chunk_sketch_top_k(ctx, n, nnz, k, chunk_size, m_cap, d_ptr, d_ind, cp, ri, table, overflow,
-                       overflow_count);
+    chunk_sketch_top_k(ctx, n, nnz, k, chunk_size, m_cap, d_ptr, d_ind, cp, ri, table,
+                       lists + chunks, counts + 1);
   } else {
+    t_csc->begin(ctx.stream);
     t_csc->end(ctx.stream);
   }
+  chunk_local_sketch_top_k(ctx, n, k, chunk_size, m_cap, d_ptr, d_ind, table, lists, counts, 1);
+  if (run_t2) join_side(ctx, 1);
+  if (run_global) join_side(ctx, 0);
+  t_sim->end(ctx.stream);
 }
 
 

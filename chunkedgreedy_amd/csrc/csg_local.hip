@@ -157,7 +157,9 @@ __global__ void __launch_bounds__(kLocalThreads)
     const int32_t e0 = row_ptr[cs];
     const int32_t E = row_ptr[ce] - e0;
     if (E > KEYCAP || rows > ROWCAP) {
-      if (tid == 0) overflow[atomicAdd(overflow_count, 1)] = chunk;
+      // Another tier's chunk: listed here, or already listed by the
+      // classification when `overflow` is null.
+      if (tid == 0 && overflow != nullptr) overflow[atomicAdd(overflow_count, 1)] = chunk;
       continue; // uniform across the workgroup
     }
     // Buckets for about 8 keys each (at most NB, at least 64).
@@ -374,6 +376,99 @@ __global__ void __launch_bounds__(kLocalThreads)
 constexpr int kT1Keys = 16384, kT1Rows = 1024, kT1Nb = 11;
 constexpr int kT2Keys = 32768, kT2Rows = 4096, kT2Nb = 10;
 
+constexpr int kClassifyThreads = 1024;
+// Up to this many chunks one workgroup classifies and orders the lists,
+// holding kClassifyPer chunk sizes per thread in registers.
+constexpr int kClassifyPer = 8;
+constexpr int kClassifyOrderCap = kClassifyThreads * kClassifyPer;
+
+// Tier of a chunk of `rows` rows and E nonzeros: 1 and 2 are the LDS tiers
+// (1 only when t1 is set), 3 the global-CSC path.  The same tests as the
+// tier kernels' own.
+__device__ __forceinline__ int chunk_tier(int32_t E, int32_t rows, bool t1) {
+  if (t1 && E <= kT1Keys && rows <= kT1Rows) return 1;
+  if (E <= kT2Keys && rows <= kT2Rows) return 2;
+  return 3;
+}
+
+// Lists the chunks beyond tier 1: tier-2 chunks in lists[0 .. counts[0]),
+// global-path chunks in lists[chunks .. chunks + counts[1]).  With one
+// workgroup each list is ordered by floor(log2(nonzeros)), largest first (a
+// counting sort in LDS; order inside a class is arbitrary), so heavy chunks
+// start first, and counts are written, not added.  With several workgroups
+// (more than kClassifyOrderCap chunks) the lists are unordered and counts
+// must be zero on entry.  The table does not depend on list order.
+__global__ void __launch_bounds__(kClassifyThreads)
+    classify_chunks_kernel(int32_t n, int32_t chunk_size, int t1,
+                           const int32_t *__restrict__ row_ptr, int32_t *__restrict__ lists,
+                           int32_t *__restrict__ counts) {
+  __shared__ int32_t s_cls[2][kClasses + 1];
+  const int64_t chunks = ceil_div64(n, chunk_size);
+  const int tid = threadIdx.x, lane = lane_id();
+  auto chunk_of = [&](int64_t q, int32_t *E) {
+    const int64_t cs = q * chunk_size;
+    const int64_t ce = cs + chunk_size < n ? cs + chunk_size : n;
+    *E = row_ptr[ce] - row_ptr[cs];
+    return chunk_tier(*E, static_cast<int32_t>(ce - cs), t1 != 0);
+  };
+  if (gridDim.x > 1) {
+    for (int64_t q0 = static_cast<int64_t>(blockIdx.x) * kClassifyThreads; q0 < chunks;
+         q0 += static_cast<int64_t>(gridDim.x) * kClassifyThreads) {
+      const int64_t q = q0 + tid;
+      int32_t E = 0;
+      const int tier = q < chunks ? chunk_of(q, &E) : 1;
+#pragma unroll
+      for (int l = 0; l < 2; ++l) {
+        const uint64_t m = ballot(tier == l + 2);
+        int32_t base = 0;
+        if (m != 0 && lane == 0) base = atomicAdd(&counts[l], __popcll(m));
+        base = readlane(base, 0);
+        if (tier == l + 2) {
+          lists[l * chunks + base + __popcll(m & ((1ull << lane) - 1ull))] =
+              static_cast<int32_t>(q);
+        }
+      }
+    }
+    return;
+  }
+  for (int i = tid; i < 2 * (kClasses + 1); i += kClassifyThreads) (&s_cls[0][0])[i] = 0;
+  // Chunk tid + u * kClassifyThreads: its tier and its class 31 -
+  // floor(log2(E)) (ascending class = descending size; E = 0 always fits
+  // tier 1 or 2).
+  int tier[kClassifyPer], cls[kClassifyPer];
+#pragma unroll
+  for (int u = 0; u < kClassifyPer; ++u) {
+    const int64_t q = tid + static_cast<int64_t>(u) * kClassifyThreads;
+    int32_t E = 0;
+    tier[u] = q < chunks ? chunk_of(q, &E) : 1;
+    cls[u] = __clz(E > 0 ? E : 1);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int u = 0; u < kClassifyPer; ++u) {
+    if (tier[u] > 1) atomicAdd(&s_cls[tier[u] - 2][cls[u]], 1);
+  }
+  __syncthreads();
+  if (tid < 2) {
+    int32_t run = 0;
+    for (int c = 0; c <= kClasses; ++c) {
+      const int32_t v = s_cls[tid][c];
+      s_cls[tid][c] = run;
+      run += v;
+    }
+    counts[tid] = run;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int u = 0; u < kClassifyPer; ++u) {
+    if (tier[u] > 1) {
+      const int l = tier[u] - 2;
+      lists[l * chunks + atomicAdd(&s_cls[l][cls[u]], 1)] =
+          tid + u * kClassifyThreads;
+    }
+  }
+}
+
 template <int CELLS, int KEYCAP, int ROWCAP, int NB_LOG2>
 void launch_tier(Context &ctx, int32_t n, int32_t k, int32_t chunk_size, int32_t lb,
                  const int32_t *d_ptr, const int32_t *d_ind, uint64_t *d_table,
@@ -392,23 +487,15 @@ void launch_tier(Context &ctx, int32_t n, int32_t k, int32_t chunk_size, int32_t
 template <int CELLS>
 void launch_local(Context &ctx, int32_t n, int32_t k, int32_t chunk_size, int32_t lb,
                   const int32_t *d_ptr, const int32_t *d_ind, uint64_t *d_table,
-                  int32_t *lists, int32_t *counts, int32_t **final_list,
-                  int32_t **final_count) {
-  const int64_t chunks = ceil_div64(n, chunk_size);
-  int32_t *list_a = lists, *list_b = lists + chunks;
-  if (chunk_size <= kT1Rows) {
-    launch_tier<CELLS, kT1Keys, kT1Rows, kT1Nb>(ctx, n, k, chunk_size, lb, d_ptr, d_ind,
-                                                d_table, nullptr, nullptr, list_a, counts, 2);
+                  const int32_t *lists, const int32_t *counts, int tiers) {
+  if (tiers & 2) {
     launch_tier<CELLS, kT2Keys, kT2Rows, kT2Nb>(ctx, n, k, chunk_size, lb, d_ptr, d_ind,
-                                                d_table, list_a, counts, list_b, counts + 1,
-                                                1);
-  } else {
-    launch_tier<CELLS, kT2Keys, kT2Rows, kT2Nb>(ctx, n, k, chunk_size, lb, d_ptr, d_ind,
-                                                d_table, nullptr, nullptr, list_b, counts + 1,
-                                                1);
+                                                d_table, lists, counts, nullptr, nullptr, 1);
   }
-  *final_list = list_b;
-  *final_count = counts + 1;
+  if ((tiers & 1) && chunk_size <= kT1Rows) {
+    launch_tier<CELLS, kT1Keys, kT1Rows, kT1Nb>(ctx, n, k, chunk_size, lb, d_ptr, d_ind,
+                                                d_table, nullptr, nullptr, nullptr, nullptr, 2);
+  }
 }
 
 } // namespace
@@ -417,10 +504,25 @@ bool chunk_local_supported(int32_t n, int32_t chunk_size) {
   return chunk_size <= kLocalRowCap && bits_for(n - 1) + bits_for(chunk_size - 1) <= 32;
 }
 
+void chunk_local_classify(Context &ctx, int32_t n, int32_t chunk_size, const int32_t *d_ptr,
+                          int32_t *d_lists, int32_t *d_counts) {
+  SP_EXPECT(chunk_local_supported(n, chunk_size), "chunk-local sketch not applicable");
+  const int64_t chunks = ceil_div64(n, chunk_size);
+  const int t1 = chunk_size <= kT1Rows ? 1 : 0;
+  int grid = 1;
+  if (chunks > kClassifyOrderCap) {
+    grid = ctx.grid_for(ceil_div64(chunks, kClassifyThreads), kClassifyThreads, 1);
+    fill_u32(ctx, d_counts, 2, 0u);
+  }
+  classify_chunks_kernel<<<grid, kClassifyThreads, 0, ctx.stream>>>(n, chunk_size, t1, d_ptr,
+                                                                    d_lists, d_counts);
+  SP_LAUNCH_CHECK();
+}
+
 void chunk_local_sketch_top_k(Context &ctx, int32_t n, int32_t k, int32_t chunk_size,
                               int32_t m_capacity, const int32_t *d_ptr, const int32_t *d_ind,
-                              uint64_t *d_table, int32_t *d_lists, int32_t *d_counts,
-                              int32_t **d_overflow, int32_t **d_overflow_count) {
+                              uint64_t *d_table, const int32_t *d_lists,
+                              const int32_t *d_counts, int tiers) {
   SP_EXPECT(k <= 256, "k must be <= 256");
   SP_EXPECT(chunk_local_supported(n, chunk_size), "chunk-local sketch not applicable");
   const int32_t lb = bits_for(chunk_size - 1);
@@ -428,7 +530,7 @@ void chunk_local_sketch_top_k(Context &ctx, int32_t n, int32_t k, int32_t chunk_
 #define SP_CASE(C)                                                                       \
   case C:                                                                                \
     launch_local<C>(ctx, n, k, chunk_size, lb, d_ptr, d_ind, d_table, d_lists, d_counts, \
-                    d_overflow, d_overflow_count);                                       \
+                    tiers);                                                              \
     break;
     SP_CASE(1) SP_CASE(2) SP_CASE(3) SP_CASE(4) SP_CASE(5) SP_CASE(6)
     SP_CASE(7) SP_CASE(8) SP_CASE(9) SP_CASE(10) SP_CASE(11) SP_CASE(12)

@@ -277,6 +277,45 @@ def test_overflow_chunks_take_global_path(sporder, symmetric, chunk):
     assert np.array_equal(g.cpu().numpy(), o)
 
 
+def hub_matrix(n, deg, hubs, seed, symmetric):
+    """Random rows of `deg` columns plus hub rows {row: nonzeros}."""
+    rng = np.random.default_rng(seed)
+    rows = [np.repeat(np.arange(n), deg)]
+    cols = [rng.integers(0, n, size=n * deg)]
+    for r, d in hubs.items():
+        rows.append(np.full(d, r))
+        cols.append(rng.choice(n, size=d, replace=False))
+    rows, cols = np.concatenate(rows), np.concatenate(cols)
+    if symmetric:
+        rows, cols = np.concatenate([rows, cols]), np.concatenate([cols, rows])
+    keys = np.unique(rows.astype(np.int64) * n + cols)
+    r, c = keys // n, keys % n
+    ptr = np.zeros(n + 1, np.int64)
+    np.cumsum(np.bincount(r, minlength=n), out=ptr[1:])
+    return ptr.astype(np.int32), c.astype(np.int32)
+
+
+@pytest.mark.parametrize("symmetric", [False, True])
+def test_tier_lists_many_chunks(sporder, symmetric):
+    """More chunks than one classification workgroup orders (8192): the tier-2
+    and global-path lists are built by a grid of workgroups, and chunks of all
+    three tiers (hub rows of 7000 to 12000 nonzeros in chunks of 4 rows) are
+    sketched concurrently.  Bit-exact table and permutation."""
+    hubs = {5: 12000, 6: 9000, 20000: 12000, 20001: 12000, 20002: 10000, 39998: 7000}
+    ptr, ind = hub_matrix(40000, 8, hubs, 41, symmetric)
+    assert synth.is_pattern_symmetric(ptr, ind) == symmetric
+    chunk = 4
+    E = ptr[np.minimum(np.arange(0, 40000, chunk) + chunk, 40000)] - ptr[np.arange(0, 40000, chunk)]
+    assert E.size > 8192 and (E > 16384).any() and (E > 32768).any()
+    check_table(sporder, ptr, ind, 16, 4.0, chunk, symmetric)
+    dptr, dind = dev_csr(ptr, ind)
+    g = sporder.chunk_similarity_greedy(dptr, dind, is_symmetric=symmetric, k=16,
+                                        oversampling=4.0, chunk_size=chunk)
+    o, _ = oracle.chunk_similarity_greedy(ptr, ind, is_symmetric=symmetric, k=16,
+                                          oversampling=4.0, chunk_size=chunk)
+    assert np.array_equal(g.cpu().numpy(), o)
+
+
 def test_greedy_compact_overflow_entries(sporder):
     """A chunk whose top-k slice has more valid entries than the compact LDS
     capacity (2048) reads entries from global memory: same order."""
