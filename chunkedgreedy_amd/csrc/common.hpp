@@ -66,6 +66,7 @@ struct Context {
   hipStream_t side[2] = {};
   hipEvent_t fork_ev = nullptr;
   hipEvent_t join_ev[2] = {};
+  hipEvent_t prep_ev = nullptr; // a stage's preparation done (csg's global path)
   // Pinned host words for small device-to-host readbacks.
   int32_t *host_words = nullptr;
   static constexpr int kHostWords = 16;
@@ -178,14 +179,16 @@ void csr2csc(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
 
 // Chunk-restricted sketch + top-k table (u64 weighted_index, n*k) from the
 // global CSC.  With d_chunks non-null only the rows of the chunks listed in
-// d_chunks[0 .. *d_chunk_count) are computed.
+// d_chunks[0 .. *d_chunk_count) are computed.  `prepared`, when given, is
+// recorded once the run search is done and before the sketch launch.
 size_t chunk_sketch_ws_bytes(int32_t n, int32_t nnz, int32_t chunk_size);
 void chunk_sketch_top_k(Context &ctx, int32_t n, int32_t nnz, int32_t k, int32_t chunk_size,
                         int32_t m_capacity, const int32_t *d_ptr,
                         const int32_t *d_ind, const int32_t *d_col_ptr,
                         const int32_t *d_row_ind, uint64_t *d_table,
                         const int32_t *d_chunks = nullptr,
-                        const int32_t *d_chunk_count = nullptr);
+                        const int32_t *d_chunk_count = nullptr,
+                        hipEvent_t prepared = nullptr);
 
 // Chunk-local variant: one workgroup per chunk with the chunk's transpose in
 // LDS.  Applicable when chunk_local_supported(n, chunk_size).

@@ -27,6 +27,7 @@ void Context::init() {
   for (auto &s : side) SP_HIP(hipStreamCreate(&s));
   SP_HIP(hipEventCreateWithFlags(&fork_ev, hipEventDisableTiming));
   for (auto &e : join_ev) SP_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+  SP_HIP(hipEventCreateWithFlags(&prep_ev, hipEventDisableTiming));
   SP_HIP(hipHostMalloc(reinterpret_cast<void **>(&host_words), kHostWords * sizeof(int32_t),
                        hipHostMallocDefault));
   SP_HIP(hipDeviceGetAttribute(&num_cus, hipDeviceAttributeMultiprocessorCount,
@@ -55,6 +56,7 @@ void Context::destroy() {
     aux.base = nullptr;
   }
   SP_HIP(hipHostFree(host_words));
+  SP_HIP(hipEventDestroy(prep_ev));
   for (auto &e : join_ev) SP_HIP(hipEventDestroy(e));
   SP_HIP(hipEventDestroy(fork_ev));
   for (auto &s : side) SP_HIP(hipStreamDestroy(s));

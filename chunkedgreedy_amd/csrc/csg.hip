@@ -600,10 +600,13 @@ void build_table(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
   // sketch paths that have work, which write disjoint table rows, run
   // concurrently: tier 2 (mid-size chunks) on side stream 1, the global-CSC
   // path (large chunks, whose hub rows set the critical path on power-law
-  // inputs) on side stream 0, tier 1 on the library stream.  Tier 2 is
-  // launched first so that its workgroups, which need a whole CU's LDS, are
-  // placed before tier 1 fills the CUs.  The transpose of a non-symmetric
-  // matrix is built only when the global path has chunks.
+  // inputs) on side stream 0, tier 1 on the library stream.  Tier 1's
+  // workgroups take two per CU and leave no room for others, so it starts
+  // last: tier 2 (whose workgroups need a whole CU's LDS) is launched first,
+  // and tier 1 waits until the global path's run search is done and its
+  // sketch, whose first rows are the heaviest chunk's, is queued.  The
+  // transpose of a non-symmetric matrix is built only when the global path
+  // has chunks.
   t_sim->begin(ctx.stream);
   chunk_local_classify(ctx, n, chunk_size, d_ptr, lists, counts);
   int32_t *h_counts = ctx.host_words;
@@ -625,11 +628,12 @@ void build_table(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
     global_csc(&cp, &ri);
     t_csc->end(ctx.stream);
     chunk_sketch_top_k(ctx, n, nnz, k, chunk_size, m_cap, d_ptr, d_ind, cp, ri, table,
-                       lists + chunks, counts + 1);
+                       lists + chunks, counts + 1, ctx.prep_ev);
   } else {
     t_csc->begin(ctx.stream);
     t_csc->end(ctx.stream);
   }
+  if (run_global) SP_HIP(hipStreamWaitEvent(ctx.stream, ctx.prep_ev, 0));
   chunk_local_sketch_top_k(ctx, n, k, chunk_size, m_cap, d_ptr, d_ind, table, lists, counts, 1);
   if (run_t2) join_side(ctx, 1);
   if (run_global) join_side(ctx, 0);

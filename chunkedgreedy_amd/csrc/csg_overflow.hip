@@ -13,13 +13,15 @@
 // Four launches:
 //   1. plan (one workgroup): the listed chunks' nonzeros cut into tasks of
 //      kRunTask; exclusive task offsets per list entry.
-//   2. runs (one lane per nonzero of the listed chunks): the run [a, a + len)
-//      of the chunk's rows in the nonzero's column, by two binary searches.
-//      The searches of one row are spread over the whole device, so a hub row
+//   2. pairs (one lane per CSC entry): (row, |row|), so one 8-byte load gives
+//      an item's key and the operand of its weight; and every 16th CSC row
+//      index copied into a sample (nnz/16 words) for the run search.
+//   3. runs (one lane per nonzero of the listed chunks): the run [a, a + len)
+//      of the chunk's rows in the nonzero's column, by a binary search over
+//      the sample finished inside one 64-byte line, then a gallop.  The
+//      searches of one row are spread over the whole device, so a hub row
 //      with 600K columns costs 600K independent searches, not one wave's
 //      serial walk.
-//   3. pairs (one lane per CSC entry): (row, |row|), so one 8-byte load gives
-//      an item's key and the operand of its weight.
 //   4. sketch (one wave per row): walks the row's runs 64 nonzeros at a time
 //      with four blocks of runs in flight and item batches loaded one batch
 //      ahead, feeding the wave64 space-saving sketch (sketch.hpp).  An item's
@@ -33,10 +35,13 @@ namespace sporder_hip {
 namespace {
 
 constexpr int kRunTask = 1024;   // nonzeros per runs task
-constexpr int kPlanBlock = 1024;
+// One workgroup of 4 waves: small enough to be placed beside an LDS tier-2
+// workgroup, which leaves a CU too few wave slots for a 16-wave group.
+constexpr int kPlanBlock = 256;
 constexpr int kRunsBlock = 256;
 constexpr int kOvfBlock = 256;
 constexpr int kOvfWaves = kOvfBlock / kWave;
+constexpr int kSample = 16;      // run-search sample stride (one 64-byte line)
 
 __device__ __forceinline__ int64_t list_len(const int32_t *list, const int32_t *list_count,
                                             int64_t num_chunks) {
@@ -81,11 +86,28 @@ __global__ void __launch_bounds__(kPlanBlock)
   if (tid == 0) task_off[L] = s_carry;
 }
 
+// First index in [lo, hi) with a[i] >= t, for a sorted range of `a` whose
+// every kSample-th element (global positions 0, kSample, 2*kSample, ...) is
+// copied in `sample`: the search runs over the sample, a small array that
+// stays in cache, and ends inside one 64-byte line of `a`.
+__device__ __forceinline__ int32_t sampled_lower_bound(const int32_t *__restrict__ a,
+                                                       const int32_t *__restrict__ sample,
+                                                       int32_t lo, int32_t hi, int32_t t) {
+  if (hi - lo < 2 * kSample) return lower_bound_dev(a, lo, hi, t);
+  // Samples at positions inside [lo, hi): indices [s_lo, s_hi).
+  const int32_t s_lo = (lo + kSample - 1) / kSample, s_hi = (hi - 1) / kSample + 1;
+  const int32_t s = lower_bound_dev(sample, s_lo, s_hi, t);
+  // a[kSample*(s-1)] < t (when s > s_lo) and a[kSample*s] >= t (when s < s_hi).
+  const int32_t from = s > s_lo ? kSample * (s - 1) + 1 : lo;
+  const int32_t to = s < s_hi ? kSample * s : hi;
+  return lower_bound_dev(a, from, to, t);
+}
+
 __global__ void __launch_bounds__(kRunsBlock)
     ovf_runs_kernel(int32_t n, int32_t chunk_size, const int32_t *__restrict__ row_ptr,
                     const int32_t *__restrict__ col_ind, const int32_t *__restrict__ col_ptr,
-                    const int32_t *__restrict__ row_ind, const int32_t *__restrict__ list,
-                    const int32_t *__restrict__ list_count,
+                    const int32_t *__restrict__ row_ind, const int32_t *__restrict__ sample,
+                    const int32_t *__restrict__ list, const int32_t *__restrict__ list_count,
                     const int32_t *__restrict__ task_off, int2 *__restrict__ runs) {
   const int64_t L = list_len(list, list_count, ceil_div64(n, chunk_size));
   if (L == 0) return;
@@ -112,7 +134,7 @@ __global__ void __launch_bounds__(kRunsBlock)
     for (int64_t p = p0 + threadIdx.x; p < p1; p += kRunsBlock) {
       const int32_t c = col_ind[p];
       const int32_t b0 = col_ptr[c], b1 = col_ptr[c + 1];
-      const int32_t a = lower_bound_dev(row_ind, b0, b1, cs);
+      const int32_t a = sampled_lower_bound(row_ind, sample, b0, b1, cs);
       // The run of chunk rows is short next to the column: gallop from a.
       const int32_t b = gallop_lower_bound(row_ind, a, b1, ce);
       runs[p] = make_int2(a, b - a);
@@ -120,15 +142,19 @@ __global__ void __launch_bounds__(kRunsBlock)
   }
 }
 
+// pairs[t] = (row, |row|) of CSC entry t, and the run search's sample of
+// every kSample-th entry.
 __global__ void __launch_bounds__(256)
     ovf_pairs_kernel(int32_t nnz, const int32_t *__restrict__ row_ptr,
                      const int32_t *__restrict__ row_ind, const int32_t *__restrict__ list,
-                     const int32_t *__restrict__ list_count, int2 *__restrict__ pairs) {
+                     const int32_t *__restrict__ list_count, int2 *__restrict__ pairs,
+                     int32_t *__restrict__ sample) {
   if (list && *list_count == 0) return;
   for (int64_t t = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; t < nnz;
        t += static_cast<int64_t>(gridDim.x) * blockDim.x) {
     const int32_t s = row_ind[t];
     pairs[t] = make_int2(s, row_ptr[s + 1] - row_ptr[s]);
+    if (t % kSample == 0) sample[t / kSample] = s;
   }
 }
 
@@ -294,14 +320,14 @@ void launch_ovf_sketch(Context &ctx, int32_t n, int32_t k, int32_t chunk_size,
 size_t chunk_sketch_ws_bytes(int32_t n, int32_t nnz, int32_t chunk_size) {
   return 2 * ws_bytes<int2>(static_cast<size_t>(nnz)) +
          ws_bytes<int32_t>(static_cast<size_t>(ceil_div64(n, chunk_size)) + 1) +
-         ws_bytes<uint32_t>(1);
+         ws_bytes<uint32_t>(1) + ws_bytes<int32_t>(static_cast<size_t>(nnz) / kSample + 1);
 }
 
 void chunk_sketch_top_k(Context &ctx, int32_t n, int32_t nnz, int32_t k, int32_t chunk_size,
                         int32_t m_capacity, const int32_t *d_ptr, const int32_t *d_ind,
                         const int32_t *d_col_ptr, const int32_t *d_row_ind,
                         uint64_t *d_table, const int32_t *d_chunks,
-                        const int32_t *d_chunk_count) {
+                        const int32_t *d_chunk_count, hipEvent_t prepared) {
   SP_EXPECT(k <= 256, "k must be <= 256");
   SP_EXPECT(m_capacity % 32 == 0 && m_capacity >= 32 && m_capacity <= 512,
             "sketch capacity must be a multiple of 32 in [32, 512]");
@@ -310,20 +336,22 @@ void chunk_sketch_top_k(Context &ctx, int32_t n, int32_t nnz, int32_t k, int32_t
   int2 *pairs = ctx.take<int2>(static_cast<size_t>(nnz));
   int32_t *task_off = ctx.take<int32_t>(static_cast<size_t>(chunks) + 1);
   uint32_t *claim = ctx.take<uint32_t>(1);
+  int32_t *sample = ctx.take<int32_t>(static_cast<size_t>(nnz) / kSample + 1);
 
   ovf_plan_kernel<<<1, kPlanBlock, 0, ctx.stream>>>(n, chunk_size, d_ptr, d_chunks,
                                                     d_chunk_count, task_off);
   SP_LAUNCH_CHECK();
+  const int gp = ctx.grid_for(ceil_div64(nnz, 256), 256, 4);
+  ovf_pairs_kernel<<<gp, 256, 0, ctx.stream>>>(nnz, d_ptr, d_row_ind, d_chunks,
+                                               d_chunk_count, pairs, sample);
+  SP_LAUNCH_CHECK();
   const int64_t max_tasks = ceil_div64(nnz, kRunTask) + chunks;
   const int gr = ctx.grid_for(max_tasks, kRunsBlock, 4);
   ovf_runs_kernel<<<gr, kRunsBlock, 0, ctx.stream>>>(n, chunk_size, d_ptr, d_ind, d_col_ptr,
-                                                     d_row_ind, d_chunks, d_chunk_count,
-                                                     task_off, runs);
+                                                     d_row_ind, sample, d_chunks,
+                                                     d_chunk_count, task_off, runs);
   SP_LAUNCH_CHECK();
-  const int gp = ctx.grid_for(ceil_div64(nnz, 256), 256, 4);
-  ovf_pairs_kernel<<<gp, 256, 0, ctx.stream>>>(nnz, d_ptr, d_row_ind, d_chunks,
-                                               d_chunk_count, pairs);
-  SP_LAUNCH_CHECK();
+  if (prepared != nullptr) SP_HIP(hipEventRecord(prepared, ctx.stream));
   switch (m_capacity / 32) {
 #define SP_CASE(C)                                                                       \
   case C:                                                                                \
