@@ -115,8 +115,17 @@ __device__ __forceinline__ void register_sort_keys(uint32_t *keys, int32_t lo, i
   }
 }
 
+// Tier 1 (about 78 KiB of LDS) is sized for two workgroups per CU, which
+// needs 8 waves per SIMD and so at most 64 VGPRs; the bound asks the
+// compiler for that.  Capacities of 256 slots and more (CELLS >= 8) would
+// spill to scratch under it and keep one workgroup per CU instead.
+template <int CELLS, int KEYCAP>
+constexpr int local_min_waves() {
+  return (KEYCAP <= 16384 && CELLS <= 7) ? 8 : 1;
+}
+
 template <int CELLS, int KEYCAP, int ROWCAP, int NB_LOG2>
-__global__ void __launch_bounds__(kLocalThreads)
+__global__ void __launch_bounds__(kLocalThreads, (local_min_waves<CELLS, KEYCAP>()))
     chunk_local_sketch_kernel(int32_t n, int32_t k, int32_t chunk_size, int32_t lb,
                               const int32_t *__restrict__ row_ptr,
                               const int32_t *__restrict__ col_ind,
