@@ -125,7 +125,9 @@ __global__ void __launch_bounds__(kGreedyBlock)
   float link_w = 0.0f;
   double in_w = 0.0; // per lane
 
-  while (true) {
+  // One position of [start, end) per step; the bound only ends a walk whose
+  // bitmap went wrong before it could write past its chunk.
+  while (pos < end) {
     mark_visited(bm, cur - start);
     if (!use_lds) {
       // Global-memory bitmap: order the store before the loads that test it.
@@ -334,7 +336,10 @@ __global__ void __launch_bounds__(kGreedyBlock)
   int32_t cur = 0, pos = start, low_word = 0;
   int32_t restarts = 0, links = 0;
   float link_w = 0.0f;
-  while (true) {
+  // Every step writes one position of [start, end): the bound only ends a
+  // walk whose visited bitmap went wrong, before it could write past its
+  // chunk.
+  while (pos < end) {
     mark_bits(cur >> 5, 1u << (cur & 31));
     if (lane == 0) order[pos] = start + cur;
     pos += 1;
@@ -428,7 +433,10 @@ __global__ void __launch_bounds__(kGreedyBlock)
                                 : free_bits;
       if (emit) {
         if (lane < 32 && ((emit >> lane) & 1u)) {
-          order[pos + __popc(emit & ((1u << lane) - 1u))] = start + r;
+          // Bounded like the walk itself (a store predicate, not a second
+          // exit from this loop).
+          const int32_t at = pos + __popc(emit & ((1u << lane) - 1u));
+          if (at < end) order[at] = start + r;
         }
         mark_bits(w, emit);
         const int32_t m = __popc(emit);
