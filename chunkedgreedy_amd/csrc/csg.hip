@@ -29,6 +29,7 @@
 
 #include <algorithm>
 #include <chrono>
+#include <type_traits>
 
 namespace sporder_hip {
 
@@ -269,12 +270,16 @@ __global__ void __launch_bounds__(kGreedyBlock)
     if (lane == 0 && in_w != 0.0) atomicAdd(&counters->in_chunk_weight, in_w);
   }
   __syncthreads();
-  // Inclusive scan of s_off[1..size] by wave 0 -> offsets.
+  // Inclusive scan of s_off[1..size] by wave 0 -> offsets.  Wave 0 also
+  // counts the rows with exactly one in-chunk entry and those with any.
+  int32_t single_rows = 0, entry_rows = 0;
   if (wave == 0) {
     int32_t carry = 0;
     for (int32_t base = 1; base <= size; base += kWave) {
       int32_t i = base + lane;
       int32_t v = i <= size ? s_off[i] : 0;
+      single_rows += __popcll(ballot(v == 1));
+      entry_rows += __popcll(ballot(v > 0));
       int32_t incl = wave_incl_scan(v) + carry;
       if (i <= size) s_off[i] = incl;
       carry = readlane(incl, kWave - 1);
@@ -339,118 +344,149 @@ __global__ void __launch_bounds__(kGreedyBlock)
   // Every step writes one position of [start, end): the bound only ends a
   // walk whose visited bitmap went wrong, before it could write past its
   // chunk.
-  while (pos < end) {
-    mark_bits(cur >> 5, 1u << (cur & 31));
-    if (lane == 0) order[pos] = start + cur;
-    pos += 1;
-    const int32_t d0 = s_off[cur], d1 = s_off[cur + 1];
-    float best_w = -1.0f;
-    int32_t best_c = -1;
-    if (d1 > d0) {
-      // Compacted: the row's in-chunk entries in LDS.  Otherwise the row's
-      // valid prefix from the table, filtered to the chunk.
-      const int32_t len = compact ? d1 - d0 : k;
-      bool open = true; // valid prefix not yet ended (table reads)
-      for (int32_t j0 = 0; j0 < len; j0 += kWave) {
-        const int32_t j = j0 + lane;
-        int32_t cl = -1;
-        float w = 0.0f;
-        if (j < len) {
-          if (compact) {
-            const uint64_t e = s_ent[d0 + j];
-            cl = static_cast<int32_t>(static_cast<uint32_t>(e));
-            w = wi_weight(e);
-          } else {
-            const uint64_t e = slice[static_cast<size_t>(cur) * k + j];
-            const int32_t c = wi_index(e);
-            if (c < 0) open = false; // valid entries form a prefix
-            cl = (open && c >= start && c < end) ? c - start : -1;
-            w = wi_weight(e);
+  // The walk is compiled twice: with a path for rows of one in-chunk entry,
+  // taken when such rows are at least half of the rows with entries (mostly
+  // one-step links), and without it (a test of it on every step slowed walks
+  // over rows of many entries by about 7 %).
+  auto walk = [&](auto single_tag) {
+    constexpr bool kSingle = decltype(single_tag)::value;
+    while (pos < end) {
+      mark_bits(cur >> 5, 1u << (cur & 31));
+      if (lane == 0) order[pos] = start + cur;
+      pos += 1;
+      const int32_t d0 = s_off[cur], d1 = s_off[cur + 1];
+      float best_w = -1.0f;
+      int32_t best_c = -1;
+      if (d1 > d0) {
+        if (kSingle && d1 - d0 == 1) {
+          // One in-chunk entry (most rows that have any on scrambled inputs):
+          // every lane reads it from the same address, and its visited bit is a
+          // lane read of the bitmap word.
+          const uint64_t e = s_ent[d0];
+          const int32_t cl =
+              __builtin_amdgcn_readfirstlane(static_cast<int32_t>(static_cast<uint32_t>(e)));
+          if (cl >= 0 && cl < size) {
+            const int32_t w = cl >> 5;
+            const uint32_t word =
+                static_cast<uint32_t>(w < kWave ? readlane(static_cast<int32_t>(bm0), w)
+                                                : readlane(static_cast<int32_t>(bm1), w - kWave));
+            if (!((word >> (cl & 31)) & 1u)) {
+              best_c = cl;
+              best_w = wi_weight(e);
+            }
           }
-        }
-        const int32_t wi = cl >= 0 ? cl >> 5 : 0;
-        uint32_t word =
-            static_cast<uint32_t>(__shfl(static_cast<int32_t>(bm0), wi & (kWave - 1), kWave));
-        if (words > kWave) { // wave-uniform
-          const uint32_t v1 =
-              static_cast<uint32_t>(__shfl(static_cast<int32_t>(bm1), wi & (kWave - 1), kWave));
-          word = wi < kWave ? word : v1;
-        }
-        const bool cand = cl >= 0 && !((word >> (cl & 31)) & 1u);
-        if (cand && (w > best_w || (w == best_w && cl < best_c))) {
-          best_w = w;
-          best_c = cl;
-        }
-        if (!compact && ballot(open) != ~0ull) break; // some lane passed the prefix
+        } else {
+          // Compacted: the row's in-chunk entries in LDS.  Otherwise the row's
+          // valid prefix from the table, filtered to the chunk.
+          const int32_t len = compact ? d1 - d0 : k;
+          bool open = true; // valid prefix not yet ended (table reads)
+          for (int32_t j0 = 0; j0 < len; j0 += kWave) {
+            const int32_t j = j0 + lane;
+            int32_t cl = -1;
+            float w = 0.0f;
+            if (j < len) {
+              if (compact) {
+                const uint64_t e = s_ent[d0 + j];
+                cl = static_cast<int32_t>(static_cast<uint32_t>(e));
+                w = wi_weight(e);
+              } else {
+                const uint64_t e = slice[static_cast<size_t>(cur) * k + j];
+                const int32_t c = wi_index(e);
+                if (c < 0) open = false; // valid entries form a prefix
+                cl = (open && c >= start && c < end) ? c - start : -1;
+                w = wi_weight(e);
+              }
+            }
+            const int32_t wi = cl >= 0 ? cl >> 5 : 0;
+            uint32_t word =
+                static_cast<uint32_t>(__shfl(static_cast<int32_t>(bm0), wi & (kWave - 1), kWave));
+            if (words > kWave) { // wave-uniform
+              const uint32_t v1 =
+                  static_cast<uint32_t>(__shfl(static_cast<int32_t>(bm1), wi & (kWave - 1), kWave));
+              word = wi < kWave ? word : v1;
+            }
+            const bool cand = cl >= 0 && !((word >> (cl & 31)) & 1u);
+            if (cand && (w > best_w || (w == best_w && cl < best_c))) {
+              best_w = w;
+              best_c = cl;
+            }
+            if (!compact && ballot(open) != ~0ull) break; // some lane passed the prefix
+          }
+          const uint64_t m = ballot(best_c >= 0);
+          if (m != 0 && (m & (m - 1)) == 0) {
+            // One lane holds a candidate: it is the best.
+            const int l = __builtin_ctzll(m);
+            best_w = readlane_f(best_w, l);
+            best_c = readlane(best_c, l);
+          } else {
+            wave_argmax(&best_w, &best_c);
+            best_c = __builtin_amdgcn_readfirstlane(best_c);
+          }
+            }
       }
-      const uint64_t m = ballot(best_c >= 0);
-      if (m != 0 && (m & (m - 1)) == 0) {
-        // One lane holds a candidate: it is the best.
-        const int l = __builtin_ctzll(m);
-        best_w = readlane_f(best_w, l);
-        best_c = readlane(best_c, l);
-      } else {
-        wave_argmax(&best_w, &best_c);
-        best_c = __builtin_amdgcn_readfirstlane(best_c);
+      if (best_c >= 0) {
+        links += 1;
+        link_w += readlane_f(best_w, 0);
+        cur = best_c;
+        continue;
       }
+      // Restart.  The chain now visits the lowest unvisited row; a row with no
+      // table entries at all restarts again at once, so the free rows of one
+      // bitmap word below the first row that has entries are exactly the next
+      // restarts, in index order: emit them in one step.
+      int32_t nxt = -1;
+      while (true) {
+        // Lowest word at or after low_word with a free bit.
+        const uint32_t f0 =
+            (lane < words && lane >= low_word) ? (~bm0 & full_bits(lane)) : 0u;
+        const uint32_t f1 = (kWave + lane < words && kWave + lane >= low_word)
+                                ? (~bm1 & full_bits(kWave + lane))
+                                : 0u;
+        const uint64_t m0 = ballot(f0 != 0u), m1 = ballot(f1 != 0u);
+        int32_t w = -1;
+        uint32_t free_bits = 0u;
+        if (m0 != 0) {
+          w = __builtin_ctzll(m0);
+          free_bits = static_cast<uint32_t>(readlane(static_cast<int32_t>(f0), w));
+        } else if (m1 != 0) {
+          w = kWave + __builtin_ctzll(m1);
+          free_bits = static_cast<uint32_t>(readlane(static_cast<int32_t>(f1), w - kWave));
+        }
+        if (w < 0) break;
+        low_word = w;
+        const int32_t r = w * 32 + (lane & 31);
+        const bool free_here = lane < 32 && ((free_bits >> (lane & 31)) & 1u);
+        const bool has_entries = free_here && s_off[r + 1] > s_off[r];
+        const uint32_t with_entries = static_cast<uint32_t>(ballot(has_entries));
+        const uint32_t emit = with_entries
+                                  ? free_bits & ((with_entries & (0u - with_entries)) - 1u)
+                                  : free_bits;
+        if (emit) {
+          if (lane < 32 && ((emit >> lane) & 1u)) {
+            // Bounded like the walk itself (a store predicate, not a second
+            // exit from this loop).
+            const int32_t at = pos + __popc(emit & ((1u << lane) - 1u));
+            if (at < end) order[at] = start + r;
+          }
+          mark_bits(w, emit);
+          const int32_t m = __popc(emit);
+          pos += m;
+          restarts += m;
+        }
+        if (with_entries) {
+          nxt = w * 32 + __builtin_ctz(with_entries);
+          break;
+        }
+      }
+      if (nxt < 0) break;
+      restarts += 1;
+      cur = nxt;
     }
-    if (best_c >= 0) {
-      links += 1;
-      link_w += readlane_f(best_w, 0);
-      cur = best_c;
-      continue;
-    }
-    // Restart.  The chain now visits the lowest unvisited row; a row with no
-    // table entries at all restarts again at once, so the free rows of one
-    // bitmap word below the first row that has entries are exactly the next
-    // restarts, in index order: emit them in one step.
-    int32_t nxt = -1;
-    while (true) {
-      // Lowest word at or after low_word with a free bit.
-      const uint32_t f0 =
-          (lane < words && lane >= low_word) ? (~bm0 & full_bits(lane)) : 0u;
-      const uint32_t f1 = (kWave + lane < words && kWave + lane >= low_word)
-                              ? (~bm1 & full_bits(kWave + lane))
-                              : 0u;
-      const uint64_t m0 = ballot(f0 != 0u), m1 = ballot(f1 != 0u);
-      int32_t w = -1;
-      uint32_t free_bits = 0u;
-      if (m0 != 0) {
-        w = __builtin_ctzll(m0);
-        free_bits = static_cast<uint32_t>(readlane(static_cast<int32_t>(f0), w));
-      } else if (m1 != 0) {
-        w = kWave + __builtin_ctzll(m1);
-        free_bits = static_cast<uint32_t>(readlane(static_cast<int32_t>(f1), w - kWave));
-      }
-      if (w < 0) break;
-      low_word = w;
-      const int32_t r = w * 32 + (lane & 31);
-      const bool free_here = lane < 32 && ((free_bits >> (lane & 31)) & 1u);
-      const bool has_entries = free_here && s_off[r + 1] > s_off[r];
-      const uint32_t with_entries = static_cast<uint32_t>(ballot(has_entries));
-      const uint32_t emit = with_entries
-                                ? free_bits & ((with_entries & (0u - with_entries)) - 1u)
-                                : free_bits;
-      if (emit) {
-        if (lane < 32 && ((emit >> lane) & 1u)) {
-          // Bounded like the walk itself (a store predicate, not a second
-          // exit from this loop).
-          const int32_t at = pos + __popc(emit & ((1u << lane) - 1u));
-          if (at < end) order[at] = start + r;
-        }
-        mark_bits(w, emit);
-        const int32_t m = __popc(emit);
-        pos += m;
-        restarts += m;
-      }
-      if (with_entries) {
-        nxt = w * 32 + __builtin_ctz(with_entries);
-        break;
-      }
-    }
-    if (nxt < 0) break;
-    restarts += 1;
-    cur = nxt;
+  };
+  if (compact && 2 * single_rows >= entry_rows) {
+    walk(std::true_type{});
+  } else {
+    walk(std::false_type{});
   }
   if (counters != nullptr && lane == 0) {
     atomicAdd(&counters->restarts, restarts);
