@@ -187,6 +187,9 @@ __global__ void __launch_bounds__(kGreedyBlock)
 // entries keeps the offsets in LDS and reads the rows from global memory.
 constexpr int kGreedyCompactRows = 4096;
 
+// Walk modes of greedy_compact_kernel.
+constexpr int kWalkTable = 0, kWalkSingle = 1, kWalkAhead = 2;
+
 // Dynamic LDS layout: entries u64[entry_cap] | offsets i32[rows_cap + 1] |
 // bitmap u32[ceil(rows_cap / 32)].  A staged entry is (weight bits << 32) |
 // (slice position << 12) | local index: positions are below 4096 * 256 = 2^20
@@ -196,6 +199,9 @@ size_t greedy_compact_lds(int32_t rows_cap, int32_t entry_cap) {
          static_cast<size_t>((rows_cap + 31) / 32) * 4u;
 }
 
+// kStagePer: staged entries each thread moves to their rows (entry_cap is at
+// most kStagePer * kGreedyBlock).
+template <int kStagePer>
 __global__ void __launch_bounds__(kGreedyBlock)
     greedy_compact_kernel(int32_t n, int32_t k, int32_t chunk_size,
                           const uint64_t *__restrict__ table, int32_t *__restrict__ order,
@@ -294,7 +300,7 @@ __global__ void __launch_bounds__(kGreedyBlock)
     // among the row's in-chunk entries): j itself unless the row is flagged as
     // mixed.  Every thread takes its staged entries into registers before any
     // is overwritten.
-    constexpr int kPerThread = 8; // entry_cap <= kPerThread * kGreedyBlock
+    constexpr int kPerThread = kStagePer;
     uint64_t sv[kPerThread];
 #pragma unroll
     for (int q = 0; q < kPerThread; ++q) {
@@ -323,6 +329,27 @@ __global__ void __launch_bounds__(kGreedyBlock)
     }
   }
   __syncthreads();
+  if (compact) {
+    // Each row's entries into chain preference order: weight descending, then
+    // local index ascending.  Entries are (weight bits << 32) | local with
+    // positive weights, so with the low word flipped that order is the
+    // descending order of the 64-bit value.  Table rows are already in weight
+    // order, so the insertion sort only moves entries of equal weight.
+    for (int32_t r = tid; r < size; r += kGreedyBlock) {
+      const int32_t a = s_off[r], b = s_off[r + 1];
+      for (int32_t i = a + 1; i < b; ++i) {
+        const uint64_t x = s_ent[i];
+        const uint64_t kx = x ^ 0xFFFFFFFFull;
+        int32_t j = i;
+        while (j > a && (s_ent[j - 1] ^ 0xFFFFFFFFull) < kx) {
+          s_ent[j] = s_ent[j - 1];
+          --j;
+        }
+        s_ent[j] = x;
+      }
+    }
+    __syncthreads();
+  }
   if (wave != 0) return;
 
   // The chain runs on wave 0 with the visited bitmap in registers: lane l
@@ -344,17 +371,35 @@ __global__ void __launch_bounds__(kGreedyBlock)
   // Every step writes one position of [start, end): the bound only ends a
   // walk whose visited bitmap went wrong, before it could write past its
   // chunk.
-  // The walk is compiled twice: with a path for rows of one in-chunk entry,
-  // taken when such rows are at least half of the rows with entries (mostly
-  // one-step links), and without it (a test of it on every step slowed walks
-  // over rows of many entries by about 7 %).
-  auto walk = [&](auto single_tag) {
-    constexpr bool kSingle = decltype(single_tag)::value;
+  // The walk is compiled in three modes (a branch on the mode in every step
+  // cost up to 7 % on walks that did not use it):
+  //   kWalkTable   slices past the LDS capacity: rows read from the table;
+  //   kWalkSingle  compacted, at least half of the rows with entries have
+  //                exactly one (mostly one-step links): those take a
+  //                lane-read path;
+  //   kWalkAhead   compacted, rows of several entries: the next row's offsets
+  //                are read during the visited test.
+  auto walk = [&](auto mode_tag) {
+    constexpr int kMode = decltype(mode_tag)::value;
+    constexpr bool kSorted = kMode != kWalkTable; // rows compacted and sorted in LDS
+    constexpr bool kSingle = kMode == kWalkSingle;
+    constexpr bool kAhead = kMode == kWalkAhead;
+    // Offsets of the next row, read ahead by the step that chose it.
+    bool have_next = false;
+    int32_t nd0 = 0, nd1 = 0;
     while (pos < end) {
       mark_bits(cur >> 5, 1u << (cur & 31));
       if (lane == 0) order[pos] = start + cur;
       pos += 1;
-      const int32_t d0 = s_off[cur], d1 = s_off[cur + 1];
+      int32_t d0, d1;
+      if constexpr (kAhead) {
+        d0 = have_next ? nd0 : s_off[cur];
+        d1 = have_next ? nd1 : s_off[cur + 1];
+        have_next = false;
+      } else {
+        d0 = s_off[cur];
+        d1 = s_off[cur + 1];
+      }
       float best_w = -1.0f;
       int32_t best_c = -1;
       if (d1 > d0) {
@@ -375,27 +420,59 @@ __global__ void __launch_bounds__(kGreedyBlock)
               best_w = wi_weight(e);
             }
           }
+        } else if (kSorted) {
+          // The row's in-chunk entries in LDS, in preference order: the step
+          // takes the first unvisited one.  With read-ahead, every lane also
+          // reads its entry's row offsets while the visited bits are gathered,
+          // so the next step starts without an LDS read.  Staged local indices
+          // are below `size`, so both reads stay inside the offsets array.
+          const int32_t len = d1 - d0;
+          for (int32_t j0 = 0; j0 < len && best_c < 0; j0 += kWave) {
+            const int32_t j = j0 + lane;
+            int32_t cl = -1, o0 = 0, o1 = 0;
+            float w = 0.0f;
+            if (j < len) {
+              const uint64_t e = s_ent[d0 + j];
+              cl = static_cast<int32_t>(static_cast<uint32_t>(e));
+              w = wi_weight(e);
+              if constexpr (kAhead) {
+                o0 = s_off[cl];
+                o1 = s_off[cl + 1];
+              }
+            }
+            const int32_t wi = cl >= 0 ? cl >> 5 : 0;
+            uint32_t word =
+                static_cast<uint32_t>(__shfl(static_cast<int32_t>(bm0), wi & (kWave - 1), kWave));
+            if (words > kWave) { // wave-uniform
+              const uint32_t v1 =
+                  static_cast<uint32_t>(__shfl(static_cast<int32_t>(bm1), wi & (kWave - 1), kWave));
+              word = wi < kWave ? word : v1;
+            }
+            const uint64_t m = ballot(cl >= 0 && !((word >> (cl & 31)) & 1u));
+            if (m != 0) {
+              const int l = __builtin_ctzll(m);
+              best_c = readlane(cl, l);
+              best_w = readlane_f(w, l);
+              if constexpr (kAhead) {
+                nd0 = readlane(o0, l);
+                nd1 = readlane(o1, l);
+                have_next = true;
+              }
+            }
+          }
         } else {
-          // Compacted: the row's in-chunk entries in LDS.  Otherwise the row's
-          // valid prefix from the table, filtered to the chunk.
-          const int32_t len = compact ? d1 - d0 : k;
-          bool open = true; // valid prefix not yet ended (table reads)
-          for (int32_t j0 = 0; j0 < len; j0 += kWave) {
+          // The row's valid prefix from the table, filtered to the chunk.
+          bool open = true; // valid prefix not yet ended
+          for (int32_t j0 = 0; j0 < k; j0 += kWave) {
             const int32_t j = j0 + lane;
             int32_t cl = -1;
             float w = 0.0f;
-            if (j < len) {
-              if (compact) {
-                const uint64_t e = s_ent[d0 + j];
-                cl = static_cast<int32_t>(static_cast<uint32_t>(e));
-                w = wi_weight(e);
-              } else {
-                const uint64_t e = slice[static_cast<size_t>(cur) * k + j];
-                const int32_t c = wi_index(e);
-                if (c < 0) open = false; // valid entries form a prefix
-                cl = (open && c >= start && c < end) ? c - start : -1;
-                w = wi_weight(e);
-              }
+            if (j < k) {
+              const uint64_t e = slice[static_cast<size_t>(cur) * k + j];
+              const int32_t c = wi_index(e);
+              if (c < 0) open = false; // valid entries form a prefix
+              cl = (open && c >= start && c < end) ? c - start : -1;
+              w = wi_weight(e);
             }
             const int32_t wi = cl >= 0 ? cl >> 5 : 0;
             uint32_t word =
@@ -410,7 +487,7 @@ __global__ void __launch_bounds__(kGreedyBlock)
               best_w = w;
               best_c = cl;
             }
-            if (!compact && ballot(open) != ~0ull) break; // some lane passed the prefix
+            if (ballot(open) != ~0ull) break; // some lane passed the prefix
           }
           const uint64_t m = ballot(best_c >= 0);
           if (m != 0 && (m & (m - 1)) == 0) {
@@ -422,7 +499,7 @@ __global__ void __launch_bounds__(kGreedyBlock)
             wave_argmax(&best_w, &best_c);
             best_c = __builtin_amdgcn_readfirstlane(best_c);
           }
-            }
+        }
       }
       if (best_c >= 0) {
         links += 1;
@@ -483,10 +560,12 @@ __global__ void __launch_bounds__(kGreedyBlock)
       cur = nxt;
     }
   };
-  if (compact && 2 * single_rows >= entry_rows) {
-    walk(std::true_type{});
+  if (!compact) {
+    walk(std::integral_constant<int, kWalkTable>{});
+  } else if (2 * single_rows >= entry_rows) {
+    walk(std::integral_constant<int, kWalkSingle>{});
   } else {
-    walk(std::false_type{});
+    walk(std::integral_constant<int, kWalkAhead>{});
   }
   if (counters != nullptr && lane == 0) {
     atomicAdd(&counters->restarts, restarts);
@@ -739,15 +818,28 @@ SeriationOut seriate(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
 
   t_greedy.begin(ctx.stream);
   if (compact) {
-    // About 20 KiB of LDS per chunk at chain_chunk 1024: several chunks per CU.
-    const int32_t entry_cap = 2048; // at most 8 staged entries per thread
     // Staged entries pack the slice position in 20 bits.
     SP_EXPECT(static_cast<int64_t>(rows_max) * k <= (int64_t{1} << 20),
               "compact chain slice exceeds 2^20 entries");
-    greedy_compact_kernel<<<dim3(static_cast<unsigned>(num_chunks)), kGreedyBlock,
-                            greedy_compact_lds(rows_max, entry_cap), ctx.stream>>>(
-        n, k, chain_chunk, table, d_new_order, want_stats ? counters : nullptr, rows_max,
-        entry_cap);
+    // About 20 KiB of LDS per chunk at chain_chunk 1024, so that several chunks
+    // share a CU.  When there are at most two chunks per CU that LDS would sit
+    // idle: the wide variant stages up to 8192 entries (about 70 KiB), so that
+    // slices with several in-chunk entries per row still walk from LDS.
+    constexpr int32_t kNarrowCap = 8 * kGreedyBlock, kWideCap = 32 * kGreedyBlock;
+    const bool wide = num_chunks <= 2 * static_cast<int64_t>(ctx.num_cus) &&
+                      static_cast<int64_t>(rows_max) * k > kNarrowCap &&
+                      greedy_compact_lds(rows_max, kWideCap) <= ctx.lds_per_block;
+    const int32_t entry_cap = wide ? kWideCap : kNarrowCap;
+    const dim3 grid(static_cast<unsigned>(num_chunks));
+    const size_t lds = greedy_compact_lds(rows_max, entry_cap);
+    ChainCounters *cnt = want_stats ? counters : nullptr;
+    if (wide) {
+      greedy_compact_kernel<32><<<grid, kGreedyBlock, lds, ctx.stream>>>(
+          n, k, chain_chunk, table, d_new_order, cnt, rows_max, entry_cap);
+    } else {
+      greedy_compact_kernel<8><<<grid, kGreedyBlock, lds, ctx.stream>>>(
+          n, k, chain_chunk, table, d_new_order, cnt, rows_max, entry_cap);
+    }
     SP_LAUNCH_CHECK();
   } else {
     int64_t blocks = ceil_div64(num_chunks, general_wpb);

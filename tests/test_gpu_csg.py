@@ -318,12 +318,57 @@ def test_tier_lists_many_chunks(sporder, symmetric):
 
 def test_greedy_compact_overflow_entries(sporder):
     """A chunk whose top-k slice has more valid entries than the compact LDS
-    capacity (2048) reads entries from global memory: same order."""
+    capacity (8192 entries when there are few chunks) reads entries from
+    global memory: same order."""
     ptr, ind = dense_random(4096, 12, 32, True)
     for chunk in (4096, 4000):
         dptr, dind = dev_csr(ptr, ind)
         g, s = sporder.chunk_similarity_greedy(dptr, dind, is_symmetric=True, chunk_size=chunk,
                                                with_stats=True)
         o, os_ = oracle.chunk_similarity_greedy(ptr, ind, is_symmetric=True, chunk_size=chunk)
-        assert s["avg_degree"] * 4096 > 2048
+        assert s["avg_degree"] * 4096 > 8192
         assert np.array_equal(g.cpu().numpy(), o)
+
+
+def block_random(n, block, deg, seed):
+    """Symmetric pattern whose columns stay inside diagonal blocks of `block`
+    rows, so a row's table entries are rows of its own block."""
+    rng = np.random.default_rng(seed)
+    rows = np.repeat(np.arange(n), deg)
+    cols = (rows // block) * block + rng.integers(0, block, size=n * deg)
+    cols = np.minimum(cols, n - 1)
+    rows, cols = np.concatenate([rows, cols]), np.concatenate([cols, rows])
+    keys = np.unique(rows.astype(np.int64) * n + cols)
+    r, c = keys // n, keys % n
+    ptr = np.zeros(n + 1, np.int64)
+    np.cumsum(np.bincount(r, minlength=n), out=ptr[1:])
+    return ptr.astype(np.int32), c.astype(np.int32)
+
+
+def in_chunk_totals(ptr, ind, k, chunk):
+    n = ptr.shape[0] - 1
+    idx, _ = oracle.unpack_table(oracle.chunk_similarity_top_k(ptr, ind, k, chunk, 4.0, True))
+    inside = (idx >= 0) & (idx // chunk == np.arange(n)[:, None] // chunk)
+    return np.add.reduceat(inside.sum(1), np.arange(0, n, chunk))
+
+
+@pytest.mark.parametrize("case", ["few_chunks", "many_chunks"])
+def test_greedy_staging_capacity(sporder, case):
+    """Slices of 2049 to 8192 in-chunk entries: with at most two chunks per CU
+    the chain stages up to 8192 entries in LDS, with more chunks it stages
+    2048 and reads longer slices from global memory.  Same order either way."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    if case == "few_chunks":
+        chunk, n, block = 1024, 8 * 1024, 6
+    else:
+        chunk, n, block = 256, 256 * (2 * cus + 64), 24
+    print(f"[staging] {case} n={n} chunk={chunk} block={block} cus={cus}", flush=True)
+    ptr, ind = block_random(n, block, 4, 51)
+    tot = in_chunk_totals(ptr, ind, 16, chunk)
+    assert tot.min() > 2048 and tot.max() <= 8192
+    dptr, dind = dev_csr(ptr, ind)
+    g = sporder.chunk_similarity_greedy(dptr, dind, is_symmetric=True, k=16, oversampling=4.0,
+                                        chunk_size=chunk)
+    o, _ = oracle.chunk_similarity_greedy(ptr, ind, is_symmetric=True, k=16, oversampling=4.0,
+                                          chunk_size=chunk)
+    assert np.array_equal(g.cpu().numpy(), o)
