@@ -181,6 +181,9 @@ void csr2csc(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
 // global CSC.  With d_chunks non-null only the rows of the chunks listed in
 // d_chunks[0 .. *d_chunk_count) are computed.  `prepared`, when given, is
 // recorded once the run search is done and before the sketch launch.
+// d_row_valid, when given, receives each computed row's number of valid table
+// entries (the non-empty prefix of its table row, written with the row); rows
+// not computed are left as they are.
 size_t chunk_sketch_ws_bytes(int32_t n, int32_t nnz, int32_t chunk_size);
 void chunk_sketch_top_k(Context &ctx, int32_t n, int32_t nnz, int32_t k, int32_t chunk_size,
                         int32_t m_capacity, const int32_t *d_ptr,
@@ -188,7 +191,7 @@ void chunk_sketch_top_k(Context &ctx, int32_t n, int32_t nnz, int32_t k, int32_t
                         const int32_t *d_row_ind, uint64_t *d_table,
                         const int32_t *d_chunks = nullptr,
                         const int32_t *d_chunk_count = nullptr,
-                        hipEvent_t prepared = nullptr);
+                        hipEvent_t prepared = nullptr, int32_t *d_row_valid = nullptr);
 
 // Chunk-local variant: one workgroup per chunk with the chunk's transpose in
 // LDS.  Applicable when chunk_local_supported(n, chunk_size).
@@ -198,7 +201,7 @@ void chunk_sketch_top_k(Context &ctx, int32_t n, int32_t nnz, int32_t k, int32_t
 // latter for chunk_sketch_top_k over the global CSC.  chunk_local_sketch_top_k
 // then writes the rows of tier-1 chunks (tiers & 1; chunk_size <= 1024) and of
 // the listed tier-2 chunks (tiers & 2); the two launches are independent and
-// may run on different streams.
+// may run on different streams.  d_row_valid as for chunk_sketch_top_k.
 constexpr int kLocalRowCap = 4096;
 bool chunk_local_supported(int32_t n, int32_t chunk_size);
 void chunk_local_classify(Context &ctx, int32_t n, int32_t chunk_size, const int32_t *d_ptr,
@@ -206,7 +209,8 @@ void chunk_local_classify(Context &ctx, int32_t n, int32_t chunk_size, const int
 void chunk_local_sketch_top_k(Context &ctx, int32_t n, int32_t k, int32_t chunk_size,
                               int32_t m_capacity, const int32_t *d_ptr, const int32_t *d_ind,
                               uint64_t *d_table, const int32_t *d_lists,
-                              const int32_t *d_counts, int tiers);
+                              const int32_t *d_counts, int tiers,
+                              int32_t *d_row_valid = nullptr);
 
 // Degree / weight totals of a top-k table (reference
 // sporder/src/common/similarity_top_k.cu:120-172).

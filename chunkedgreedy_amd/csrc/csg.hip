@@ -191,12 +191,12 @@ constexpr int kGreedyCompactRows = 4096;
 constexpr int kWalkTable = 0, kWalkSingle = 1, kWalkAhead = 2;
 
 // Dynamic LDS layout: entries u64[entry_cap] | offsets i32[rows_cap + 1] |
-// bitmap u32[ceil(rows_cap / 32)].  A staged entry is (weight bits << 32) |
+// bitmap u32[ceil(rows_cap / 32)] | valid counts u8[rows_cap].  A staged entry is (weight bits << 32) |
 // (slice position << 12) | local index: positions are below 4096 * 256 = 2^20
 // and local indices below 4096.
 size_t greedy_compact_lds(int32_t rows_cap, int32_t entry_cap) {
   return static_cast<size_t>(entry_cap) * 8u + static_cast<size_t>(rows_cap + 1) * 4u +
-         static_cast<size_t>((rows_cap + 31) / 32) * 4u;
+         static_cast<size_t>((rows_cap + 31) / 32) * 4u + static_cast<size_t>(rows_cap);
 }
 
 // kStagePer: staged entries each thread moves to their rows (entry_cap is at
@@ -205,13 +205,16 @@ template <int kStagePer>
 __global__ void __launch_bounds__(kGreedyBlock)
     greedy_compact_kernel(int32_t n, int32_t k, int32_t chunk_size,
                           const uint64_t *__restrict__ table, int32_t *__restrict__ order,
-                          ChainCounters *counters, int32_t rows_cap, int32_t entry_cap) {
+                          ChainCounters *counters, int32_t rows_cap, int32_t entry_cap,
+                          const int32_t *__restrict__ row_valid) {
   extern __shared__ uint64_t smem_u64[];
   __shared__ int32_t s_total;
   __shared__ int32_t s_staged;
+  __shared__ int32_t s_valid;
   uint64_t *s_ent = smem_u64;
   int32_t *s_off = reinterpret_cast<int32_t *>(smem_u64 + entry_cap);
   uint32_t *s_bm = reinterpret_cast<uint32_t *>(s_off + rows_cap + 1);
+  uint8_t *s_rv = reinterpret_cast<uint8_t *>(s_bm + (rows_cap + 31) / 32);
 
   const int tid = threadIdx.x;
   const int lane = lane_id();
@@ -228,8 +231,28 @@ __global__ void __launch_bounds__(kGreedyBlock)
 
   for (int32_t r = tid; r <= size; r += kGreedyBlock) s_off[r] = 0;
   for (int32_t w = tid; w < words; w += kGreedyBlock) s_bm[w] = 0u;
-  if (tid == 0) s_staged = 0;
+  // The sketch's per-row valid counts (k <= 255), when given, and their sum.
+  if (tid == 0) {
+    s_staged = 0;
+    s_valid = 0;
+  }
   __syncthreads();
+  if (row_valid != nullptr) {
+    int32_t vsum = 0;
+    for (int32_t r = tid; r < size; r += kGreedyBlock) {
+      const int32_t c = min(max(row_valid[start + r], 0), k);
+      s_rv[r] = static_cast<uint8_t>(c);
+      vsum += c;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) vsum += __shfl_xor(vsum, off, kWave);
+    if (lane == 0 && vsum != 0) atomicAdd(&s_valid, vsum);
+  }
+  __syncthreads();
+  // A slice with under a quarter of its entries valid is read row by row, only
+  // each row's valid prefix (rows without entries cost no table traffic and a
+  // thread waits on one load per row); a denser one is swept whole, coalesced.
+  const bool by_rows = row_valid != nullptr && 4 * static_cast<int64_t>(s_valid) < slice_len;
   // Per-row count of valid entries inside the chunk (valid entries form a
   // prefix of each row; only in-chunk entries can be followed), read as a
   // coalesced sweep of the slice.  Rows that also hold out-of-chunk entries
@@ -237,7 +260,37 @@ __global__ void __launch_bounds__(kGreedyBlock)
   // visited bitmap in registers.  With counters, the in-chunk weight is summed for the cut
   // statistic.
   double in_w = 0.0;
-  for (int64_t e0 = static_cast<int64_t>(tid) * 4; e0 < slice_len;
+  if (by_rows) {
+    // Same staging as the sweep below, one lane per row: per-lane LDS atomics
+    // (few entries), slice positions below 2^20 (checked by the host).
+    for (int32_t r = tid; r < size; r += kGreedyBlock) {
+      const int32_t rv = s_rv[r];
+      const uint64_t *row = slice + static_cast<size_t>(r) * k;
+      for (int32_t j0 = 0; j0 < rv; j0 += 4) {
+        uint64_t v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = j0 + u < rv ? row[j0 + u] : 0;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int32_t c = wi_index(v[u]); // an empty entry reads as -1
+          if (c < 0) continue;
+          if (c >= start && c < end) {
+            atomicAdd(&s_off[r + 1], 1);
+            in_w += wi_weight(v[u]);
+            const int32_t si = atomicAdd(&s_staged, 1);
+            if (si < entry_cap) {
+              s_ent[si] = (v[u] & 0xFFFFFFFF00000000ull) |
+                          (static_cast<uint64_t>(r * k + j0 + u) << 12) |
+                          static_cast<uint32_t>(c - start);
+            }
+          } else {
+            atomicOr(&s_bm[r >> 5], 1u << (r & 31));
+          }
+        }
+      }
+    }
+  }
+  for (int64_t e0 = static_cast<int64_t>(tid) * 4; !by_rows && e0 < slice_len;
        e0 += static_cast<int64_t>(kGreedyBlock) * 4) {
     uint64_t v[4];
 #pragma unroll
@@ -683,12 +736,13 @@ size_t table_ws_bytes(int32_t n, int32_t nnz, int32_t k, int32_t chunk_size,
   return b;
 }
 
-// Fills `table` (n*k) for the chunked sketch.  Records the transpose and
+// Fills `table` (n*k) for the chunked sketch, and `row_valid` (n, when given)
+// with each row's number of valid entries.  Records the transpose and
 // similarity spans when the spans are enabled.
 void build_table(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
                  const int32_t *d_ind, bool is_symmetric, int32_t k, int32_t m_cap,
                  int32_t chunk_size, uint64_t *table, EventSpan *t_csc,
-                 EventSpan *t_sim) {
+                 EventSpan *t_sim, int32_t *row_valid = nullptr) {
   const int64_t chunks = ceil_div64(n, chunk_size);
   int32_t *lists = ctx.take<int32_t>(2 * static_cast<size_t>(chunks));
   int32_t *counts = ctx.take<int32_t>(2);
@@ -714,7 +768,8 @@ void build_table(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
     global_csc(&cp, &ri);
     t_csc->end(ctx.stream);
     t_sim->begin(ctx.stream);
-    chunk_sketch_top_k(ctx, n, nnz, k, chunk_size, m_cap, d_ptr, d_ind, cp, ri, table);
+    chunk_sketch_top_k(ctx, n, nnz, k, chunk_size, m_cap, d_ptr, d_ind, cp, ri, table,
+                       nullptr, nullptr, nullptr, row_valid);
     t_sim->end(ctx.stream);
     return;
   }
@@ -741,7 +796,7 @@ void build_table(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
     fork_side(ctx, 1);
     OnStream on(ctx, ctx.side[1]);
     chunk_local_sketch_top_k(ctx, n, k, chunk_size, m_cap, d_ptr, d_ind, table, lists, counts,
-                             2);
+                             2, row_valid);
   }
   if (run_global) {
     fork_side(ctx, 0);
@@ -751,13 +806,14 @@ void build_table(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
     global_csc(&cp, &ri);
     t_csc->end(ctx.stream);
     chunk_sketch_top_k(ctx, n, nnz, k, chunk_size, m_cap, d_ptr, d_ind, cp, ri, table,
-                       lists + chunks, counts + 1, ctx.prep_ev);
+                       lists + chunks, counts + 1, ctx.prep_ev, row_valid);
   } else {
     t_csc->begin(ctx.stream);
     t_csc->end(ctx.stream);
   }
   if (run_global) SP_HIP(hipStreamWaitEvent(ctx.stream, ctx.prep_ev, 0));
-  chunk_local_sketch_top_k(ctx, n, k, chunk_size, m_cap, d_ptr, d_ind, table, lists, counts, 1);
+  chunk_local_sketch_top_k(ctx, n, k, chunk_size, m_cap, d_ptr, d_ind, table, lists, counts, 1,
+                           row_valid);
   if (run_t2) join_side(ctx, 1);
   if (run_global) join_side(ctx, 0);
   t_sim->end(ctx.stream);
@@ -793,6 +849,19 @@ SeriationOut seriate(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
 
   size_t need = table_ws_bytes(n, nnz, k, sketch_chunk, is_symmetric) +
                 ws_bytes<ChainCounters>(1) + ws_bytes<TopKTotals>(1);
+  // About 20 KiB of LDS per chunk at chain_chunk 1024, so that several chunks
+  // share a CU.  When there are at most two chunks per CU that LDS would sit
+  // idle: the wide variant stages up to 8192 entries (about 70 KiB), so that
+  // slices with several in-chunk entries per row still walk from LDS.
+  constexpr int32_t kNarrowCap = 8 * kGreedyBlock, kWideCap = 32 * kGreedyBlock;
+  const bool wide = compact && num_chunks <= 2 * static_cast<int64_t>(ctx.num_cus) &&
+                    static_cast<int64_t>(rows_max) * k > kNarrowCap &&
+                    greedy_compact_lds(rows_max, kWideCap) <= ctx.lds_per_block;
+  // With many chunks the compact chain can stage only the valid prefix of each
+  // table row, from the counts the sketch writes (held as bytes in LDS); a
+  // launch of a few chunks is latency-bound and does not use them.
+  const bool use_row_valid = compact && !wide && k <= 255;
+  if (use_row_valid) need += ws_bytes<int32_t>(static_cast<size_t>(n));
   if (!compact && !bitmap_lds) need += ws_bytes<uint32_t>(static_cast<size_t>(num_chunks) * words);
   ctx.reserve(need);
   uint64_t *table = ctx.take<uint64_t>(static_cast<size_t>(n) * k);
@@ -801,6 +870,7 @@ SeriationOut seriate(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
   uint32_t *gbitmap = (!compact && !bitmap_lds)
                           ? ctx.take<uint32_t>(static_cast<size_t>(num_chunks) * words)
                           : nullptr;
+  int32_t *row_valid = use_row_valid ? ctx.take<int32_t>(static_cast<size_t>(n)) : nullptr;
 
   EventSpan t_csc, t_sim, t_greedy;
   t_csc.create(want_timing);
@@ -813,7 +883,7 @@ SeriationOut seriate(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
   }
 
   build_table(ctx, n, nnz, d_ptr, d_ind, is_symmetric, k, m_cap, sketch_chunk, table, &t_csc,
-              &t_sim);
+              &t_sim, row_valid);
   if (want_stats) top_k_stats(ctx, n, k, table, totals);
 
   t_greedy.begin(ctx.stream);
@@ -821,24 +891,16 @@ SeriationOut seriate(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
     // Staged entries pack the slice position in 20 bits.
     SP_EXPECT(static_cast<int64_t>(rows_max) * k <= (int64_t{1} << 20),
               "compact chain slice exceeds 2^20 entries");
-    // About 20 KiB of LDS per chunk at chain_chunk 1024, so that several chunks
-    // share a CU.  When there are at most two chunks per CU that LDS would sit
-    // idle: the wide variant stages up to 8192 entries (about 70 KiB), so that
-    // slices with several in-chunk entries per row still walk from LDS.
-    constexpr int32_t kNarrowCap = 8 * kGreedyBlock, kWideCap = 32 * kGreedyBlock;
-    const bool wide = num_chunks <= 2 * static_cast<int64_t>(ctx.num_cus) &&
-                      static_cast<int64_t>(rows_max) * k > kNarrowCap &&
-                      greedy_compact_lds(rows_max, kWideCap) <= ctx.lds_per_block;
     const int32_t entry_cap = wide ? kWideCap : kNarrowCap;
     const dim3 grid(static_cast<unsigned>(num_chunks));
     const size_t lds = greedy_compact_lds(rows_max, entry_cap);
     ChainCounters *cnt = want_stats ? counters : nullptr;
     if (wide) {
       greedy_compact_kernel<32><<<grid, kGreedyBlock, lds, ctx.stream>>>(
-          n, k, chain_chunk, table, d_new_order, cnt, rows_max, entry_cap);
+          n, k, chain_chunk, table, d_new_order, cnt, rows_max, entry_cap, row_valid);
     } else {
       greedy_compact_kernel<8><<<grid, kGreedyBlock, lds, ctx.stream>>>(
-          n, k, chain_chunk, table, d_new_order, cnt, rows_max, entry_cap);
+          n, k, chain_chunk, table, d_new_order, cnt, rows_max, entry_cap, row_valid);
     }
     SP_LAUNCH_CHECK();
   } else {

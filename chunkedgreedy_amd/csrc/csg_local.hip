@@ -133,7 +133,8 @@ __global__ void __launch_bounds__(kLocalThreads, (local_min_waves<CELLS, KEYCAP>
                               const int32_t *__restrict__ chunk_list,
                               const int32_t *__restrict__ chunk_list_count,
                               int32_t *__restrict__ overflow,
-                              int32_t *__restrict__ overflow_count) {
+                              int32_t *__restrict__ overflow_count,
+                              int32_t *__restrict__ row_valid) {
   constexpr int NB = 1 << NB_LOG2;
   static_assert(KEYCAP / (kSmallBucket + 1) <= ROWCAP, "large-bucket list must fit s_order");
   static_assert(NB <= kMultiMark && ROWCAP <= kMultiMark, "kMultiMark must be unused");
@@ -185,6 +186,9 @@ __global__ void __launch_bounds__(kLocalThreads, (local_min_waves<CELLS, KEYCAP>
     }
     for (int32_t r = tid; r < rows; r += kLocalThreads) {
       s_size[r] = row_ptr[cs + r + 1] - row_ptr[cs + r];
+      // Valid counts start at zero, one coalesced store per row; the wave
+      // that sketches a row overwrites its count after the barriers below.
+      if (row_valid != nullptr) row_valid[cs + r] = 0;
     }
     __syncthreads();
     for (int32_t i = tid; i < E; i += kLocalThreads) {
@@ -376,6 +380,7 @@ __global__ void __launch_bounds__(kLocalThreads, (local_min_waves<CELLS, KEYCAP>
         }
       }
       store.select_top_k(k, out);
+      if (row_valid != nullptr && lane == 0) row_valid[row] = min(k, store.filled);
     }
     __syncthreads(); // LDS is reused by the next chunk of this workgroup
   }
@@ -482,28 +487,32 @@ template <int CELLS, int KEYCAP, int ROWCAP, int NB_LOG2>
 void launch_tier(Context &ctx, int32_t n, int32_t k, int32_t chunk_size, int32_t lb,
                  const int32_t *d_ptr, const int32_t *d_ind, uint64_t *d_table,
                  const int32_t *list, const int32_t *list_count, int32_t *ovf,
-                 int32_t *ovf_count, int per_cu) {
+                 int32_t *ovf_count, int per_cu, int32_t *d_row_valid) {
   const int64_t chunks = ceil_div64(n, chunk_size);
   // A fixed grid striding over the work: no launch per chunk of an empty list.
   int64_t grid = list ? std::min<int64_t>(chunks, static_cast<int64_t>(ctx.num_cus) * per_cu)
                       : chunks;
   chunk_local_sketch_kernel<CELLS, KEYCAP, ROWCAP, NB_LOG2>
       <<<dim3(static_cast<unsigned>(grid)), kLocalThreads, 0, ctx.stream>>>(
-          n, k, chunk_size, lb, d_ptr, d_ind, d_table, list, list_count, ovf, ovf_count);
+          n, k, chunk_size, lb, d_ptr, d_ind, d_table, list, list_count, ovf, ovf_count,
+          d_row_valid);
   SP_LAUNCH_CHECK();
 }
 
 template <int CELLS>
 void launch_local(Context &ctx, int32_t n, int32_t k, int32_t chunk_size, int32_t lb,
                   const int32_t *d_ptr, const int32_t *d_ind, uint64_t *d_table,
-                  const int32_t *lists, const int32_t *counts, int tiers) {
+                  const int32_t *lists, const int32_t *counts, int tiers,
+                  int32_t *d_row_valid) {
   if (tiers & 2) {
     launch_tier<CELLS, kT2Keys, kT2Rows, kT2Nb>(ctx, n, k, chunk_size, lb, d_ptr, d_ind,
-                                                d_table, lists, counts, nullptr, nullptr, 1);
+                                                d_table, lists, counts, nullptr, nullptr, 1,
+                                                d_row_valid);
   }
   if ((tiers & 1) && chunk_size <= kT1Rows) {
     launch_tier<CELLS, kT1Keys, kT1Rows, kT1Nb>(ctx, n, k, chunk_size, lb, d_ptr, d_ind,
-                                                d_table, nullptr, nullptr, nullptr, nullptr, 2);
+                                                d_table, nullptr, nullptr, nullptr, nullptr, 2,
+                                                d_row_valid);
   }
 }
 
@@ -531,7 +540,7 @@ void chunk_local_classify(Context &ctx, int32_t n, int32_t chunk_size, const int
 void chunk_local_sketch_top_k(Context &ctx, int32_t n, int32_t k, int32_t chunk_size,
                               int32_t m_capacity, const int32_t *d_ptr, const int32_t *d_ind,
                               uint64_t *d_table, const int32_t *d_lists,
-                              const int32_t *d_counts, int tiers) {
+                              const int32_t *d_counts, int tiers, int32_t *d_row_valid) {
   SP_EXPECT(k <= 256, "k must be <= 256");
   SP_EXPECT(chunk_local_supported(n, chunk_size), "chunk-local sketch not applicable");
   const int32_t lb = bits_for(chunk_size - 1);
@@ -539,7 +548,7 @@ void chunk_local_sketch_top_k(Context &ctx, int32_t n, int32_t k, int32_t chunk_
 #define SP_CASE(C)                                                                       \
   case C:                                                                                \
     launch_local<C>(ctx, n, k, chunk_size, lb, d_ptr, d_ind, d_table, d_lists, d_counts, \
-                    tiers);                                                              \
+                    tiers, d_row_valid);                                                 \
     break;
     SP_CASE(1) SP_CASE(2) SP_CASE(3) SP_CASE(4) SP_CASE(5) SP_CASE(6)
     SP_CASE(7) SP_CASE(8) SP_CASE(9) SP_CASE(10) SP_CASE(11) SP_CASE(12)

@@ -249,7 +249,8 @@ __global__ void __launch_bounds__(kOvfBlock)
                       const int32_t *__restrict__ row_ptr, const int2 *__restrict__ runs,
                       const int2 *__restrict__ pairs, uint64_t *__restrict__ table,
                       const int32_t *__restrict__ list,
-                      const int32_t *__restrict__ list_count, uint32_t *__restrict__ claim) {
+                      const int32_t *__restrict__ list_count, uint32_t *__restrict__ claim,
+                      int32_t *__restrict__ row_valid) {
   __shared__ RunLookup s_lookup[kOvfWaves];
   const int lane = lane_id();
   RunLookup *lk = &s_lookup[threadIdx.x / kWave];
@@ -274,6 +275,7 @@ __global__ void __launch_bounds__(kOvfBlock)
     const int32_t deg = re - rs;
     if (deg == 0) {
       for (int32_t j = lane; j < k; j += kWave) out[j] = 0;
+      if (row_valid != nullptr && lane == 0) row_valid[row] = 0;
       continue;
     }
     store.clear();
@@ -299,6 +301,7 @@ __global__ void __launch_bounds__(kOvfBlock)
       r3 = load_runs(runs, rs, re, blk + 7, lane);
     }
     store.select_top_k(k, out);
+    if (row_valid != nullptr && lane == 0) row_valid[row] = min(k, store.filled);
   }
 }
 
@@ -306,12 +309,12 @@ template <int CELLS>
 void launch_ovf_sketch(Context &ctx, int32_t n, int32_t k, int32_t chunk_size,
                        const int32_t *d_ptr, const int2 *runs, const int2 *pairs,
                        uint64_t *d_table, const int32_t *list, const int32_t *list_count,
-                       uint32_t *claim) {
+                       uint32_t *claim, int32_t *d_row_valid) {
   const int g = ctx.grid_for(ceil_div64(n, kOvfWaves), kOvfBlock, 4);
   fill_u32(ctx, claim, 1, 0u);
   ovf_sketch_kernel<CELLS><<<g, kOvfBlock, 0, ctx.stream>>>(n, k, chunk_size, d_ptr, runs,
                                                             pairs, d_table, list, list_count,
-                                                            claim);
+                                                            claim, d_row_valid);
   SP_LAUNCH_CHECK();
 }
 
@@ -327,7 +330,8 @@ void chunk_sketch_top_k(Context &ctx, int32_t n, int32_t nnz, int32_t k, int32_t
                         int32_t m_capacity, const int32_t *d_ptr, const int32_t *d_ind,
                         const int32_t *d_col_ptr, const int32_t *d_row_ind,
                         uint64_t *d_table, const int32_t *d_chunks,
-                        const int32_t *d_chunk_count, hipEvent_t prepared) {
+                        const int32_t *d_chunk_count, hipEvent_t prepared,
+                        int32_t *d_row_valid) {
   SP_EXPECT(k <= 256, "k must be <= 256");
   SP_EXPECT(m_capacity % 32 == 0 && m_capacity >= 32 && m_capacity <= 512,
             "sketch capacity must be a multiple of 32 in [32, 512]");
@@ -356,7 +360,7 @@ void chunk_sketch_top_k(Context &ctx, int32_t n, int32_t nnz, int32_t k, int32_t
 #define SP_CASE(C)                                                                       \
   case C:                                                                                \
     launch_ovf_sketch<C>(ctx, n, k, chunk_size, d_ptr, runs, pairs, d_table, d_chunks,   \
-                         d_chunk_count, claim);                                          \
+                         d_chunk_count, claim, d_row_valid);                             \
     break;
     SP_CASE(1) SP_CASE(2) SP_CASE(3) SP_CASE(4) SP_CASE(5) SP_CASE(6)
     SP_CASE(7) SP_CASE(8) SP_CASE(9) SP_CASE(10) SP_CASE(11) SP_CASE(12)

@@ -85,3 +85,35 @@ def test_cg_return_shapes_and_edges(sporder):
     with pytest.raises(ValueError):
         sporder.chunk_greedy(torch.zeros(1, dtype=torch.int32, device="cuda"),
                              torch.zeros(0, dtype=torch.int32, device="cuda"))
+
+
+def small_blocks(n, block, deg, seed):
+    """Symmetric pattern with columns inside diagonal blocks of `block` rows:
+    each row is similar to its block-mates only."""
+    rng = np.random.default_rng(seed)
+    rows = np.repeat(np.arange(n), deg)
+    cols = np.minimum((rows // block) * block + rng.integers(0, block, size=n * deg), n - 1)
+    rows, cols = np.concatenate([rows, cols]), np.concatenate([cols, rows])
+    keys = np.unique(rows.astype(np.int64) * n + cols)
+    r, c = keys // n, keys % n
+    ptr = np.zeros(n + 1, np.int64)
+    np.cumsum(np.bincount(r, minlength=n), out=ptr[1:])
+    return ptr.astype(np.int32), c.astype(np.int32)
+
+
+def test_cg_sparse_table_many_chunks(sporder):
+    """Global table with two or three valid entries per row and chain chunks
+    (64 rows) that cut blocks of 3: many chunks, so the chain stages each
+    row's valid prefix from the sketch's counts, including rows whose entries
+    fall partly outside their chunk.  Bit-exact permutation and restarts."""
+    ptr, ind = small_blocks(60000, 3, 3, 61)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    assert 60000 // 64 > 2 * cus
+    dptr, dind = dev_csr(ptr, ind)
+    order, stats = sporder.chunk_greedy(dptr, dind, is_symmetric=True, k=16, oversampling=4.0,
+                                        chunk_size=64, with_stats=True)
+    o_order, o_stats = oracle.chunk_greedy(ptr, ind, is_symmetric=True, k=16, oversampling=4.0,
+                                           chunk_size=64)
+    assert o_stats["avg_degree"] < 4.0
+    assert np.array_equal(order.cpu().numpy(), o_order)
+    assert stats["chain_restarts"] == o_stats["chain_restarts"]
