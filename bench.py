@@ -90,8 +90,8 @@ def main():
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the Chunked Greedy path has no multi-GPU "
-              "execution in this build (chunks shard by row range; see DESIGN.md)",
-              file=sys.stderr)
+              "execution in this build (its chunks would shard by row range, one range "
+              "per GPU)", file=sys.stderr)
         sys.exit(2)
 
     import torch
