@@ -177,6 +177,7 @@ def test_csg_headline_config_bit_exact(sporder):
     o_order, o_stats, o_table = oracle.chunk_similarity_greedy(ptr, ind, return_table=True)
     assert np.array_equal(order.cpu().numpy(), o_order)
     assert stats["chain_restarts"] == o_stats["chain_restarts"]
+    assert np.array_equal(sporder.chunk_similarity_greedy(dptr, dind).cpu().numpy(), o_order)
     gi, gw = sporder.chunk_similarity_top_k(dptr, dind, k=16, oversampling=4.0, chunk_size=1024)
     oi, ow = oracle.unpack_table(o_table)
     assert np.array_equal(gi.cpu().numpy(), oi)
@@ -210,6 +211,10 @@ def test_full_config_bit_exact(sporder, name):
     assert np.array_equal(order.cpu().numpy(), o_order)
     assert stats["chain_restarts"] == o_stats["chain_restarts"]
     assert stats["zero_degree_rows"] == o_stats["zero_degree_rows"]
+    # Without statistics the sketch leaves rows without entries unwritten and
+    # the chain reads the table through the valid counts: same permutation.
+    assert np.array_equal(
+        sporder.chunk_similarity_greedy(dptr, dind, is_symmetric=sym).cpu().numpy(), o_order)
 
     dval = torch.from_numpy(val).to("cuda:0")
     p2, i2, v2 = sporder.reorder(dptr, dind, order, val=dval, symmetric=True)
