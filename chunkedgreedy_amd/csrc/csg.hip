@@ -189,6 +189,14 @@ constexpr int kGreedyCompactRows = 4096;
 
 // Walk modes of greedy_compact_kernel.
 constexpr int kWalkTable = 0, kWalkSingle = 1, kWalkAhead = 2;
+// Compacted rows: the offsets array becomes row headers, the offset in the low
+// kOffBits bits (entries are at most 32 * kGreedyBlock) and the local index of
+// the row's first (preferred) entry above it (below kGreedyCompactRows).
+constexpr int kOffBits = 14;
+constexpr int32_t kOffMask = (1 << kOffBits) - 1;
+static_assert(32 * kGreedyBlock <= kOffMask && kGreedyCompactRows <= 4096 &&
+                  kOffBits + 12 <= 31,
+              "row header fields");
 
 // Dynamic LDS layout: entries u64[entry_cap] | offsets i32[rows_cap + 1] |
 // bitmap u32[ceil(rows_cap / 32)] | valid counts u8[rows_cap].  A staged entry is (weight bits << 32) |
@@ -402,6 +410,13 @@ __global__ void __launch_bounds__(kGreedyBlock)
       }
     }
     __syncthreads();
+    // Row headers (see kOffBits).  A row's offset bits never change, so reading
+    // the next row's offset while its header is written is safe.
+    for (int32_t r = tid; r < size; r += kGreedyBlock) {
+      const int32_t a = s_off[r], b = s_off[r + 1] & kOffMask;
+      if (b > a) s_off[r] = a | (static_cast<int32_t>(s_ent[a] & 0xFFFu) << kOffBits);
+    }
+    __syncthreads();
   }
   if (wave != 0) return;
 
@@ -444,34 +459,40 @@ __global__ void __launch_bounds__(kGreedyBlock)
       mark_bits(cur >> 5, 1u << (cur & 31));
       if (lane == 0) order[pos] = start + cur;
       pos += 1;
-      int32_t d0, d1;
+      int32_t h0, h1; // row headers of cur and cur + 1 (offsets for table reads)
       if constexpr (kAhead) {
-        d0 = have_next ? nd0 : s_off[cur];
-        d1 = have_next ? nd1 : s_off[cur + 1];
+        h0 = have_next ? nd0 : s_off[cur];
+        h1 = have_next ? nd1 : s_off[cur + 1];
         have_next = false;
       } else {
-        d0 = s_off[cur];
-        d1 = s_off[cur + 1];
+        h0 = s_off[cur];
+        h1 = s_off[cur + 1];
       }
+      const int32_t d0 = kSorted ? (h0 & kOffMask) : h0;
+      const int32_t d1 = kSorted ? (h1 & kOffMask) : h1;
       float best_w = -1.0f;
       int32_t best_c = -1;
       if (d1 > d0) {
-        if (kSingle && d1 - d0 == 1) {
-          // One in-chunk entry (most rows that have any on scrambled inputs):
-          // every lane reads it from the same address, and its visited bit is a
-          // lane read of the bitmap word.
-          const uint64_t e = s_ent[d0];
-          const int32_t cl =
-              __builtin_amdgcn_readfirstlane(static_cast<int32_t>(static_cast<uint32_t>(e)));
-          if (cl >= 0 && cl < size) {
-            const int32_t w = cl >> 5;
-            const uint32_t word =
-                static_cast<uint32_t>(w < kWave ? readlane(static_cast<int32_t>(bm0), w)
-                                                : readlane(static_cast<int32_t>(bm1), w - kWave));
-            if (!((word >> (cl & 31)) & 1u)) {
-              best_c = cl;
-              best_w = wi_weight(e);
-            }
+        // kWalkSingle: the row's first (preferred) entry comes with its header;
+        // its visited bit is a lane read of the bitmap word.  Weights are read
+        // only for the statistics.  (With read-ahead, taking the first entry
+        // this way would give up the next row's early header read: slower on
+        // rows of several entries.)
+        const int32_t c0 = __builtin_amdgcn_readfirstlane((h0 >> kOffBits) & 0xFFF);
+        bool first_free = false;
+        if constexpr (kSingle) {
+          const int32_t w0 = c0 >> 5;
+          const uint32_t word0 =
+              static_cast<uint32_t>(w0 < kWave ? readlane(static_cast<int32_t>(bm0), w0)
+                                               : readlane(static_cast<int32_t>(bm1), w0 - kWave));
+          first_free = c0 < size && !((word0 >> (c0 & 31)) & 1u);
+        }
+        if (kSingle && (first_free || d1 - d0 == 1)) {
+          // The first entry is the step's choice, or the row's only one and
+          // visited (most rows that have any on scrambled inputs have one).
+          if (first_free) {
+            best_c = c0;
+            if (counters != nullptr) best_w = wi_weight(s_ent[d0]);
           }
         } else if (kSorted) {
           // The row's in-chunk entries in LDS, in preference order: the step
@@ -586,7 +607,9 @@ __global__ void __launch_bounds__(kGreedyBlock)
         low_word = w;
         const int32_t r = w * 32 + (lane & 31);
         const bool free_here = lane < 32 && ((free_bits >> (lane & 31)) & 1u);
-        const bool has_entries = free_here && s_off[r + 1] > s_off[r];
+        const bool has_entries =
+            free_here && (kSorted ? (s_off[r + 1] & kOffMask) > (s_off[r] & kOffMask)
+                                  : s_off[r + 1] > s_off[r]);
         const uint32_t with_entries = static_cast<uint32_t>(ballot(has_entries));
         const uint32_t emit = with_entries
                                   ? free_bits & ((with_entries & (0u - with_entries)) - 1u)
