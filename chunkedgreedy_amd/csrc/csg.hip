@@ -21,9 +21,12 @@
 // Both produce the same table.
 //
 // Greedy: one wave per chunk.  For chunk_size <= kGreedyCompactRows the
-// chunk's table slice is compacted into LDS (valid entries only, with
-// per-row offsets) so the serial chain touches only LDS; otherwise the chain
-// reads the table in global memory.
+// chunk's in-chunk table entries are compacted into LDS (per-row offsets,
+// each row sorted into the chain's preference order, offsets turned into row
+// headers that carry the first entry) so the serial chain touches only LDS;
+// slices past the LDS capacity, and longer chunks, read the table in global
+// memory.  With many chunks the sketch also writes per-row valid counts, and
+// sparse slices are staged from them row by row.
 #include "common.hpp"
 #include "sketch.hpp"
 
