@@ -63,6 +63,24 @@ def pmc_traffic(kernel, n, nnz):
     return rec.get("bytes_per_launch")
 
 
+def host_cpu():
+    """(CPU model, os.cpu_count(), CPUs this process may run on)."""
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        usable = os.cpu_count() or 1
+    return model, os.cpu_count() or 1, usable
+
+
 def reorder_bytes(n, nnz, k, symmetric):
     b = 2 * (4 * (n + 1) + 4 * nnz) + 8 * n * k   # sketch: CSR + CSC reads, table write
     b += 8 * n * k + 4 * n                         # greedy: table read, order write
@@ -257,9 +275,14 @@ def main():
     if not args.no_cpu:
         import oracle
 
-        threads = min(os.cpu_count() or 1, 16)
+        # Every usable host CPU, unless OMP_NUM_THREADS sets the allotment (the
+        # GPU boxes set it to their per-GPU CPU share).
+        model, ncpu, usable = host_cpu()
+        threads = usable
+        if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+            threads = max(1, min(usable, int(os.environ["OMP_NUM_THREADS"])))
         oracle.set_num_threads(threads)
-        log(f"cpu baseline on {threads} threads")
+        log(f"cpu baseline on {threads} threads ({model}; {usable} usable of {ncpu})")
         cpu_reorder = []
         for _ in range(3):
             t1 = time.perf_counter()
@@ -268,18 +291,31 @@ def main():
         parity = bool(np.array_equal(o_order, order.cpu().numpy()))
         B_h = B128.cpu().numpy()
         p2h, i2h, v2h = (x.cpu().numpy() for x in reordered)
+        op, oi, ov = oracle.reorder(ptr_h, ind_h, o_order, val=val_h, symmetric=True)
+        apply_parity = bool(np.array_equal(op, p2h) and np.array_equal(oi, i2h)
+                            and np.array_equal(ov.view(np.uint32), v2h.view(np.uint32)))
         cpu_spmm = []
         for _ in range(3):
             t1 = time.perf_counter()
-            oracle.spmm_csr(p2h, i2h, v2h, B_h)
+            c_ref = oracle.spmm_csr(p2h, i2h, v2h, B_h)
             cpu_spmm.append((time.perf_counter() - t1) * 1e3)
         cs = statistics.median(cpu_spmm)
+        # The headline SpMM (reordered C2, N = 128, B seed 42) against the
+        # oracle's stated fmaf order, bit for bit.
+        c_gpu, _ = sporder.spmm_csr(p2, i2, v2, B128, ctx=ctx)
+        spmm_parity = bool(np.array_equal(c_gpu.cpu().numpy().view(np.uint32),
+                                          c_ref.view(np.uint32)))
+        del c_gpu, c_ref
+        log(f"cpu parity: permutation {parity}, apply {apply_parity}, spmm {spmm_parity}")
         cpu = {"value": round(spmm_bytes(n, nnz, 128) / (cs * 1e-3) / 1e9, 2), "unit": "GB/s",
                "cores": threads, "kind": "port",
                "sample": "full C2: oracle CSR SpMM N=128 on the reordered matrix (median of 3)"
                          "; csg reorder by the oracle on full C2 (median of 3)",
+               "cpu_model": model, "cpu_count": ncpu, "cpus_usable": usable,
                "reorder_ms": round(statistics.median(cpu_reorder), 2),
-               "spmm_ms": round(cs, 2), "permutation_bit_exact_vs_gpu": parity}
+               "spmm_ms": round(cs, 2), "permutation_bit_exact_vs_gpu": parity,
+               "reorder_apply_bit_exact_vs_gpu": apply_parity,
+               "spmm_bit_exact_vs_cpu": spmm_parity}
 
     out = {
         "metric": "reorder time (ms) + reordered vs original SpMM GB/s, N=32..256, 1 GPU",

@@ -20,8 +20,9 @@
 //     per row streams the runs into the sketch.
 // Both produce the same table.
 //
-// Greedy: one wave per chunk.  For chunk_size <= kGreedyCompactRows the
-// chunk's in-chunk table entries are compacted into LDS (per-row offsets,
+// Greedy: one wave per chunk.  For chunk_size <= kGreedyCompactRows (with at
+// most 2^20 table entries per chunk) the chunk's in-chunk table entries are
+// compacted into LDS (per-row offsets,
 // each row sorted into the chain's preference order, offsets turned into row
 // headers that carry the first entry) so the serial chain touches only LDS;
 // slices past the LDS capacity, and longer chunks, read the table in global
@@ -863,7 +864,12 @@ SeriationOut seriate(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
                      bool want_stats, bool want_timing) {
   const int64_t num_chunks = ceil_div64(n, chain_chunk);
   const int32_t rows_max = static_cast<int32_t>(std::min<int64_t>(chain_chunk, n));
-  const bool compact = rows_max <= kGreedyCompactRows;
+  // The compact chain packs a staged entry's slice position into 20 bits, so
+  // it takes chunks of at most kGreedyCompactRows rows whose slice holds at
+  // most 2^20 table entries (k up to 256 at 4096 rows); larger slices (k up
+  // to 512 is valid) take the general kernel.
+  const bool compact = rows_max <= kGreedyCompactRows &&
+                       static_cast<int64_t>(rows_max) * k <= (int64_t{1} << 20);
   const int32_t words = static_cast<int32_t>(ceil_div64(rows_max, 32));
   // General greedy: bitmap in LDS when small enough, else in the workspace.
   const size_t lds_need = static_cast<size_t>(words) * 4u;
@@ -914,9 +920,6 @@ SeriationOut seriate(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
 
   t_greedy.begin(ctx.stream);
   if (compact) {
-    // Staged entries pack the slice position in 20 bits.
-    SP_EXPECT(static_cast<int64_t>(rows_max) * k <= (int64_t{1} << 20),
-              "compact chain slice exceeds 2^20 entries");
     const int32_t entry_cap = wide ? kWideCap : kNarrowCap;
     const dim3 grid(static_cast<unsigned>(num_chunks));
     const size_t lds = greedy_compact_lds(rows_max, entry_cap);

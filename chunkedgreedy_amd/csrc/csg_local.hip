@@ -541,7 +541,7 @@ void chunk_local_sketch_top_k(Context &ctx, int32_t n, int32_t k, int32_t chunk_
                               int32_t m_capacity, const int32_t *d_ptr, const int32_t *d_ind,
                               uint64_t *d_table, const int32_t *d_lists,
                               const int32_t *d_counts, int tiers, int32_t *d_row_valid) {
-  SP_EXPECT(k <= 256, "k must be <= 256");
+  SP_EXPECT(k <= 512, "k must be <= 512");
   SP_EXPECT(chunk_local_supported(n, chunk_size), "chunk-local sketch not applicable");
   const int32_t lb = bits_for(chunk_size - 1);
   switch (m_capacity / 32) {

@@ -332,7 +332,7 @@ void chunk_sketch_top_k(Context &ctx, int32_t n, int32_t nnz, int32_t k, int32_t
                         uint64_t *d_table, const int32_t *d_chunks,
                         const int32_t *d_chunk_count, hipEvent_t prepared,
                         int32_t *d_row_valid) {
-  SP_EXPECT(k <= 256, "k must be <= 256");
+  SP_EXPECT(k <= 512, "k must be <= 512");
   SP_EXPECT(m_capacity % 32 == 0 && m_capacity >= 32 && m_capacity <= 512,
             "sketch capacity must be a multiple of 32 in [32, 512]");
   const int64_t chunks = ceil_div64(n, chunk_size);

@@ -177,7 +177,12 @@ template <int CELLS> struct WaveSketch {
       }
     }
     // k-way merge; lane (i & 63) keeps output entry i in register i >> 6.
-    uint64_t outv[4] = {0, 0, 0, 0};
+    // The row has k <= M = 32 * CELLS <= 64 * LC entries (m = (int)(k * ovs)
+    // >= k for ovs >= 1, and M rounds m up), so LC registers per lane hold the
+    // whole output row; entries past the last emitted one stay zero.
+    uint64_t outv[LC];
+#pragma unroll
+    for (int r = 0; r < LC; ++r) outv[r] = 0;
     for (int32_t i = 0; i < k; ++i) {
       bool live = lane < 32 && fk[0] != -1;
       if (ballot(live) == 0) break;
@@ -190,10 +195,10 @@ template <int CELLS> struct WaveSketch {
       const int winner = who;
       int32_t wk = readlane(fk[0], winner);
       float ww = readlane_f(fw[0], winner);
-      int slot = i >> 6;
+      int slot = i >> 6; // below LC: i < M
       if (lane == (i & 63)) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
+        for (int r = 0; r < LC; ++r) {
           if (r == slot) outv[r] = pack_wi(wk, ww);
         }
       }
@@ -208,8 +213,8 @@ template <int CELLS> struct WaveSketch {
       }
     }
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      int idx = r * 64 + lane;
+    for (int r = 0; r < LC; ++r) {
+      const int32_t idx = r * 64 + lane;
       if (idx < k) out[idx] = outv[r];
     }
   }

@@ -106,8 +106,10 @@ typedef struct {
   double cut_weight_fraction;
 } sporder_cg_stats_t;
 
-/* Global-sketch chunk greedy (sporder-cg).  Not built yet: aborts with a
- * diagnostic.  Reference: sporder.h:176-182. */
+/* Global-sketch chunk greedy (sporder-cg): the top-k table of the sketch over
+ * all rows (one chunk of n rows), then the csg greedy chain per chunk of
+ * chunk_size rows; cut_weight_fraction is the table weight leaving its chunk.
+ * Defaults as csg.  Reference: sporder.h:176-182, sporder/src/cg/. */
 SPORDER_API void sporder_chunk_greedy(sporder_context_t ctx, int32_t n,
                                       int32_t nnz, const int32_t *d_ptr,
                                       const int32_t *d_ind, bool is_symmetric,
@@ -173,8 +175,9 @@ sporder_reorder(sporder_context_t ctx, int32_t n, int32_t nnz,
                 sporder_reorder_mode_t mode, int32_t *d_ptr_new,
                 int32_t *d_ind_new, float *d_val_new);
 
-/* Pillar count.  Not built yet: aborts with a diagnostic.
- * Reference: sporder.h:276-279. */
+/* Pillar count: the number of distinct (window, column) pairs over windows of
+ * `height` consecutive rows; height 1 gives nnz for a CSR without duplicates.
+ * Reference: sporder.h:276-279, sporder/src/count_pillars.cu:11-85. */
 SPORDER_API void sporder_count_pillars(sporder_context_t ctx, int32_t n,
                                        int32_t nnz, const int32_t *d_ptr,
                                        const int32_t *d_ind, int32_t height,

@@ -601,6 +601,17 @@ void oracle_reorder(int32_t n, int32_t nnz, const int32_t *ptr_old,
 // crafted row whose value depends on the segment boundary
 // (tests/test_oracle_csr.py).
 // ---------------------------------------------------------------------------
+// part[j] = fmaf(a, b[j], part[j]) for j < N: one fused multiply-add per
+// element, so lane-wise vector FMAs give the same bits as the scalar loop.
+// Built for FMA-capable hosts and for a generic x86-64 one, chosen at load time.
+__attribute__((target_clones("fma", "default"))) static void
+fma_row(float a, const float *__restrict b, float *__restrict part, int32_t N) {
+#pragma omp simd
+  for (int32_t j = 0; j < N; ++j) {
+    part[j] = std::fmaf(a, b[j], part[j]);
+  }
+}
+
 void oracle_spmm_csr(int32_t n, const int32_t *ptr, const int32_t *ind,
                      const float *val, int32_t N, const float *B, float *C,
                      int32_t long_row, int32_t seg_len) {
@@ -616,11 +627,7 @@ void oracle_spmm_csr(int32_t n, const int32_t *ptr, const int32_t *ind,
         part[j] = 0.0f;
       }
       for (int32_t p = q0; p < q1; ++p) {
-        float a = val[p];
-        const float *brow = B + static_cast<size_t>(ind[p]) * N;
-        for (int32_t j = 0; j < N; ++j) {
-          part[j] = std::fmaf(a, brow[j], part[j]);
-        }
+        fma_row(val[p], B + static_cast<size_t>(ind[p]) * N, part.data(), N);
       }
       for (int32_t j = 0; j < N; ++j) {
         crow[j] = (q0 == s) ? part[j] : crow[j] + part[j];

@@ -55,6 +55,21 @@ def test_cg_permutation_bit_exact(sporder, name, k, ovs, chunk):
     assert timing["wall_ms"] >= timing["chunk_greedy_ms"] >= 0.0
 
 
+@pytest.mark.parametrize("k,ovs", [(512, 1.0), (257, 1.5)])
+def test_cg_large_k_wide_chunks(sporder, k, ovs):
+    """Chain chunks of 4096 rows with k past 256 (slices past 2^20 table
+    entries) read the table in global memory: bit-exact permutation."""
+    ptr, ind = MATS["chunglu5k"]
+    sym = synth.is_pattern_symmetric(ptr, ind)
+    dptr, dind = dev_csr(ptr, ind)
+    order, stats = sporder.chunk_greedy(dptr, dind, is_symmetric=sym, k=k, oversampling=ovs,
+                                        chunk_size=4096, with_stats=True)
+    o_order, o_stats = oracle.chunk_greedy(ptr, ind, is_symmetric=sym, k=k, oversampling=ovs,
+                                           chunk_size=4096)
+    assert np.array_equal(order.cpu().numpy(), o_order)
+    assert stats["chain_restarts"] == o_stats["chain_restarts"]
+
+
 def test_cg_single_chunk_equals_csg(sporder):
     ptr, ind = MATS["C1"]
     n = ptr.shape[0] - 1

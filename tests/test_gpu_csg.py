@@ -130,6 +130,26 @@ def test_csg_permutation_bit_exact(sporder, name, k, ovs, chunk):
     assert timing["wall_ms"] >= timing["chunk_greedy_ms"] >= 0.0
 
 
+@pytest.mark.parametrize("k,ovs", [(512, 1.0), (257, 1.5), (256, 2.0)])
+def test_csg_large_k_wide_chunks(sporder, k, ovs):
+    """Chunks of 4096 rows with k past 256: the slice holds more than 2^20
+    table entries, which the LDS-compacted chain cannot index, so the chain
+    reads the table in global memory; k = 256 is the largest that compacts.
+    Permutation and restart count bit-exact."""
+    for name in ("chunglu20k", "rmat13"):
+        ptr, ind = MATS[name]
+        sym = synth.is_pattern_symmetric(ptr, ind)
+        print(f"[csg-large-k] {name} k={k} ovs={ovs}", flush=True)
+        dptr, dind = dev_csr(ptr, ind)
+        order, stats = sporder.chunk_similarity_greedy(dptr, dind, is_symmetric=sym, k=k,
+                                                       oversampling=ovs, chunk_size=4096,
+                                                       with_stats=True)
+        o_order, o_stats = oracle.chunk_similarity_greedy(ptr, ind, is_symmetric=sym, k=k,
+                                                          oversampling=ovs, chunk_size=4096)
+        assert np.array_equal(order.cpu().numpy(), o_order)
+        assert stats["k_used"] == k and stats["chain_restarts"] == o_stats["chain_restarts"]
+
+
 def test_csg_return_shapes(sporder):
     ptr, ind = MATS["C1"]
     dptr, dind = dev_csr(ptr, ind)
@@ -169,8 +189,11 @@ def test_csg_rejects_bad_sizes(sporder):
 
 
 def test_csg_headline_config_bit_exact(sporder):
-    """Full C2 (n = 2^20, 16 nnz/row): permutation and table bit-exact."""
-    ptr, ind, _ = synth.config2(seed=2)
+    """Full C2 (n = 2^20, 16 nnz/row, seed 2: the bench's matrix): csg
+    permutation and table, then the symmetric permutation apply with values
+    (P A P^T) and the reordered SpMM at N = 32 and N = 128 (B = torch.randn,
+    seed 42, as the bench draws it), all bit-exact against the oracle."""
+    ptr, ind, val = synth.config2(seed=2)
     print("[csg] C2 full", flush=True)
     dptr, dind = dev_csr(ptr, ind)
     order, stats = sporder.chunk_similarity_greedy(dptr, dind, with_stats=True)
@@ -187,13 +210,27 @@ def test_csg_headline_config_bit_exact(sporder):
     g = order.cpu().numpy().reshape(-1, 1024)
     assert np.array_equal(np.sort(g, axis=1), np.arange(n).reshape(-1, 1024))
 
+    dval = torch.from_numpy(val).to("cuda:0")
+    p2, i2, v2 = sporder.reorder(dptr, dind, order, val=dval, symmetric=True)
+    op, oi, ov = oracle.reorder(ptr, ind, o_order, val=val, symmetric=True)
+    assert np.array_equal(p2.cpu().numpy(), op)
+    assert np.array_equal(i2.cpu().numpy(), oi)
+    assert np.array_equal(v2.cpu().numpy().view(np.uint32), ov.view(np.uint32))
+    for N in (32, 128):
+        gen = torch.Generator(device="cuda:0").manual_seed(42)
+        B = torch.randn((n, N), generator=gen, dtype=torch.float32, device="cuda:0")
+        C, _ = sporder.spmm_csr(p2, i2, v2, B)
+        ref = oracle.spmm_csr(op, oi, ov, B.cpu().numpy())
+        print(f"[csg] C2 full spmm N={N}", flush=True)
+        assert np.array_equal(C.cpu().numpy().view(np.uint32), ref.view(np.uint32)), N
+
 
 @pytest.mark.parametrize("name", ["C3", "C4", "C5"])
 def test_full_config_bit_exact(sporder, name):
     """Full-size power-law and mesh configurations (C3 R-MAT scale 22, C4 160^3
     stencil, C5 Chung-Lu with 613K-entry hubs): csg permutation and chain
-    restarts, the permutation apply with values, and the reordered SpMM at the
-    first of the configuration's widths, all bit-exact against the oracle."""
+    restarts, the permutation apply with values, and the reordered SpMM at
+    every width the configuration names, all bit-exact against the oracle."""
     import time
 
     gen = {"C3": synth.config3, "C4": synth.config4, "C5": synth.config5}[name]
@@ -211,8 +248,7 @@ def test_full_config_bit_exact(sporder, name):
     assert np.array_equal(order.cpu().numpy(), o_order)
     assert stats["chain_restarts"] == o_stats["chain_restarts"]
     assert stats["zero_degree_rows"] == o_stats["zero_degree_rows"]
-    # Without statistics the sketch leaves rows without entries unwritten and
-    # the chain reads the table through the valid counts: same permutation.
+    # Without statistics the chain runs without its counters: same permutation.
     assert np.array_equal(
         sporder.chunk_similarity_greedy(dptr, dind, is_symmetric=sym).cpu().numpy(), o_order)
 
@@ -225,13 +261,16 @@ def test_full_config_bit_exact(sporder, name):
     assert np.array_equal(i2.cpu().numpy(), oi)
     assert np.array_equal(v2.cpu().numpy().view(np.uint32), ov.view(np.uint32))
 
-    N = {"C3": 32, "C4": 16, "C5": 128}[name]
-    B = np.random.default_rng(42).standard_normal((ptr.shape[0] - 1, N)).astype(np.float32)
-    C, _ = sporder.spmm_csr(p2, i2, v2, torch.from_numpy(B).to("cuda:0"))
-    t0 = time.time()
-    ref = oracle.spmm_csr(op, oi, ov, B)
-    print(f"[full] {name} oracle spmm {time.time() - t0:.1f}s", flush=True)
-    assert np.array_equal(C.cpu().numpy().view(np.uint32), ref.view(np.uint32))
+    widths = {"C3": (32, 64, 256), "C4": (16, 32, 64, 128, 256), "C5": (128,)}[name]
+    n = ptr.shape[0] - 1
+    for N in widths:
+        B = np.random.default_rng(42).standard_normal((n, N)).astype(np.float32)
+        C, _ = sporder.spmm_csr(p2, i2, v2, torch.from_numpy(B).to("cuda:0"))
+        t0 = time.time()
+        ref = oracle.spmm_csr(op, oi, ov, B)
+        print(f"[full] {name} oracle spmm N={N} {time.time() - t0:.1f}s", flush=True)
+        assert np.array_equal(C.cpu().numpy().view(np.uint32), ref.view(np.uint32)), N
+        del B, C, ref
 
 
 GOLDEN = __import__("json").loads(
