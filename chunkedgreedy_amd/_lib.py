@@ -94,6 +94,8 @@ REORDER_SYMMETRIC = 1
 SPMM_AUTO = 0
 SPMM_ROW_SPLIT = 1
 SPMM_MERGE_PATH = 2
+SPMM_NOALLOC_SCRATCH_BYTES = 64 << 20  # SPORDER_SPMM_NOALLOC_SCRATCH_BYTES
+SPMM_NOALLOC_TOO_LARGE = 1             # SPORDER_SPMM_NOALLOC_TOO_LARGE
 
 # Every symbol include/sporder.h declares, with its ctypes signature.
 SIGNATURES = {
@@ -115,6 +117,7 @@ SIGNATURES = {
     "sporder_chunk_similarity_top_k": (
         [vp, i32, i32, vp, vp, ctypes.c_bool, i32, f32, i32, vp, vp], None),
     "sporder_spmm_csr": ([vp, i32, i32, vp, vp, vp, i32, vp, vp, i32, P(f32)], None),
+    "sporder_spmm_csr_noalloc": ([vp, i32, i32, vp, vp, vp, i32, vp, vp], i32),
 }
 
 _lib = None

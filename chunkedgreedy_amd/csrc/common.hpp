@@ -154,6 +154,10 @@ struct EventSpan {
 
 // ---- host-side stages shared between files -------------------------------
 
+// Takes, with `device` current, that device's address of the no-allocation
+// SpMM scratch (spmm.hip); called once per context creation.
+void spmm_noalloc_setup(int device);
+
 // In-place exclusive (inclusive=false) or inclusive scan of `count` int32
 // values; `tmp` must hold scan_tmp_elems(count) int32.
 size_t scan_tmp_elems(int64_t count);

@@ -39,6 +39,7 @@ void Context::init() {
   SP_HIP(hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock,
                                device));
   lds_per_block = static_cast<size_t>(lds);
+  spmm_noalloc_setup(device);
 }
 
 void Context::destroy() {

@@ -30,6 +30,8 @@
 // row-split one up to the rounding of the split rows.
 #include "common.hpp"
 
+#include <mutex>
+
 namespace sporder_hip {
 
 namespace {
@@ -663,7 +665,7 @@ SpmmLongWs take_long_ws(Context &ctx, int32_t nnz, int32_t N) {
 template <int G>
 void launch_rowsplit_g(Context &ctx, int32_t n, int32_t nnz, const int32_t *ptr,
                        const int32_t *ind, const float *val, int32_t N, const float *B,
-                       float *C, const SpmmLongWs &w) {
+                       float *C, const SpmmLongWs &w, int64_t seg_cap, int64_t long_cap) {
   constexpr int rpw = kWave / G;
   fill_u32(ctx, w.ctl, sizeof(LongCtl) / 4, 0u);
   // Narrow widths (G <= 8 lanes per row, 8+ rows per wave) lose most to
@@ -680,11 +682,11 @@ void launch_rowsplit_g(Context &ctx, int32_t n, int32_t nnz, const int32_t *ptr,
   }
   SP_LAUNCH_CHECK();
   // Persistent grid over the registered segment units (none: exits at once).
-  const int g = ctx.grid_for(ceil_div64(max_segments(nnz), rpw * kSpmmWaves), kSpmmBlock, 2);
+  const int g = ctx.grid_for(ceil_div64(seg_cap, rpw * kSpmmWaves), kSpmmBlock, 2);
   spmm_long_segments<G><<<g, kSpmmBlock, 0, ctx.stream>>>(ptr, ind, val, N, B, w.ctl,
                                                             w.longs, w.owner, w.part);
   SP_LAUNCH_CHECK();
-  const int gf = ctx.grid_for(ceil_div64(max_long_rows(nnz), rpw * kSpmmWaves), kSpmmBlock, 2);
+  const int gf = ctx.grid_for(ceil_div64(long_cap, rpw * kSpmmWaves), kSpmmBlock, 2);
   spmm_long_fixup<G><<<gf, kSpmmBlock, 0, ctx.stream>>>(N, C, w.ctl, w.longs, w.part);
   SP_LAUNCH_CHECK();
 }
@@ -697,10 +699,13 @@ size_t spmm_ws_bytes(int32_t nnz, int32_t N) {
          ws_bytes<float>(static_cast<size_t>(max_segments(nnz)) * N);
 }
 
-// Row-split SpMM in the stated order; `w` comes from take_long_ws.
+// Row-split SpMM in the stated order.  `w` holds room for `long_cap` long rows
+// and `seg_cap` segments (take_long_ws: the most nnz nonzeros allow).
 void spmm_rowsplit(Context &ctx, int32_t n, int32_t nnz, const int32_t *ptr,
                    const int32_t *ind, const float *val, int32_t N, const float *B, float *C,
-                   const SpmmLongWs &w) {
+                   const SpmmLongWs &w, int64_t seg_cap = -1, int64_t long_cap = -1) {
+  if (seg_cap < 0) seg_cap = max_segments(nnz);
+  if (long_cap < 0) long_cap = max_long_rows(nnz);
   bool aligned = (N % 4 == 0) && (reinterpret_cast<uintptr_t>(B) % 16 == 0) &&
                  (reinterpret_cast<uintptr_t>(C) % 16 == 0);
   if (!aligned) {
@@ -711,19 +716,19 @@ void spmm_rowsplit(Context &ctx, int32_t n, int32_t nnz, const int32_t *ptr,
   }
   int32_t q = N / 4; // float4 columns
   if (q <= 1) {
-    launch_rowsplit_g<1>(ctx, n, nnz, ptr, ind, val, N, B, C, w);
+    launch_rowsplit_g<1>(ctx, n, nnz, ptr, ind, val, N, B, C, w, seg_cap, long_cap);
   } else if (q <= 2) {
-    launch_rowsplit_g<2>(ctx, n, nnz, ptr, ind, val, N, B, C, w);
+    launch_rowsplit_g<2>(ctx, n, nnz, ptr, ind, val, N, B, C, w, seg_cap, long_cap);
   } else if (q <= 4) {
-    launch_rowsplit_g<4>(ctx, n, nnz, ptr, ind, val, N, B, C, w);
+    launch_rowsplit_g<4>(ctx, n, nnz, ptr, ind, val, N, B, C, w, seg_cap, long_cap);
   } else if (q <= 8) {
-    launch_rowsplit_g<8>(ctx, n, nnz, ptr, ind, val, N, B, C, w);
+    launch_rowsplit_g<8>(ctx, n, nnz, ptr, ind, val, N, B, C, w, seg_cap, long_cap);
   } else if (q <= 16) {
-    launch_rowsplit_g<16>(ctx, n, nnz, ptr, ind, val, N, B, C, w);
+    launch_rowsplit_g<16>(ctx, n, nnz, ptr, ind, val, N, B, C, w, seg_cap, long_cap);
   } else if (q <= 32) {
-    launch_rowsplit_g<32>(ctx, n, nnz, ptr, ind, val, N, B, C, w);
+    launch_rowsplit_g<32>(ctx, n, nnz, ptr, ind, val, N, B, C, w, seg_cap, long_cap);
   } else {
-    launch_rowsplit_g<64>(ctx, n, nnz, ptr, ind, val, N, B, C, w);
+    launch_rowsplit_g<64>(ctx, n, nnz, ptr, ind, val, N, B, C, w, seg_cap, long_cap);
   }
 }
 
@@ -792,11 +797,129 @@ void spmm_merge(Context &ctx, int32_t n, int32_t nnz, const int32_t *ptr,
   SP_LAUNCH_CHECK();
 }
 
+// ---- no-allocation variant -----------------------------------------------------
+//
+// sporder_spmm_csr_noalloc runs the row-split kernels above with their scratch
+// (long-row descriptors, segment owners, segment partial rows) carved from
+// `scratch`, a file-scope device array of SPORDER_SPMM_NOALLOC_SCRATCH_BYTES
+// that every GPU the library runs on holds until the process ends.  Host code
+// never passes the array's name to a kernel (in host code it is a host-side
+// stand-in, not a device address): each device's address comes from
+// hipGetSymbolAddress, taken once per device when a context is created on it
+// (spmm_noalloc_setup) and kept in noalloc_ptr.  Every call on one GPU uses
+// that GPU's array, so calls that overlap on one GPU (two contexts, two
+// threads) race; the counters it holds are cleared by a fill kernel at the
+// start of each call.
+
+namespace {
+
+constexpr size_t kNoAllocBytes = SPORDER_SPMM_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kNoAllocBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex noalloc_mu;
+void *noalloc_ptr[kMaxDevices] = {};
+
+// Rows past kLongRow nonzeros and their segments: ctl->rows, ctl->segments
+// (zeroed by the caller).  Grid-stride, one lane per row.
+__global__ void __launch_bounds__(256)
+    spmm_count_long(int32_t n, const int32_t *__restrict__ ptr, LongCtl *ctl) {
+  int32_t rows = 0, segs = 0;
+  for (int64_t r = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; r < n;
+       r += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int32_t len = ptr[r + 1] - ptr[r];
+    if (len > kLongRow) {
+      rows += 1;
+      segs += (len + kSegLen - 1) / kSegLen;
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    rows += __shfl_xor(rows, off, kWave);
+    segs += __shfl_xor(segs, off, kWave);
+  }
+  if (lane_id() == 0 && rows != 0) {
+    atomicAdd(&ctl->rows, rows);
+    atomicAdd(&ctl->segments, segs);
+  }
+}
+
+} // namespace
+
+// Takes this device's address of `scratch` (the device must be current).
+void spmm_noalloc_setup(int device) {
+  SP_EXPECT(device >= 0 && device < kMaxDevices, "device index out of range");
+  std::lock_guard<std::mutex> lock(noalloc_mu);
+  if (noalloc_ptr[device] != nullptr) return;
+  void *p = nullptr;
+  SP_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+  SP_EXPECT(p != nullptr, "hipGetSymbolAddress returned no address for the SpMM scratch");
+  noalloc_ptr[device] = p;
+}
+
+namespace {
+
+void *noalloc_scratch(int device) {
+  std::lock_guard<std::mutex> lock(noalloc_mu);
+  void *p = device >= 0 && device < kMaxDevices ? noalloc_ptr[device] : nullptr;
+  SP_EXPECT(p != nullptr, "no SpMM scratch address for this device (context not set up)");
+  return p;
+}
+
+} // namespace
+
 } // namespace sporder_hip
 
 using namespace sporder_hip;
 
 extern "C" {
+
+int32_t sporder_spmm_csr_noalloc(sporder_context_t h, int32_t n, int32_t nnz,
+                                 const int32_t *d_ptr, const int32_t *d_ind,
+                                 const float *d_val, int32_t cols, const float *d_b,
+                                 float *d_c) {
+  SP_EXPECT(h != nullptr, "null context");
+  SP_EXPECT(n >= 1 && nnz >= 0, "expect n >= 1 and nnz >= 0");
+  SP_EXPECT(cols >= 1, "cols must be >= 1");
+  Context &ctx = h->impl;
+  char *base = static_cast<char *>(noalloc_scratch(ctx.device));
+  const bool aligned = (cols % 4 == 0) && (reinterpret_cast<uintptr_t>(d_b) % 16 == 0) &&
+                       (reinterpret_cast<uintptr_t>(d_c) % 16 == 0);
+  if (!aligned) {
+    // One wave per row in the stated order: no scratch.
+    int g = ctx.grid_for(ceil_div64(n, kSpmmBlock / kWave), kSpmmBlock, 8);
+    spmm_rowsplit_scalar<<<g, kSpmmBlock, 0, ctx.stream>>>(n, d_ptr, d_ind, d_val, cols, d_b,
+                                                           d_c);
+    SP_LAUNCH_CHECK();
+    ctx.sync();
+    return 0;
+  }
+  // Exact need: count the long rows and their segments first.
+  LongCtl *ctl = reinterpret_cast<LongCtl *>(base);
+  fill_u32(ctx, ctl, sizeof(LongCtl) / 4, 0u);
+  const int gc = ctx.grid_for(ceil_div64(n, 256), 256, 2);
+  spmm_count_long<<<gc, 256, 0, ctx.stream>>>(n, d_ptr, ctl);
+  SP_LAUNCH_CHECK();
+  SP_HIP(hipMemcpyAsync(ctx.host_words, ctl, sizeof(LongCtl), hipMemcpyDeviceToHost,
+                        ctx.stream));
+  ctx.sync();
+  const int64_t long_rows = ctx.host_words[0], segments = ctx.host_words[1];
+  const size_t need = ws_bytes<LongCtl>(1) + ws_bytes<LongRow>(static_cast<size_t>(long_rows)) +
+                      ws_bytes<int32_t>(static_cast<size_t>(segments)) +
+                      ws_bytes<float>(static_cast<size_t>(segments) * cols);
+  if (need > kNoAllocBytes) return SPORDER_SPMM_NOALLOC_TOO_LARGE;
+  SpmmLongWs w;
+  size_t off = ws_bytes<LongCtl>(1);
+  w.ctl = ctl;
+  w.longs = reinterpret_cast<LongRow *>(base + off);
+  off += ws_bytes<LongRow>(static_cast<size_t>(long_rows));
+  w.owner = reinterpret_cast<int32_t *>(base + off);
+  off += ws_bytes<int32_t>(static_cast<size_t>(segments));
+  w.part = reinterpret_cast<float *>(base + off);
+  spmm_rowsplit(ctx, n, nnz, d_ptr, d_ind, d_val, cols, d_b, d_c, w, segments, long_rows);
+  ctx.sync();
+  return 0;
+}
 
 void sporder_spmm_csr(sporder_context_t h, int32_t n, int32_t nnz,
                       const int32_t *d_ptr, const int32_t *d_ind, const float *d_val,

@@ -26,6 +26,7 @@ from ._sporder import reorder as _reorder
 from ._sporder import similarity_graph as _similarity_graph
 from ._sporder import similarity_graph_exact as _similarity_graph_exact
 from ._sporder import spmm_csr as _spmm_csr
+from ._sporder import spmm_csr_noalloc as _spmm_csr_noalloc
 
 __all__ = [
     "bench_cusparse_spmm",
@@ -39,6 +40,7 @@ __all__ = [
     "similarity_graph",
     "similarity_graph_exact",
     "spmm_csr",
+    "spmm_csr_noalloc",
 ]
 
 
@@ -157,6 +159,15 @@ def spmm_csr(ptr, ind, val, B, *, out=None, algo="row_split", ctx=None):
     "merge_path" splits the nonzeros evenly across waves and adds the partial
     sums of cut rows with atomics.  Returns (C, kernel_ms)."""
     return _spmm_csr(ptr, ind, val, B, out=out, algo=algo, ctx=ctx)
+
+
+def spmm_csr_noalloc(ptr, ind, val, B, *, out, ctx=None):
+    """(new) spmm_csr's row-split into the caller's ``out`` with no device
+    allocation by the library: its long-row scratch is a 64 MiB static device
+    array per GPU, shared by every call on that GPU (overlapping calls race).
+    Bit-identical to spmm_csr(algo="row_split").  Raises ValueError when the
+    matrix's long rows need more scratch than that.  Returns ``out``."""
+    return _spmm_csr_noalloc(ptr, ind, val, B, out, ctx=ctx)
 
 
 def hierarchical_matching(ptr, ind, *, is_symmetric=False, num_levels=1, k=0,

@@ -331,6 +331,40 @@ def spmm_csr(ptr, ind, val, B, out=None, algo="row_split", ctx=None):
     return out, ms.value
 
 
+def spmm_csr_noalloc(ptr, ind, val, B, out, ctx=None):
+    """C = A @ B into the caller's `out` with no device allocation by the
+    library (new export, the row-split in the stated order).  Raises
+    ValueError when the matrix's long rows need more scratch than the
+    library's static array holds."""
+    ptr = _gpu_in(ptr, torch.int32, "ptr")
+    ind = _gpu_in(ind, torch.int32, "ind")
+    val = _gpu_in(val, torch.float32, "val")
+    n, nnz = _sizes(ptr, ind)
+    if val.numel() != nnz:
+        raise ValueError("val must have length nnz")
+    B = _as_tensor(B, "B")
+    if not B.is_cuda or B.dtype != torch.float32 or B.dim() != 2 or B.shape[0] != n \
+            or not B.is_contiguous():
+        raise ValueError("B must be a contiguous (n, N) float32 GPU tensor")
+    cols = B.shape[1]
+    if cols < 1:
+        raise ValueError("B must have at least one column")
+    if (out is None or out.shape != (n, cols) or out.dtype != torch.float32
+            or not out.is_contiguous() or out.device != B.device):
+        raise ValueError("out must be a contiguous (n, N) float32 tensor on B's device")
+    c = _resolve(ctx, ptr)
+    rc = c._lib.sporder_spmm_csr_noalloc(c.handle, n, nnz, _addr(ptr), _addr(ind), _addr(val),
+                                         cols, _addr(B), _addr(out))
+    if rc == _lib.SPMM_NOALLOC_TOO_LARGE:
+        raise ValueError(
+            f"the long rows of this matrix need more than the "
+            f"{_lib.SPMM_NOALLOC_SCRATCH_BYTES >> 20} MiB no-allocation scratch at N={cols}; "
+            "use spmm_csr")
+    if rc != 0:
+        raise RuntimeError(f"sporder_spmm_csr_noalloc returned {rc}")
+    return out
+
+
 def _not_built(name):
     def fn(*args, **kwargs):
         raise NotImplementedError(f"sporder.{name} is not part of this build")

@@ -298,6 +298,29 @@ SPORDER_API void sporder_spmm_csr(sporder_context_t ctx, int32_t n,
                                   int32_t cols, const float *d_b, float *d_c,
                                   sporder_spmm_algo_t algo, float *kernel_ms);
 
+/*
+ * (new) sporder_spmm_csr (ROW_SPLIT) that allocates nothing.  It has no
+ * counterpart in the reference: it is for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  The result equals sporder_spmm_csr's bit for bit (same
+ * kernels, same stated order).  The caller passes every input and output; the
+ * scratch the row-split needs for rows past SPORDER_SPMM_LONG_ROW nonzeros
+ * (a 16-byte descriptor per such row, 4 bytes per segment and a partial row of
+ * `cols` floats per segment, each part rounded up to 256 bytes) comes from a
+ * static device array of SPORDER_SPMM_NOALLOC_SCRATCH_BYTES that each GPU
+ * holds from the first context created on it until the process ends.  Every
+ * call on one GPU shares that array: calls that overlap on one GPU race.
+ * Returns 0 when C is written, or SPORDER_SPMM_NOALLOC_TOO_LARGE (nothing
+ * computed) when the input's long rows need more scratch than the array
+ * holds.  Invalid arguments abort, as elsewhere.  Synchronous.
+ */
+#define SPORDER_SPMM_NOALLOC_SCRATCH_BYTES (64u << 20)
+#define SPORDER_SPMM_NOALLOC_TOO_LARGE 1
+SPORDER_API int32_t sporder_spmm_csr_noalloc(sporder_context_t ctx, int32_t n,
+                                             int32_t nnz, const int32_t *d_ptr,
+                                             const int32_t *d_ind, const float *d_val,
+                                             int32_t cols, const float *d_b, float *d_c);
+
 #ifdef __cplusplus
 }
 #endif
