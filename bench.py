@@ -89,6 +89,77 @@ def reorder_bytes(n, nnz, k, symmetric):
     return b
 
 
+def band_demo(sporder, torch, dev, ctx, iters):
+    """The blocked SpMM where rows share columns: a band |i - j| <= 8 of
+    n = 2^20 rows (17 nonzeros per row, values U(-1, 1) seed 1), N = 128,
+    B = randn seed 42.  Per-launch times of the row-split and of the planned
+    SpMM (every tile in 8-row blocks), algorithmic GB/s and the fraction of
+    8 TB/s; '_check' compares the planned C with the oracle (CPU leg)."""
+    from chunkedgreedy_amd import synth
+
+    n = 1 << 20
+    ptr_h, ind_h, _ = synth.band(n, 8)
+    val_h = np.random.default_rng(1).uniform(-1, 1, ind_h.shape[0]).astype(np.float32)
+    nnz = int(ind_h.shape[0])
+    p, i, v = (torch.from_numpy(a).to(dev) for a in (ptr_h, ind_h, val_h))
+    gen = torch.Generator(device=dev).manual_seed(42)
+    B = torch.randn((n, 128), generator=gen, dtype=torch.float32, device=dev)
+    t0 = time.perf_counter()
+    plan = sporder.spmm_plan(p, i, ctx=ctx)
+    plan_ms = (time.perf_counter() - t0) * 1e3
+    out = torch.empty((n, 128), dtype=torch.float32, device=dev)
+
+    def timed(pl):
+        for _ in range(30):
+            sporder.spmm_csr(p, i, v, B, out=out, ctx=ctx, plan=pl)
+        tot = 0.0
+        for _ in range(iters):
+            tot += sporder.spmm_csr(p, i, v, B, out=out, ctx=ctx, plan=pl)[1]
+        return tot / iters
+
+    t_rs = timed(None)
+    ref = out.clone()
+    t_bl = timed(plan)
+    same = bool(torch.equal(out.view(torch.int32), ref.view(torch.int32)))
+    bts = spmm_bytes(n, nnz, 128)
+    res = {"workload": "band |i-j|<=8, n=2^20, N=128", "n": n, "nnz": nnz,
+           "plan": plan.info, "plan_ms": round(plan_ms, 2),
+           "rowsplit_ms": round(t_rs, 4), "blocked_ms": round(t_bl, 4),
+           "blocked_gbs": round(bts / t_bl / 1e6, 1),
+           "frac": round(bts / t_bl / 1e6 / HBM_PEAK_GBS, 4),
+           "rowsplit_frac": round(bts / t_rs / 1e6 / HBM_PEAK_GBS, 4),
+           "bit_exact_vs_rowsplit": same}
+    log(f"band demo {res}")
+    C_h = out.cpu().numpy()
+    B_h = B.cpu().numpy()
+
+    def check():
+        import oracle
+
+        want = oracle.spmm_csr(ptr_h, ind_h, val_h, B_h)
+        return bool(np.array_equal(C_h.view(np.uint32), want.view(np.uint32)))
+
+    res["_check"] = check
+    return res
+
+
+def copy_rate(torch, dev):
+    """Device-to-device copy rate of a 1 GiB tensor (bytes read + written per
+    second, median of 5): the practical HBM ceiling beside the 8 TB/s peak."""
+    src = torch.ones((1 << 30) // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    ts = []
+    for _ in range(6):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        dst.copy_(src)
+        b.record()
+        b.synchronize()
+        ts.append(a.elapsed_time(b))
+    del src, dst
+    return round(2 * (1 << 30) / statistics.median(ts[1:]) / 1e6, 1)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -104,6 +175,9 @@ def main():
     ap.add_argument("--only-spmm", action="store_true",
                     help="profiler pass: one reorder, then --spmm-iters SpMMs at N=128 on the "
                          "reordered matrix; prints no JSON line")
+    ap.add_argument("--only-band", action="store_true",
+                    help="profiler pass: the band demo's SpMMs only (row-split and blocked); "
+                         "prints no JSON line")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -149,26 +223,39 @@ def main():
     ctx = sporder.Context()
     out128 = torch.empty((n, 128), dtype=torch.float32, device=dev)
 
-    def step():
+    def step(plan=None):
+        """csg reorder, P A P^T with values, SpMM at N=128 on the reordered
+        matrix (through `plan` when given: the SpMM harness builds it in its
+        untimed prepare step)."""
         order = sporder.chunk_similarity_greedy(ptr, ind, is_symmetric=is_sym, ctx=ctx)
         p2, i2, v2 = sporder.reorder(ptr, ind, order, val=val, symmetric=True, ctx=ctx)
-        sporder.spmm_csr(p2, i2, v2, B128, out=out128, ctx=ctx)
+        sporder.spmm_csr(p2, i2, v2, B128, out=out128, ctx=ctx, plan=plan)
         return order, (p2, i2, v2)
 
+    # The reordered pattern (the same each step: csg is deterministic) and its
+    # SpMM plan, built once outside the timed region.
+    order, (p2, i2, v2) = step()
+    t_plan = time.perf_counter()
+    plan = sporder.spmm_plan(p2, i2, ctx=ctx)
+    plan_ms = (time.perf_counter() - t_plan) * 1e3
+    log(f"spmm plan of the reordered C2: {plan.info} in {plan_ms:.1f} ms")
+
     if args.only_spmm:
-        order, (p2, i2, v2) = step()
         for _ in range(args.spmm_iters):
-            sporder.spmm_csr(p2, i2, v2, B128, out=out128, ctx=ctx)
+            sporder.spmm_csr(p2, i2, v2, B128, out=out128, ctx=ctx, plan=plan)
         torch.cuda.synchronize()
         log(f"only-spmm: {args.spmm_iters} SpMMs at N=128 on the reordered matrix")
         return
+    if args.only_band:
+        band_demo(sporder, torch, dev, ctx, args.spmm_iters)
+        return
 
     for _ in range(args.warmup):
-        step()
+        step(plan)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        order, reordered = step()
+        order, reordered = step(plan)
     torch.cuda.synchronize()
     ms_per_step = (time.perf_counter() - t0) * 1e3 / max(args.steps, 1)
     log(f"step {ms_per_step:.3f} ms")
@@ -200,23 +287,25 @@ def main():
         perm_ms.append((time.perf_counter() - t1) * 1e3)
     perm_med = statistics.median(perm_ms)
 
-    # SpMM per-launch kernel time, original vs reordered.
+    # SpMM per-launch kernel time, original vs reordered, each through its
+    # plan (the harness's prepare step, untimed).
     p2, i2, v2 = reordered
+    plan_orig = sporder.spmm_plan(ptr, ind, ctx=ctx)
 
-    def spmm_ms(p, i, v, B):
+    def spmm_ms(p, i, v, B, pl=None):
         out = torch.empty((n, B.shape[1]), dtype=torch.float32, device=dev)
         for _ in range(30):
-            sporder.spmm_csr(p, i, v, B, out=out, ctx=ctx)
+            sporder.spmm_csr(p, i, v, B, out=out, ctx=ctx, plan=pl)
         tot = 0.0
         for _ in range(args.spmm_iters):
-            _, ms = sporder.spmm_csr(p, i, v, B, out=out, ctx=ctx)
+            _, ms = sporder.spmm_csr(p, i, v, B, out=out, ctx=ctx, plan=pl)
             tot += ms
         return tot / args.spmm_iters
 
     spmm = {}
     for N, B in ((32, B32), (128, B128)):
-        t_orig = spmm_ms(ptr, ind, val, B)
-        t_re = spmm_ms(p2, i2, v2, B)
+        t_orig = spmm_ms(ptr, ind, val, B, plan_orig)
+        t_re = spmm_ms(p2, i2, v2, B, plan)
         bts = spmm_bytes(n, nnz, N)
         spmm[str(N)] = {
             "orig_ms": round(t_orig, 4), "reordered_ms": round(t_re, 4),
@@ -243,6 +332,8 @@ def main():
                           "gather_gbs": round(4.0 * nnz * 128 / t_c / 1e6, 1)}
         del cind
     log(f"spmm ceiling {ceiling}")
+    band = band_demo(sporder, torch, dev, ctx, args.spmm_iters)
+    copy_gbs = copy_rate(torch, dev)
 
     k_used = stats["k_used"]
     # Dominant kernel of the step: compare the stage spans with the SpMM.
@@ -300,12 +391,14 @@ def main():
             c_ref = oracle.spmm_csr(p2h, i2h, v2h, B_h)
             cpu_spmm.append((time.perf_counter() - t1) * 1e3)
         cs = statistics.median(cpu_spmm)
-        # The headline SpMM (reordered C2, N = 128, B seed 42) against the
-        # oracle's stated fmaf order, bit for bit.
-        c_gpu, _ = sporder.spmm_csr(p2, i2, v2, B128, ctx=ctx)
+        # The headline SpMM (reordered C2, N = 128, B seed 42, through its
+        # plan) against the oracle's stated fmaf order, bit for bit; and the
+        # band demo's blocked SpMM.
+        c_gpu, _ = sporder.spmm_csr(p2, i2, v2, B128, ctx=ctx, plan=plan)
         spmm_parity = bool(np.array_equal(c_gpu.cpu().numpy().view(np.uint32),
                                           c_ref.view(np.uint32)))
         del c_gpu, c_ref
+        band["bit_exact_vs_cpu"] = band.pop("_check")()
         log(f"cpu parity: permutation {parity}, apply {apply_parity}, spmm {spmm_parity}")
         cpu = {"value": round(spmm_bytes(n, nnz, 128) / (cs * 1e-3) / 1e9, 2), "unit": "GB/s",
                "cores": threads, "kind": "port",
@@ -343,8 +436,12 @@ def main():
         "roofline": roofline,
         "roofline_spmm": roofline_spmm,
         "spmm_ceiling_n128": ceiling,
+        "spmm_plan_c2": {"info": plan.info, "plan_ms": round(plan_ms, 2)},
+        "spmm_block_band": band,
+        "hbm_copy_gbs": copy_gbs,
         "cpu_baseline": cpu,
     }
+    band.pop("_check", None)
     print(json.dumps(out), flush=True)
 
 

@@ -37,6 +37,13 @@ class CsgStats(ctypes.Structure):
                 ("avg_followed_weight", f64)]
 
 
+class SpmmPlanInfo(ctypes.Structure):
+    """sporder_spmm_plan_info_t (new)."""
+
+    _fields_ = [("tiles", i32), ("blocked_tiles", i32), ("blocked_rows", ctypes.c_int64),
+                ("blocked_nnz", ctypes.c_int64), ("entries", ctypes.c_int64)]
+
+
 class CgTiming(ctypes.Structure):
     """sporder_cg_timing_t (reference sporder/include/sporder.h:128-133)."""
 
@@ -118,6 +125,9 @@ SIGNATURES = {
         [vp, i32, i32, vp, vp, ctypes.c_bool, i32, f32, i32, vp, vp], None),
     "sporder_spmm_csr": ([vp, i32, i32, vp, vp, vp, i32, vp, vp, i32, P(f32)], None),
     "sporder_spmm_csr_noalloc": ([vp, i32, i32, vp, vp, vp, i32, vp, vp], i32),
+    "sporder_spmm_plan_create": ([vp, i32, i32, vp, vp, P(SpmmPlanInfo)], vp),
+    "sporder_spmm_plan_destroy": ([vp], None),
+    "sporder_spmm_csr_plan": ([vp, vp, i32, i32, vp, vp, vp, i32, vp, vp, P(f32)], None),
 }
 
 _lib = None

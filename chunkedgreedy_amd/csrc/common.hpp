@@ -158,6 +158,16 @@ struct EventSpan {
 // SpMM scratch (spmm.hip); called once per context creation.
 void spmm_noalloc_setup(int device);
 
+// Rows of a tile of an SpMM plan (spmm_plan.hip); row-split tile lists count
+// in these units.
+constexpr int kSpmmTileRows = 64;
+
+// Row-split SpMM in the stated order over the listed tiles (every row when
+// `tiles` is null), long rows in segments; reserves the context workspace.
+void spmm_rowsplit_tiles(Context &ctx, int32_t n, int32_t nnz, const int32_t *ptr,
+                         const int32_t *ind, const float *val, int32_t N, const float *B,
+                         float *C, const int32_t *tiles, int64_t ntiles);
+
 // In-place exclusive (inclusive=false) or inclusive scan of `count` int32
 // values; `tmp` must hold scan_tmp_elems(count) int32.
 size_t scan_tmp_elems(int64_t count);

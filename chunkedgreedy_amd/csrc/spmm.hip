@@ -41,6 +41,7 @@ constexpr int kSpmmWaves = kSpmmBlock / kWave;
 constexpr int kSpmmDepth = 8; // B rows in flight per row group
 constexpr int kLongRow = SPORDER_SPMM_LONG_ROW;
 constexpr int kSegLen = SPORDER_SPMM_SEGMENT;
+constexpr int kTileRows = kSpmmTileRows; // rows of a tile of an SpMM plan
 
 // Long rows: rows past kLongRow nonzeros leave the row-split launch, which
 // appends a descriptor; each becomes nseg segment units whose partials the
@@ -137,14 +138,21 @@ __global__ void __launch_bounds__(kSpmmBlock)
                      const int32_t *__restrict__ ind,
                      const float *__restrict__ val, int32_t N,
                      const float *__restrict__ B, float *__restrict__ C,
-                     LongCtl *ctl, LongRow *longs, int32_t *owner) {
+                     LongCtl *ctl, LongRow *longs, int32_t *owner,
+                     const int32_t *__restrict__ tiles, int64_t ntiles) {
   constexpr int kRowsPerWave = kWave / G;
   const int lane = lane_id();
   const int sub = lane / G;  // row slot within the wave
   const int gl = lane % G;   // lane within the row group
   const int gbase = sub * G; // first lane of the group
   const int64_t wave = static_cast<int64_t>(blockIdx.x) * kSpmmWaves + threadIdx.x / kWave;
-  const int64_t row = wave * kRowsPerWave + sub;
+  // With a tile list, G waves cover each listed tile of kTileRows rows; the
+  // waves past the list (the grid is whole blocks) take no row.
+  const int64_t row = tiles == nullptr ? wave * kRowsPerWave + sub
+                      : wave / G < ntiles
+                          ? static_cast<int64_t>(tiles[wave / G]) * kTileRows +
+                                (wave % G) * kRowsPerWave + sub
+                          : static_cast<int64_t>(n);
   const bool row_ok = row < n;
   int32_t s = row_ok ? ptr[row] : 0;
   const int32_t e = row_ok ? ptr[row + 1] : 0;
@@ -171,13 +179,16 @@ template <int G>
 __global__ void __launch_bounds__(kSpmmBlock)
     spmm_rows_dyn(int32_t n, const int32_t *__restrict__ ptr, const int32_t *__restrict__ ind,
                   const float *__restrict__ val, int32_t N, const float *__restrict__ B,
-                  float *__restrict__ C, LongCtl *ctl, LongRow *longs, int32_t *owner) {
+                  float *__restrict__ C, LongCtl *ctl, LongRow *longs, int32_t *owner,
+                  const int32_t *__restrict__ tiles, int64_t ntiles) {
+  static_assert(kTileRows == kWave, "a wave owns one tile");
   constexpr int U = kSpmmDepth;
   constexpr int RPW = kWave / G;
   const int lane = lane_id();
   const int sub = lane / G, gl = lane % G, gbase = sub * G;
   const int64_t wave = static_cast<int64_t>(blockIdx.x) * kSpmmWaves + threadIdx.x / kWave;
-  const int64_t r0 = wave * kWave;
+  if (tiles != nullptr && wave >= ntiles) return; // past the list (whole blocks)
+  const int64_t r0 = tiles == nullptr ? wave * kWave : static_cast<int64_t>(tiles[wave]) * kWave;
   if (r0 >= n) return;
   const int32_t nrows = static_cast<int32_t>(n - r0 < kWave ? n - r0 : kWave);
   // Lane i holds ptr[r0 + i] (i <= nrows); ptr[r0 + 64] separately.
@@ -665,20 +676,24 @@ SpmmLongWs take_long_ws(Context &ctx, int32_t nnz, int32_t N) {
 template <int G>
 void launch_rowsplit_g(Context &ctx, int32_t n, int32_t nnz, const int32_t *ptr,
                        const int32_t *ind, const float *val, int32_t N, const float *B,
-                       float *C, const SpmmLongWs &w, int64_t seg_cap, int64_t long_cap) {
+                       float *C, const SpmmLongWs &w, int64_t seg_cap, int64_t long_cap,
+                       const int32_t *tiles, int64_t ntiles) {
   constexpr int rpw = kWave / G;
   fill_u32(ctx, w.ctl, sizeof(LongCtl) / 4, 0u);
   // Narrow widths (G <= 8 lanes per row, 8+ rows per wave) lose most to
   // row-length imbalance inside a wave: claim rows dynamically there.  With
-  // wider rows the fixed assignment keeps more waves in flight.
+  // wider rows the fixed assignment keeps more waves in flight.  With a tile
+  // list only the listed tiles' rows are computed.
+  const int64_t waves = tiles == nullptr ? ceil_div64(n, rpw) : ntiles * (kTileRows / rpw);
   if (G <= 8 && N <= 4 * G) {
-    const int64_t blocks = ceil_div64(ceil_div64(n, kWave), kSpmmWaves);
+    const int64_t dyn_waves = tiles == nullptr ? ceil_div64(n, kWave) : ntiles;
+    const int64_t blocks = ceil_div64(dyn_waves, kSpmmWaves);
     spmm_rows_dyn<G><<<dim3(static_cast<unsigned>(blocks)), kSpmmBlock, 0, ctx.stream>>>(
-        n, ptr, ind, val, N, B, C, w.ctl, w.longs, w.owner);
+        n, ptr, ind, val, N, B, C, w.ctl, w.longs, w.owner, tiles, ntiles);
   } else {
-    const int64_t blocks = ceil_div64(ceil_div64(n, rpw), kSpmmWaves);
+    const int64_t blocks = ceil_div64(waves, kSpmmWaves);
     spmm_rowsplit_v4<G><<<dim3(static_cast<unsigned>(blocks)), kSpmmBlock, 0, ctx.stream>>>(
-        n, ptr, ind, val, N, B, C, w.ctl, w.longs, w.owner);
+        n, ptr, ind, val, N, B, C, w.ctl, w.longs, w.owner, tiles, ntiles);
   }
   SP_LAUNCH_CHECK();
   // Persistent grid over the registered segment units (none: exits at once).
@@ -703,12 +718,14 @@ size_t spmm_ws_bytes(int32_t nnz, int32_t N) {
 // and `seg_cap` segments (take_long_ws: the most nnz nonzeros allow).
 void spmm_rowsplit(Context &ctx, int32_t n, int32_t nnz, const int32_t *ptr,
                    const int32_t *ind, const float *val, int32_t N, const float *B, float *C,
-                   const SpmmLongWs &w, int64_t seg_cap = -1, int64_t long_cap = -1) {
+                   const SpmmLongWs &w, int64_t seg_cap = -1, int64_t long_cap = -1,
+                   const int32_t *tiles = nullptr, int64_t ntiles = 0) {
   if (seg_cap < 0) seg_cap = max_segments(nnz);
   if (long_cap < 0) long_cap = max_long_rows(nnz);
   bool aligned = (N % 4 == 0) && (reinterpret_cast<uintptr_t>(B) % 16 == 0) &&
                  (reinterpret_cast<uintptr_t>(C) % 16 == 0);
   if (!aligned) {
+    SP_EXPECT(tiles == nullptr, "internal: tile lists need aligned float4 operands");
     int g = ctx.grid_for(ceil_div64(n, kSpmmBlock / kWave), kSpmmBlock, 8);
     spmm_rowsplit_scalar<<<g, kSpmmBlock, 0, ctx.stream>>>(n, ptr, ind, val, N, B, C);
     SP_LAUNCH_CHECK();
@@ -716,20 +733,35 @@ void spmm_rowsplit(Context &ctx, int32_t n, int32_t nnz, const int32_t *ptr,
   }
   int32_t q = N / 4; // float4 columns
   if (q <= 1) {
-    launch_rowsplit_g<1>(ctx, n, nnz, ptr, ind, val, N, B, C, w, seg_cap, long_cap);
+    launch_rowsplit_g<1>(ctx, n, nnz, ptr, ind, val, N, B, C, w, seg_cap, long_cap,
+                          tiles, ntiles);
   } else if (q <= 2) {
-    launch_rowsplit_g<2>(ctx, n, nnz, ptr, ind, val, N, B, C, w, seg_cap, long_cap);
+    launch_rowsplit_g<2>(ctx, n, nnz, ptr, ind, val, N, B, C, w, seg_cap, long_cap,
+                          tiles, ntiles);
   } else if (q <= 4) {
-    launch_rowsplit_g<4>(ctx, n, nnz, ptr, ind, val, N, B, C, w, seg_cap, long_cap);
+    launch_rowsplit_g<4>(ctx, n, nnz, ptr, ind, val, N, B, C, w, seg_cap, long_cap,
+                          tiles, ntiles);
   } else if (q <= 8) {
-    launch_rowsplit_g<8>(ctx, n, nnz, ptr, ind, val, N, B, C, w, seg_cap, long_cap);
+    launch_rowsplit_g<8>(ctx, n, nnz, ptr, ind, val, N, B, C, w, seg_cap, long_cap,
+                          tiles, ntiles);
   } else if (q <= 16) {
-    launch_rowsplit_g<16>(ctx, n, nnz, ptr, ind, val, N, B, C, w, seg_cap, long_cap);
+    launch_rowsplit_g<16>(ctx, n, nnz, ptr, ind, val, N, B, C, w, seg_cap, long_cap,
+                          tiles, ntiles);
   } else if (q <= 32) {
-    launch_rowsplit_g<32>(ctx, n, nnz, ptr, ind, val, N, B, C, w, seg_cap, long_cap);
+    launch_rowsplit_g<32>(ctx, n, nnz, ptr, ind, val, N, B, C, w, seg_cap, long_cap,
+                          tiles, ntiles);
   } else {
-    launch_rowsplit_g<64>(ctx, n, nnz, ptr, ind, val, N, B, C, w, seg_cap, long_cap);
+    launch_rowsplit_g<64>(ctx, n, nnz, ptr, ind, val, N, B, C, w, seg_cap, long_cap,
+                          tiles, ntiles);
   }
+}
+
+void spmm_rowsplit_tiles(Context &ctx, int32_t n, int32_t nnz, const int32_t *ptr,
+                         const int32_t *ind, const float *val, int32_t N, const float *B,
+                         float *C, const int32_t *tiles, int64_t ntiles) {
+  ctx.reserve(spmm_ws_bytes(nnz, N));
+  const SpmmLongWs w = take_long_ws(ctx, nnz, N);
+  spmm_rowsplit(ctx, n, nnz, ptr, ind, val, N, B, C, w, -1, -1, tiles, ntiles);
 }
 
 template <int G>

@@ -27,6 +27,7 @@ from ._sporder import similarity_graph as _similarity_graph
 from ._sporder import similarity_graph_exact as _similarity_graph_exact
 from ._sporder import spmm_csr as _spmm_csr
 from ._sporder import spmm_csr_noalloc as _spmm_csr_noalloc
+from ._sporder import SpmmPlan
 
 __all__ = [
     "bench_cusparse_spmm",
@@ -41,6 +42,8 @@ __all__ = [
     "similarity_graph_exact",
     "spmm_csr",
     "spmm_csr_noalloc",
+    "spmm_plan",
+    "SpmmPlan",
 ]
 
 
@@ -150,15 +153,25 @@ def chunk_similarity_top_k(ptr, ind, *, k, oversampling, chunk_size, is_symmetri
                                    is_symmetric=is_symmetric, ctx=ctx)
 
 
-def spmm_csr(ptr, ind, val, B, *, out=None, algo="row_split", ctx=None):
+def spmm_plan(ptr, ind, *, ctx=None):
+    """(new) Analyse a CSR pattern for the planned SpMM (the harness's untimed
+    prepare step): tiles of rows that share few columns get those rows of B
+    staged in LDS.  Returns an SpmmPlan whose ``info`` dict counts the staged
+    tiles, rows, nonzeros and columns."""
+    return SpmmPlan(ptr, ind, ctx=ctx)
+
+
+def spmm_csr(ptr, ind, val, B, *, out=None, algo="row_split", ctx=None, plan=None):
     """(new) C = A @ B for CSR A (values ``val``) and row-major dense B.
 
     algo "row_split" follows the stated order of include/sporder.h: a row of
     at most 512 nonzeros is one fmaf chain in CSR order, a longer row is summed
     in 512-nonzero segments added left to right (bit-reproducible);
     "merge_path" splits the nonzeros evenly across waves and adds the partial
-    sums of cut rows with atomics.  Returns (C, kernel_ms)."""
-    return _spmm_csr(ptr, ind, val, B, out=out, algo=algo, ctx=ctx)
+    sums of cut rows with atomics.  With ``plan`` (spmm_plan of this pattern)
+    the staged tiles read B from LDS; the result equals "row_split" bit for
+    bit.  Returns (C, kernel_ms)."""
+    return _spmm_csr(ptr, ind, val, B, out=out, algo=algo, ctx=ctx, plan=plan)
 
 
 def spmm_csr_noalloc(ptr, ind, val, B, *, out, ctx=None):

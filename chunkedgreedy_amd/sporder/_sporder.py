@@ -300,9 +300,46 @@ def chunk_similarity_top_k(ptr, ind, k, oversampling, chunk_size, is_symmetric=F
     return idx.view(n, k), wgt.view(n, k)
 
 
-def spmm_csr(ptr, ind, val, B, out=None, algo="row_split", ctx=None):
+class SpmmPlan:
+    """An SpMM plan of one CSR pattern (new export): the tiles of rows whose
+    shared B rows the planned SpMM stages in LDS.  Owns device memory on the
+    context's device until closed or collected."""
+
+    def __init__(self, ptr, ind, ctx=None):
+        ptr = _gpu_in(ptr, torch.int32, "ptr")
+        ind = _gpu_in(ind, torch.int32, "ind")
+        self.n, self.nnz = _sizes(ptr, ind)
+        self._ctx = _resolve(ctx, ptr)
+        self._lib = self._ctx._lib
+        self.device = ptr.device
+        info = _lib.SpmmPlanInfo()
+        self.handle = self._lib.sporder_spmm_plan_create(self._ctx.handle, self.n, self.nnz,
+                                                         _addr(ptr), _addr(ind),
+                                                         ctypes.byref(info))
+        if not self.handle:
+            raise RuntimeError("sporder_spmm_plan_create failed")
+        self.info = {name: getattr(info, name) for name, _ in _lib.SpmmPlanInfo._fields_}
+
+    def close(self):
+        if getattr(self, "handle", None):
+            self._lib.sporder_spmm_plan_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def spmm_plan(ptr, ind, ctx=None):
+    return SpmmPlan(ptr, ind, ctx=ctx)
+
+
+def spmm_csr(ptr, ind, val, B, out=None, algo="row_split", ctx=None, plan=None):
     """C = A @ B for CSR A and row-major dense B (new export).  Returns
-    (C, kernel_ms)."""
+    (C, kernel_ms).  With a plan of this pattern, the planned SpMM (same
+    result as algo "row_split")."""
     ptr = _gpu_in(ptr, torch.int32, "ptr")
     ind = _gpu_in(ind, torch.int32, "ind")
     val = _gpu_in(val, torch.float32, "val")
@@ -326,6 +363,14 @@ def spmm_csr(ptr, ind, val, B, out=None, algo="row_split", ctx=None):
         raise ValueError(f"algo must be one of {sorted(codes)}")
     c = _resolve(ctx, ptr)
     ms = ctypes.c_float(0.0)
+    if plan is not None:
+        if algo == "merge_path":
+            raise ValueError("a plan runs the row-split order; algo must be auto or row_split")
+        if not plan.handle or plan.n != n or plan.nnz != nnz or plan.device != ptr.device:
+            raise ValueError("plan was made for another matrix or device")
+        c._lib.sporder_spmm_csr_plan(c.handle, plan.handle, n, nnz, _addr(ptr), _addr(ind),
+                                     _addr(val), cols, _addr(B), _addr(out), ctypes.byref(ms))
+        return out, ms.value
     c._lib.sporder_spmm_csr(c.handle, n, nnz, _addr(ptr), _addr(ind), _addr(val), cols,
                             _addr(B), _addr(out), codes[algo], ctypes.byref(ms))
     return out, ms.value

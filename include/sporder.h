@@ -299,6 +299,47 @@ SPORDER_API void sporder_spmm_csr(sporder_context_t ctx, int32_t n,
                                   sporder_spmm_algo_t algo, float *kernel_ms);
 
 /*
+ * (new) SpMM plans.  The reference's SpMM harness converts each matrix once,
+ * untimed, in SpMMMethod.prepare (bench/spmm/spmm_bench/base.py:41-46) and
+ * times SpMMMethod.run; a plan is that conversion for this library's CSR
+ * SpMM.  sporder_spmm_plan_create analyses a CSR pattern on the device in
+ * blocks of 8 consecutive rows: a block's entries are the distinct columns of
+ * its rows, each with the mask of rows holding it.  A tile of 64 rows whose
+ * entries number at most 60 % of its nonzeros (rows that share columns:
+ * bands, meshes in natural order, rows grouped by a reordering) is
+ * "blocked": sporder_spmm_csr_plan computes each of its blocks with one load
+ * of each entry's B row, applied to every row of the block that holds the
+ * column.  Other tiles, and tiles with a row past SPORDER_SPMM_LONG_ROW
+ * nonzeros, run the row-split.  Entries are visited in ascending column
+ * order, so the result is bit-identical to sporder_spmm_csr ROW_SPLIT (each C
+ * element is the same fmaf chain in CSR order).  Blocks apply when cols is a
+ * multiple of 64 and B and C are 16-byte aligned; otherwise the call is the
+ * row-split.  The plan owns device memory on the context's device (8 bytes
+ * per entry and 4 per block) until sporder_spmm_plan_destroy; it records n
+ * and nnz, and the d_ptr/d_ind passed to a run must be the pattern it was
+ * made from.
+ */
+typedef struct sporder_spmm_plan_struct *sporder_spmm_plan_t;
+typedef struct {
+  int32_t tiles;         /* tiles of 64 rows */
+  int32_t blocked_tiles; /* tiles computed in blocks of 8 rows */
+  int64_t blocked_rows;
+  int64_t blocked_nnz;
+  int64_t entries;       /* (column, row mask) entries of the blocked tiles */
+} sporder_spmm_plan_info_t;
+
+SPORDER_API sporder_spmm_plan_t sporder_spmm_plan_create(sporder_context_t ctx, int32_t n,
+                                                         int32_t nnz, const int32_t *d_ptr,
+                                                         const int32_t *d_ind,
+                                                         sporder_spmm_plan_info_t *info);
+SPORDER_API void sporder_spmm_plan_destroy(sporder_spmm_plan_t plan);
+SPORDER_API void sporder_spmm_csr_plan(sporder_context_t ctx, sporder_spmm_plan_t plan,
+                                       int32_t n, int32_t nnz, const int32_t *d_ptr,
+                                       const int32_t *d_ind, const float *d_val,
+                                       int32_t cols, const float *d_b, float *d_c,
+                                       float *kernel_ms);
+
+/*
  * (new) sporder_spmm_csr (ROW_SPLIT) that allocates nothing.  It has no
  * counterpart in the reference: it is for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that

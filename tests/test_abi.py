@@ -52,6 +52,7 @@ STRUCTS = {
     "sporder_hm_timing_t": _lib.HmTiming,
     "sporder_hm_stats_t": _lib.HmStats,
     "sporder_options_t": _lib.Options,
+    "sporder_spmm_plan_info_t": _lib.SpmmPlanInfo,
 }
 
 

@@ -97,6 +97,23 @@ def test_spmm_plugin(sporder, name):
 
 
 @pytest.mark.gpu
+def test_spmm_plugin_blocked_tiles(sporder):
+    """prepare builds an SpMM plan: on a band every 64-row tile runs in 8-row
+    blocks, and the plugin's C equals the oracle's stated fmaf order bit for
+    bit at N = 128."""
+    ptr, ind, _ = synth.band(4096, 8)
+    val = np.random.default_rng(3).uniform(-1, 1, ind.shape[0]).astype(np.float32)
+    a = sp.csr_matrix((val, ind, ptr), shape=(4096, 4096))
+    m = harness.SpMMMethod.create("hip-csr-spmm")
+    prepared = m.prepare(a)
+    assert prepared[3].info["blocked_tiles"] == 64
+    B = harness.generate_dense(4096, 128, device="cuda:0")
+    out, ms = m.run(prepared, B)
+    want = oracle.spmm_csr(ptr, ind, val, B.cpu().numpy())
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32)) and ms > 0
+
+
+@pytest.mark.gpu
 def test_reorder_to_perm_npz_and_csv_row(sporder, tmp_path):
     """The csg plugin's permutation flows into the reference formats: the
     .perm.npz round trip, and a CSV row whose structure metrics (computed on
