@@ -128,7 +128,8 @@ def band_demo(sporder, torch, dev, ctx, iters):
            "blocked_gbs": round(bts / t_bl / 1e6, 1),
            "frac": round(bts / t_bl / 1e6 / HBM_PEAK_GBS, 4),
            "rowsplit_frac": round(bts / t_rs / 1e6 / HBM_PEAK_GBS, 4),
-           "bit_exact_vs_rowsplit": same}
+           "bit_exact_vs_rowsplit": same,
+           "traffic": pmc_traffic("spmm_block_band_n128", n, nnz)}
     log(f"band demo {res}")
     C_h = out.cpu().numpy()
     B_h = B.cpu().numpy()
@@ -175,6 +176,8 @@ def main():
     ap.add_argument("--only-spmm", action="store_true",
                     help="profiler pass: one reorder, then --spmm-iters SpMMs at N=128 on the "
                          "reordered matrix; prints no JSON line")
+    ap.add_argument("--read-calibration", type=int, default=0, metavar="BYTES",
+                    help="first run one reduction over BYTES (a pure read of known traffic)")
     ap.add_argument("--only-band", action="store_true",
                     help="profiler pass: the band demo's SpMMs only (row-split and blocked); "
                          "prints no JSON line")
@@ -203,6 +206,15 @@ def main():
         torch.cuda.synchronize()
         log(f"copy calibration: {args.copy_calibration} bytes read + written")
         del src, dst
+    if args.read_calibration > 0:
+        src = torch.ones(args.read_calibration // 4, dtype=torch.float32, device=dev)
+        total = float(src.sum())
+        log(f"read calibration: {args.read_calibration} bytes read (sum {total:.0f})")
+        del src
+    if args.only_band:
+        band_demo(sporder, torch, dev, sporder.Context(), args.spmm_iters)
+        torch.cuda.synchronize()
+        return
 
     n_rows = args.rows
     blocks = n_rows // 64
@@ -245,9 +257,6 @@ def main():
             sporder.spmm_csr(p2, i2, v2, B128, out=out128, ctx=ctx, plan=plan)
         torch.cuda.synchronize()
         log(f"only-spmm: {args.spmm_iters} SpMMs at N=128 on the reordered matrix")
-        return
-    if args.only_band:
-        band_demo(sporder, torch, dev, ctx, args.spmm_iters)
         return
 
     for _ in range(args.warmup):

@@ -247,6 +247,16 @@ void fill_u32(Context &ctx, void *p, int64_t count, uint32_t value);
 
 __device__ __forceinline__ int lane_id() { return __lane_id(); }
 
+// Workgroup index remapped so that each XCD takes a contiguous run of the
+// grid: the dispatcher hands workgroups to the kXcds XCDs round-robin, so
+// workgroup g runs on XCD g % kXcds; neighbouring work (rows that share B
+// rows, say) then shares that XCD's L2.  A bijection of [0, gridDim.x).
+constexpr int kXcds = 8;
+__device__ __forceinline__ int64_t xcd_block() {
+  const int64_t G = gridDim.x, q = G / kXcds, rem = G % kXcds, x = blockIdx.x % kXcds;
+  return x * q + (x < rem ? x : rem) + blockIdx.x / kXcds;
+}
+
 __device__ __forceinline__ uint64_t ballot(bool p) { return __ballot(p); }
 
 __device__ __forceinline__ int32_t readlane(int32_t v, int lane) {

@@ -145,7 +145,8 @@ __global__ void __launch_bounds__(kSpmmBlock)
   const int sub = lane / G;  // row slot within the wave
   const int gl = lane % G;   // lane within the row group
   const int gbase = sub * G; // first lane of the group
-  const int64_t wave = static_cast<int64_t>(blockIdx.x) * kSpmmWaves + threadIdx.x / kWave;
+  // Consecutive rows on one XCD (rows in a good order share B rows in L2).
+  const int64_t wave = xcd_block() * kSpmmWaves + threadIdx.x / kWave;
   // With a tile list, G waves cover each listed tile of kTileRows rows; the
   // waves past the list (the grid is whole blocks) take no row.
   const int64_t row = tiles == nullptr ? wave * kRowsPerWave + sub
@@ -186,7 +187,7 @@ __global__ void __launch_bounds__(kSpmmBlock)
   constexpr int RPW = kWave / G;
   const int lane = lane_id();
   const int sub = lane / G, gl = lane % G, gbase = sub * G;
-  const int64_t wave = static_cast<int64_t>(blockIdx.x) * kSpmmWaves + threadIdx.x / kWave;
+  const int64_t wave = xcd_block() * kSpmmWaves + threadIdx.x / kWave;
   if (tiles != nullptr && wave >= ntiles) return; // past the list (whole blocks)
   const int64_t r0 = tiles == nullptr ? wave * kWave : static_cast<int64_t>(tiles[wave]) * kWave;
   if (r0 >= n) return;

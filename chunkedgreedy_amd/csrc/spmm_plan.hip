@@ -19,7 +19,7 @@
 // Inspector (spmm_plan_tiles, one workgroup per tile of kSpmmTileRows rows,
 // run twice: count, then write): each block's (column, row) keys are sorted
 // in LDS; runs of equal columns are entries.  A tile is blocked when its
-// entries are at most 60 % of its nonzeros and no row has more than
+// entries are at most half its nonzeros and no row has more than
 // SPORDER_SPMM_LONG_ROW nonzeros (those keep their segment launches); other
 // tiles run the row-split over a tile list.
 //
@@ -150,7 +150,7 @@ __global__ void __launch_bounds__(kPlanBlock)
   if (!write) {
     const int32_t total = (s_cnt[0] + s_cnt[1] + s_cnt[2] + s_cnt[3]) +
                           (s_cnt[4] + s_cnt[5] + s_cnt[6] + s_cnt[7]);
-    const bool blocked = 5 * static_cast<int64_t>(total) <= 3 * static_cast<int64_t>(m);
+    const bool blocked = 2 * static_cast<int64_t>(total) <= static_cast<int64_t>(m);
     if (tid < kTileBlocks) ecount[tile * kTileBlocks + tid] = blocked ? s_cnt[tid] : 0;
     if (tid == 0) kind[tile] = blocked ? 1 : 0;
   }
@@ -213,9 +213,9 @@ __device__ __forceinline__ void apply_nibble(int m4, const V &bv, int e,
 
 // One wave per block of kBlockRows rows of a blocked tile and slice of
 // W = 64 * VEC columns of B and C (slices are separate workgroups, so no
-// registers live across them).  Workgroups are mapped to tiles so that each
-// XCD (workgroups are dispatched round-robin over kXcds) takes a contiguous
-// run of the tile list, whose neighbouring tiles share B rows in its L2.
+// registers live across them).  Workgroups are mapped to tiles by
+// xcd_block(), so each XCD takes a contiguous run of the tile list, whose
+// neighbouring tiles share B rows in its L2.
 template <int VEC>
 __global__ void __launch_bounds__(kPlanBlock)
     spmm_block_kernel(int32_t n, const int32_t *__restrict__ tiles, int32_t ntiles,
@@ -224,12 +224,10 @@ __global__ void __launch_bounds__(kPlanBlock)
                       int32_t N, const float *__restrict__ B, float *__restrict__ C) {
   typedef typename VecOf<VEC>::T V;
   constexpr int W = kWave * VEC;
-  constexpr int kXcds = 8;
   constexpr int kWaves = kPlanBlock / kWave;
   constexpr int kGroupsPerTile = kTileBlocks / kWaves;
   constexpr int U = block_loads<VEC>();
-  const int G = gridDim.x, q = G / kXcds, rem = G % kXcds, x = blockIdx.x % kXcds;
-  const int gg = x * q + min(x, rem) + blockIdx.x / kXcds; // a bijection of [0, G)
+  const int gg = static_cast<int>(xcd_block());
   const int per_slice = ntiles * kGroupsPerTile;
   const int32_t cb = (gg / per_slice) * W;
   const int g = gg % per_slice;

@@ -63,11 +63,15 @@ def permute(ptr, ind, val, row_perm: np.ndarray | None, col_perm: np.ndarray | N
     return _sort_rows(ptr64, ind, val)
 
 
-def planted(n: int, blocks: int, nnz_per_row: int, seed: int, in_frac: float = 0.8) -> Csr:
+def planted(n: int, blocks: int, nnz_per_row: int, seed: int, in_frac: float = 0.8,
+            planted_rows: bool = False) -> Csr:
     """Planted-block matrix: row i of block b has round(in_frac*nnz_per_row)
     distinct columns inside b's column range and the rest uniform over all
     columns (all distinct); values U(-1,1); then independent random row and
-    column permutations."""
+    column permutations.  With planted_rows the rows keep the planted block
+    order (the row permutation is drawn, so the columns are the same, but
+    not applied): the blocks' rows are contiguous and share their in-block
+    columns, which the column permutation scatters."""
     rng = _rng(seed)
     sizes = np.full(blocks, n // blocks, np.int64)
     sizes[: n % blocks] += 1
@@ -99,6 +103,8 @@ def planted(n: int, blocks: int, nnz_per_row: int, seed: int, in_frac: float = 0
     vals = rng.uniform(-1.0, 1.0, size=(n, nnz_per_row)).astype(np.float32)
     row_perm = rng.permutation(n)
     col_perm = rng.permutation(n)
+    if planted_rows:
+        row_perm = np.arange(n)
     # Every row has the same length, so the permutations and the per-row sort
     # work on the dense (n, nnz_per_row) layout.
     inv = np.empty(n, np.int64)
@@ -116,8 +122,9 @@ def config1(seed: int = 1) -> Csr:
     return planted(20_000, 256, 10, seed)
 
 
-def config2(seed: int = 2, n: int = 1_048_576, blocks: int = 16_384) -> Csr:
-    return planted(n, blocks, 16, seed)
+def config2(seed: int = 2, n: int = 1_048_576, blocks: int = 16_384,
+            planted_rows: bool = False) -> Csr:
+    return planted(n, blocks, 16, seed, planted_rows=planted_rows)
 
 
 def rmat(scale: int, edge_factor: int, seed: int, a=0.57, b=0.19, c=0.19) -> Csr:

@@ -305,7 +305,7 @@ SPORDER_API void sporder_spmm_csr(sporder_context_t ctx, int32_t n,
  * SpMM.  sporder_spmm_plan_create analyses a CSR pattern on the device in
  * blocks of 8 consecutive rows: a block's entries are the distinct columns of
  * its rows, each with the mask of rows holding it.  A tile of 64 rows whose
- * entries number at most 60 % of its nonzeros (rows that share columns:
+ * entries number at most half its nonzeros (rows that share columns:
  * bands, meshes in natural order, rows grouped by a reordering) is
  * "blocked": sporder_spmm_csr_plan computes each of its blocks with one load
  * of each entry's B row, applied to every row of the block that holds the

@@ -122,7 +122,7 @@ def test_planned_spmm_equals_row_split(sporder, plans, name, N):
 def plan_model(ptr, ind):
     """The plan rule restated: 8-row blocks' entries are their distinct
     columns; a 64-row tile is blocked when no row has more than 512
-    nonzeros and 5 * entries <= 3 * nonzeros."""
+    nonzeros and 2 * entries <= nonzeros."""
     n = ptr.shape[0] - 1
     out = {"tiles": (n + 63) // 64, "blocked_tiles": 0, "blocked_rows": 0, "blocked_nnz": 0,
            "entries": 0}
@@ -132,7 +132,7 @@ def plan_model(ptr, ind):
         if m == 0 or (np.diff(ptr[r0:r1 + 1]) > 512).any():
             continue
         e = sum(np.unique(ind[ptr[b]:ptr[min(b + 8, r1)]]).size for b in range(r0, r1, 8))
-        if 5 * e <= 3 * m:
+        if 2 * e <= m:
             out["blocked_tiles"] += 1
             out["blocked_rows"] += r1 - r0
             out["blocked_nnz"] += m
