@@ -60,12 +60,12 @@ struct Context {
   size_t lds_per_block = 0;
   Workspace ws;
   Workspace aux; // second grow-only buffer, for temporaries sized mid-call
-  // Two more streams (default priority) for independent kernels of one call,
-  // forked from and joined back into `stream` with the events below, so a
-  // synchronize of `stream` also waits for their work.
-  hipStream_t side[2] = {};
+  // Three more streams (default priority) for independent kernels of one
+  // call, forked from and joined back into `stream` with the events below, so
+  // a synchronize of `stream` also waits for their work.
+  hipStream_t side[3] = {};
   hipEvent_t fork_ev = nullptr;
-  hipEvent_t join_ev[2] = {};
+  hipEvent_t join_ev[3] = {};
   hipEvent_t prep_ev = nullptr; // a stage's preparation done (csg's global path)
   // Pinned host words for small device-to-host readbacks.
   int32_t *host_words = nullptr;

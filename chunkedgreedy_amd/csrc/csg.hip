@@ -33,6 +33,7 @@
 
 #include <algorithm>
 #include <chrono>
+#include <cstring>
 #include <type_traits>
 
 namespace sporder_hip {
@@ -748,6 +749,110 @@ void validate_sketch_args(int32_t k, float oversampling, int32_t chunk_size) {
   SP_EXPECT(m <= 512, "expect k * oversampling <= 512");
 }
 
+// ---- is_symmetric: the CSR read as its own CSC ------------------------------
+//
+// With is_symmetric the reference takes the CSR as the CSC
+// (sporder/src/common/csr2csc.h:49-59): column c's list is row c.  The
+// chunk-local sketch transposes each chunk's rows instead.  For input that
+// meets the reference's precondition of sorted columns within each row
+// (sporder/include/sporder.h:27) the two agree exactly when the pattern is
+// symmetric as a multiset (as many (r, c) as (c, r) for every pair).
+// mirror_check_kernel sums sign(c - r) * H(min(r, c), max(r, c)) mod 2^64 over
+// the nonzeros, with H the splitmix64 finalizer (Steele, Lea and Flood,
+// OOPSLA 2014) of the packed pair.  A symmetric pattern sums to exactly zero;
+// an asymmetric one leaves (count(a, b) - count(b, a)) * H(a, b) terms, which
+// cancel only through a 64-bit hash collision.  A call whose sum is not zero
+// is run again with every chunk on the global path, which reads the CSR as
+// the CSC like the reference.
+
+__device__ __forceinline__ uint64_t mirror_hash(uint32_t a, uint32_t b) {
+  uint64_t x = ((static_cast<uint64_t>(a) << 32) | b) + 0x9e3779b97f4a7c15ull;
+  x = (x ^ (x >> 30)) * 0xbf58476d1ce4e5b9ull;
+  x = (x ^ (x >> 27)) * 0x94d049bb133111ebull;
+  return x ^ (x >> 31);
+}
+
+// One wave per 64 rows (grid-stride); lane l holds the end of row r0 + l and
+// each nonzero finds its row by a binary search over those ends (bpermute
+// reads, taken with every lane active).  *out gathers the signed hash sum.
+__global__ void __launch_bounds__(256)
+    mirror_check_kernel(int32_t n, const int32_t *__restrict__ ptr,
+                        const int32_t *__restrict__ ind, unsigned long long *out) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t groups = ceil_div64(n, kWave);
+  const int64_t step = static_cast<int64_t>(gridDim.x) * (blockDim.x / kWave);
+  uint64_t sum = 0;
+  for (int64_t gi = blockIdx.x * static_cast<int64_t>(blockDim.x / kWave) + threadIdx.x / kWave;
+       gi < groups; gi += step) {
+    const int32_t r0 = static_cast<int32_t>(gi * kWave);
+    const int32_t rows = static_cast<int32_t>(min<int64_t>(kWave, n - r0));
+    const int32_t p0 = ptr[r0], p1 = ptr[r0 + rows];
+    // Lanes past the last row repeat its end, so the ends stay non-decreasing.
+    const int32_t e = lane < rows ? ptr[r0 + lane + 1] : p1;
+    for (int32_t base = p0; base < p1; base += kWave) {
+      const int32_t p = base + lane;
+      // Offset of p's row: the number of lanes whose row ends at or before p
+      // (at most rows - 1 for p < p1, since lane rows - 1 ends at p1).
+      int lo = 0;
+#pragma unroll
+      for (int s = kWave / 2; s > 0; s >>= 1) {
+        if (__shfl(e, lo + s - 1) <= p) lo += s;
+      }
+      if (p < p1) {
+        const int32_t r = r0 + lo, c = ind[p];
+        if (c != r) {
+          const uint64_t h = mirror_hash(static_cast<uint32_t>(min(r, c)),
+                                         static_cast<uint32_t>(max(r, c)));
+          sum += c > r ? h : 0ull - h;
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int o = kWave / 2; o > 0; o >>= 1) {
+    sum += __shfl_xor(static_cast<unsigned long long>(sum), o);
+  }
+  if (lane == 0 && sum != 0) atomicAdd(out, static_cast<unsigned long long>(sum));
+}
+
+// A queued mirror check: its device words and whether it was queued.
+struct MirrorCheck {
+  unsigned long long *dev = nullptr;
+  bool queued = false;
+};
+
+constexpr int kMirrorHostWord = 8; // host_words[8..9] receive the sum
+
+// Queues the check on side stream 2, forked from the library stream so it
+// runs beside the sketch; mirror_collect joins it back.
+void mirror_check(Context &ctx, int32_t n, const int32_t *d_ptr, const int32_t *d_ind,
+                  MirrorCheck *m) {
+  m->dev = ctx.take<unsigned long long>(1);
+  fork_side(ctx, 2);
+  OnStream on(ctx, ctx.side[2]);
+  zero_words(ctx, m->dev, sizeof(unsigned long long));
+  const int g = ctx.grid_for(ceil_div64(ceil_div64(n, kWave), 4), 256, 2);
+  mirror_check_kernel<<<g, 256, 0, ctx.stream>>>(n, d_ptr, d_ind, m->dev);
+  SP_LAUNCH_CHECK();
+  m->queued = true;
+}
+
+// Joins the check into the library stream and queues the copy of its result;
+// the caller's synchronize makes mirror_failed valid.
+void mirror_collect(Context &ctx, const MirrorCheck &m) {
+  if (!m.queued) return;
+  join_side(ctx, 2);
+  SP_HIP(hipMemcpyAsync(ctx.host_words + kMirrorHostWord, m.dev, sizeof(unsigned long long),
+                        hipMemcpyDeviceToHost, ctx.stream));
+}
+
+bool mirror_failed(const Context &ctx, const MirrorCheck &m) {
+  if (!m.queued) return false;
+  unsigned long long sum;
+  std::memcpy(&sum, ctx.host_words + kMirrorHostWord, sizeof(sum));
+  return sum != 0;
+}
+
 // ---- table construction (both paths) ---------------------------------------
 
 size_t table_ws_bytes(int32_t n, int32_t nnz, int32_t k, int32_t chunk_size,
@@ -759,21 +864,29 @@ size_t table_ws_bytes(int32_t n, int32_t nnz, int32_t k, int32_t chunk_size,
   if (!is_symmetric) {
     b += ws_bytes<int32_t>(static_cast<size_t>(n) + 1) +
          ws_bytes<int32_t>(static_cast<size_t>(nnz)) + csr2csc_ws_bytes(n, nnz);
+  } else {
+    b += ws_bytes<unsigned long long>(1);
   }
   return b;
 }
 
 // Fills `table` (n*k) for the chunked sketch, and `row_valid` (n, when given)
 // with each row's number of valid entries.  Records the transpose and
-// similarity spans when the spans are enabled.
+// similarity spans when the spans are enabled.  With `allow_local` false every
+// chunk takes the global path.  When is_symmetric chunks go to the chunk-local
+// sketch, the mirror check is queued into `mirror`; the caller collects it and,
+// if it failed, builds the table again with `allow_local` false.
 void build_table(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
                  const int32_t *d_ind, bool is_symmetric, int32_t k, int32_t m_cap,
                  int32_t chunk_size, uint64_t *table, EventSpan *t_csc,
-                 EventSpan *t_sim, int32_t *row_valid = nullptr) {
+                 EventSpan *t_sim, MirrorCheck *mirror, bool allow_local,
+                 int32_t *row_valid = nullptr) {
   const int64_t chunks = ceil_div64(n, chunk_size);
   int32_t *lists = ctx.take<int32_t>(2 * static_cast<size_t>(chunks));
   int32_t *counts = ctx.take<int32_t>(2);
-  const bool local = chunk_local_supported(n, chunk_size);
+  const bool local = allow_local && chunk_local_supported(n, chunk_size);
+  // Forked before any sketch work so that it waits on nothing of this call.
+  if (local && is_symmetric) mirror_check(ctx, n, d_ptr, d_ind, mirror);
 
   auto global_csc = [&](const int32_t **cp, const int32_t **ri) {
     // Reference: sporder/src/common/csr2csc.h:49-59.
@@ -858,10 +971,11 @@ struct SeriationOut {
   float csr2csc_ms = 0.0f, similarity_ms = 0.0f, chunk_greedy_ms = 0.0f;
 };
 
-SeriationOut seriate(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
-                     const int32_t *d_ind, bool is_symmetric, int32_t k, int32_t m_cap,
-                     int32_t sketch_chunk, int32_t chain_chunk, int32_t *d_new_order,
-                     bool want_stats, bool want_timing) {
+SeriationOut seriate_pass(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
+                          const int32_t *d_ind, bool is_symmetric, int32_t k, int32_t m_cap,
+                          int32_t sketch_chunk, int32_t chain_chunk, int32_t *d_new_order,
+                          bool want_stats, bool want_timing, bool allow_local,
+                          bool *redo) {
   const int64_t num_chunks = ceil_div64(n, chain_chunk);
   const int32_t rows_max = static_cast<int32_t>(std::min<int64_t>(chain_chunk, n));
   // The compact chain packs a staged entry's slice position into 20 bits, so
@@ -914,8 +1028,9 @@ SeriationOut seriate(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
     zero_words(ctx, totals, sizeof(TopKTotals));
   }
 
+  MirrorCheck mirror;
   build_table(ctx, n, nnz, d_ptr, d_ind, is_symmetric, k, m_cap, sketch_chunk, table, &t_csc,
-              &t_sim, row_valid);
+              &t_sim, &mirror, allow_local, row_valid);
   if (want_stats) top_k_stats(ctx, n, k, table, totals);
 
   t_greedy.begin(ctx.stream);
@@ -950,7 +1065,9 @@ SeriationOut seriate(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
     SP_HIP(hipMemcpyAsync(&out.ht, totals, sizeof(out.ht), hipMemcpyDeviceToHost,
                           ctx.stream));
   }
+  mirror_collect(ctx, mirror);
   ctx.sync();
+  *redo = mirror_failed(ctx, mirror);
   if (want_timing) {
     out.csr2csc_ms = t_csc.ms();
     out.similarity_ms = t_sim.ms();
@@ -959,6 +1076,24 @@ SeriationOut seriate(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
   t_csc.destroy();
   t_sim.destroy();
   t_greedy.destroy();
+  return out;
+}
+
+// One seriation; a call with is_symmetric whose pattern fails the mirror
+// check is run again with every sketch chunk on the global path, which
+// rewrites the order, counters and spans.
+SeriationOut seriate(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
+                     const int32_t *d_ind, bool is_symmetric, int32_t k, int32_t m_cap,
+                     int32_t sketch_chunk, int32_t chain_chunk, int32_t *d_new_order,
+                     bool want_stats, bool want_timing) {
+  bool redo = false;
+  SeriationOut out = seriate_pass(ctx, n, nnz, d_ptr, d_ind, is_symmetric, k, m_cap,
+                                  sketch_chunk, chain_chunk, d_new_order, want_stats,
+                                  want_timing, true, &redo);
+  if (redo) {
+    out = seriate_pass(ctx, n, nnz, d_ptr, d_ind, is_symmetric, k, m_cap, sketch_chunk,
+                       chain_chunk, d_new_order, want_stats, want_timing, false, &redo);
+  }
   return out;
 }
 
@@ -1077,16 +1212,22 @@ void sporder_chunk_similarity_top_k(sporder_context_t h, int32_t n, int32_t nnz,
   SP_EXPECT(n >= 1 && nnz >= 0, "expect n >= 1 and nnz >= 0");
   validate_sketch_args(k, oversampling, chunk_size);
   Context &ctx = h->impl;
-  ctx.reserve(table_ws_bytes(n, nnz, k, chunk_size, is_symmetric));
-  uint64_t *table = ctx.take<uint64_t>(static_cast<size_t>(n) * k);
-  EventSpan off_a, off_b;
-  build_table(ctx, n, nnz, d_ptr, d_ind, is_symmetric, k, sketch_m(k, oversampling),
-              chunk_size, table, &off_a, &off_b);
-  int64_t count = static_cast<int64_t>(n) * k;
-  int g = ctx.grid_for(ceil_div64(count, 256), 256, 4);
-  unpack_table_kernel<<<g, 256, 0, ctx.stream>>>(count, table, d_indices, d_weights);
-  SP_LAUNCH_CHECK();
-  ctx.sync();
+  // A second pass, on the global path, when is_symmetric fails the mirror check.
+  for (bool allow_local = true;; allow_local = false) {
+    ctx.reserve(table_ws_bytes(n, nnz, k, chunk_size, is_symmetric));
+    uint64_t *table = ctx.take<uint64_t>(static_cast<size_t>(n) * k);
+    EventSpan off_a, off_b;
+    MirrorCheck mirror;
+    build_table(ctx, n, nnz, d_ptr, d_ind, is_symmetric, k, sketch_m(k, oversampling),
+                chunk_size, table, &off_a, &off_b, &mirror, allow_local);
+    int64_t count = static_cast<int64_t>(n) * k;
+    int g = ctx.grid_for(ceil_div64(count, 256), 256, 4);
+    unpack_table_kernel<<<g, 256, 0, ctx.stream>>>(count, table, d_indices, d_weights);
+    SP_LAUNCH_CHECK();
+    mirror_collect(ctx, mirror);
+    ctx.sync();
+    if (!mirror_failed(ctx, mirror)) break;
+  }
 }
 
 void sporder_similarity_graph(sporder_context_t h, int32_t n, int32_t nnz,
@@ -1110,30 +1251,36 @@ void sporder_similarity_graph(sporder_context_t h, int32_t n, int32_t nnz,
     stats->k_used = k;
     stats->m_used = m_cap;
   }
-  ctx.reserve(table_ws_bytes(n, nnz, k, n, is_symmetric) + ws_bytes<TopKTotals>(1));
-  uint64_t *table = ctx.take<uint64_t>(static_cast<size_t>(n) * k);
-  TopKTotals *totals = ctx.take<TopKTotals>(1);
   EventSpan t_csc, t_sim, t_unpack;
   t_csc.create(timing != nullptr);
   t_sim.create(timing != nullptr);
   t_unpack.create(timing != nullptr);
-
-  build_table(ctx, n, nnz, d_ptr, d_ind, is_symmetric, k, m_cap, n, table, &t_csc, &t_sim);
-  if (stats) {
-    zero_words(ctx, totals, sizeof(TopKTotals));
-    top_k_stats(ctx, n, k, table, totals);
-  }
-  int64_t count = static_cast<int64_t>(n) * k;
-  int g = ctx.grid_for(ceil_div64(count, 256), 256, 4);
-  t_unpack.begin(ctx.stream);
-  unpack_table_kernel<<<g, 256, 0, ctx.stream>>>(count, table, d_indices, d_weights);
-  SP_LAUNCH_CHECK();
-  t_unpack.end(ctx.stream);
   TopKTotals ht{};
-  if (stats) {
-    SP_HIP(hipMemcpyAsync(&ht, totals, sizeof(ht), hipMemcpyDeviceToHost, ctx.stream));
+  // A second pass, on the global path, when is_symmetric fails the mirror check.
+  for (bool allow_local = true;; allow_local = false) {
+    ctx.reserve(table_ws_bytes(n, nnz, k, n, is_symmetric) + ws_bytes<TopKTotals>(1));
+    uint64_t *table = ctx.take<uint64_t>(static_cast<size_t>(n) * k);
+    TopKTotals *totals = ctx.take<TopKTotals>(1);
+    MirrorCheck mirror;
+    build_table(ctx, n, nnz, d_ptr, d_ind, is_symmetric, k, m_cap, n, table, &t_csc, &t_sim,
+                &mirror, allow_local);
+    if (stats) {
+      zero_words(ctx, totals, sizeof(TopKTotals));
+      top_k_stats(ctx, n, k, table, totals);
+    }
+    int64_t count = static_cast<int64_t>(n) * k;
+    int g = ctx.grid_for(ceil_div64(count, 256), 256, 4);
+    t_unpack.begin(ctx.stream);
+    unpack_table_kernel<<<g, 256, 0, ctx.stream>>>(count, table, d_indices, d_weights);
+    SP_LAUNCH_CHECK();
+    t_unpack.end(ctx.stream);
+    if (stats) {
+      SP_HIP(hipMemcpyAsync(&ht, totals, sizeof(ht), hipMemcpyDeviceToHost, ctx.stream));
+    }
+    mirror_collect(ctx, mirror);
+    ctx.sync();
+    if (!mirror_failed(ctx, mirror)) break;
   }
-  ctx.sync();
   if (timing) {
     timing->csr2csc_ms = t_csc.ms();
     timing->similarity_ms = t_sim.ms();

@@ -416,3 +416,77 @@ def test_greedy_staging_capacity(sporder, case):
     o, _ = oracle.chunk_similarity_greedy(ptr, ind, is_symmetric=True, k=16, oversampling=4.0,
                                           chunk_size=chunk)
     assert np.array_equal(g.cpu().numpy(), o)
+
+
+def drop_one_mirror(ptr, ind, chunk):
+    """Remove one nonzero (a, b), a < b in one chunk, whose mirror (b, a) stays."""
+    n = ptr.shape[0] - 1
+    rows = np.repeat(np.arange(n), np.diff(ptr))
+    pick = np.nonzero((ind > rows) & (ind // chunk == rows // chunk))[0][0]
+    keep = np.ones(ind.shape[0], bool)
+    keep[pick] = False
+    p = ptr.astype(np.int64).copy()
+    p[rows[pick] + 1:] -= 1
+    return p.astype(np.int32), ind[keep]
+
+
+def asymmetric_cases():
+    """Non-symmetric patterns passed with is_symmetric=True: (ptr, ind, chunk)."""
+    hubs = {5: 12000, 6: 9000, 20000: 12000, 20001: 12000, 20002: 10000, 39998: 7000}
+    st = synth.stencil7(20, 13, scramble=False)[:2]
+    return {
+        "one_missing_mirror_local": (*drop_one_mirror(*st, 256), 256),
+        "random_local_and_overflow_4096": (*dense_random(12000, 40, 31, False), 4096),
+        "random_local_and_overflow_1500": (*dense_random(12000, 40, 31, False), 1500),
+        "hubs_three_tiers": (*hub_matrix(40000, 8, hubs, 41, False), 4),
+    }
+
+
+ASYM = asymmetric_cases()
+
+
+@pytest.mark.parametrize("name", sorted(ASYM))
+def test_is_symmetric_on_asymmetric_pattern_reads_csr_as_csc(sporder, name):
+    """is_symmetric=True on a pattern that is not symmetric: the reference
+    reads the CSR as its own CSC for every chunk (csr2csc.h:49-59).  The
+    chunk-local tiers would build the true transpose, so the mirror check
+    sends such a call through the global path; table, csg order and stats
+    equal the oracle's CSR-as-CSC result.  Each case is one the true
+    transpose would change (checked on the oracle)."""
+    ptr, ind, chunk = ASYM[name]
+    assert not synth.is_pattern_symmetric(ptr, ind)
+    k, ovs = 16, 4.0
+    as_csc = oracle.chunk_similarity_top_k(ptr, ind, k, chunk, ovs, is_symmetric=True)
+    transposed = oracle.chunk_similarity_top_k(ptr, ind, k, chunk, ovs, is_symmetric=False)
+    assert not np.array_equal(as_csc, transposed)
+    check_table(sporder, ptr, ind, k, ovs, chunk, True)
+    dptr, dind = dev_csr(ptr, ind)
+    g, s = sporder.chunk_similarity_greedy(dptr, dind, is_symmetric=True, k=k, oversampling=ovs,
+                                           chunk_size=chunk, with_stats=True)
+    o, os_ = oracle.chunk_similarity_greedy(ptr, ind, is_symmetric=True, k=k, oversampling=ovs,
+                                            chunk_size=chunk)
+    assert np.array_equal(g.cpu().numpy(), o)
+    assert s["chain_restarts"] == os_["chain_restarts"]
+    assert s["zero_degree_rows"] == os_["zero_degree_rows"]
+    g2 = sporder.chunk_greedy(dptr, dind, is_symmetric=True, k=k, oversampling=ovs,
+                              chunk_size=chunk)
+    o2, _ = oracle.chunk_greedy(ptr, ind, is_symmetric=True, k=k, oversampling=ovs,
+                                chunk_size=chunk)
+    assert np.array_equal(g2.cpu().numpy(), o2)
+
+
+def test_is_symmetric_one_chunk_similarity_graph(sporder):
+    """The one-chunk global sketch (similarity_graph, n within the LDS tiers)
+    with is_symmetric=True on a non-symmetric pattern equals the oracle's
+    CSR-as-CSC table; the same call on the symmetric pattern stays on the
+    chunk-local tier and is still exact."""
+    ptr, ind = dense_random(3000, 6, 71, False)
+    sptr, sind = dense_random(3000, 3, 71, True)
+    for p, i in ((ptr, ind), (sptr, sind)):
+        n = p.shape[0] - 1
+        dptr, dind = dev_csr(p, i)
+        gi, gw = sporder.similarity_graph(dptr, dind, is_symmetric=True, k=16, oversampling=2.0)
+        oi, ow = oracle.unpack_table(
+            oracle.chunk_similarity_top_k(p, i, 16, n, 2.0, is_symmetric=True))
+        assert np.array_equal(gi.cpu().numpy(), oi)
+        assert np.array_equal(weight_bits(gw.cpu().numpy()), weight_bits(ow))
