@@ -173,6 +173,12 @@ void spmm_rowsplit_tiles(Context &ctx, int32_t n, int32_t nnz, const int32_t *pt
 size_t scan_tmp_elems(int64_t count);
 void scan_i32(Context &ctx, const int32_t *in, int32_t *out, int64_t count,
               bool inclusive, int32_t *tmp);
+// The same scan when totals[t] already holds the sum of elements
+// [t * kScanTileElems, (t + 1) * kScanTileElems) (totals sized as `tmp`
+// above; overwritten).
+constexpr int kScanTileElems = 4096;
+void scan_i32_from_totals(Context &ctx, const int32_t *in, int32_t *out, int64_t count,
+                          bool inclusive, int32_t *totals);
 
 // Stable LSD radix sort of (key, value) pairs on the low `key_bits` bits.
 // Input in keys_in/vals_in (preserved), result in keys_out/vals_out; the

@@ -16,6 +16,7 @@
 #include "common.hpp"
 
 #include <algorithm>
+#include <cstring>
 #include <vector>
 
 namespace sporder_hip {
@@ -28,6 +29,7 @@ constexpr int kBlockSortThreads = 256;
 // Rows longer than kBigRow entries are copied by copy_big_rows in units of
 // kCopyUnit entries spread over the whole GPU, not by one lane group.
 constexpr int kBigRow = 1024;
+constexpr int kPrepBlock = 1024;
 constexpr int kCopyUnit = 4096;
 
 struct BigRow {
@@ -40,27 +42,88 @@ struct BigCtl {
   int32_t rows;
   int32_t units;
 };
+// One call's control words, zeroed by prepare_rows and read back once after
+// permute_rows: the three sort-list counts, the wide-remap flag, the big-row
+// registry's counts.
+struct Ctl {
+  int32_t counts[3];
+  int32_t wide;
+  BigCtl big;
+};
 
 int64_t max_big_rows(int32_t nnz) { return nnz / (kBigRow + 1) + 1; }
 int64_t max_copy_units(int32_t nnz) { return nnz / kCopyUnit + max_big_rows(nnz) + 1; }
 
-__global__ void gather_row_lengths(int32_t n, const int32_t *__restrict__ ptr_old,
-                                   const int32_t *__restrict__ new2old,
-                                   int32_t *__restrict__ ptr_new) {
-  for (int64_t p = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
-       p < n; p += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    int32_t o = new2old[p];
-    ptr_new[p + 1] = ptr_old[o + 1] - ptr_old[o];
-    if (p == 0) ptr_new[0] = 0;
+// Per new row p, with o = new2old[p]: src_new[p] = ptr_old[o] (where the old
+// row starts), ptr_new[p + 1] = the row's length (ptr_new[0] = 0, so an
+// inclusive scan gives the offsets) and, when old2new is given, old2new[o] = p.
+// Doing the two dependent loads here leaves permute_rows one coalesced load
+// before its row gathers.  One workgroup per scan tile of ptr_new (elements
+// [t * kScanTileElems, (t + 1) * kScanTileElems), element i = p + 1), whose
+// sum goes to totals[t], so the scan starts at its second pass.  Block 0 also
+// zeroes the call's control words.
+__global__ void __launch_bounds__(kPrepBlock)
+    prepare_rows(int32_t n, const int32_t *__restrict__ ptr_old,
+                 const int32_t *__restrict__ new2old, int32_t *__restrict__ ptr_new,
+                 int32_t *__restrict__ src_new, int32_t *__restrict__ old2new,
+                 int32_t *__restrict__ totals, Ctl *__restrict__ ctl) {
+  __shared__ int32_t s_wave[kPrepBlock / kWave];
+  if (blockIdx.x == 0 && threadIdx.x < sizeof(Ctl) / 4) {
+    reinterpret_cast<int32_t *>(ctl)[threadIdx.x] = 0;
+  }
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kScanTileElems;
+  int32_t sum = 0;
+#pragma unroll 4
+  for (int r = 0; r < kScanTileElems / kPrepBlock; ++r) {
+    const int64_t i = base + r * kPrepBlock + threadIdx.x;
+    if (i == 0) {
+      ptr_new[0] = 0;
+    } else if (i <= n) {
+      const int64_t p = i - 1;
+      const int32_t o = new2old[p];
+      const int32_t s = ptr_old[o];
+      const int32_t len = ptr_old[o + 1] - s;
+      src_new[p] = s;
+      ptr_new[i] = len;
+      if (old2new) old2new[o] = static_cast<int32_t>(p);
+      sum += len;
+    }
+  }
+  sum = wave_sum(sum);
+  if (lane_id() == 0) s_wave[threadIdx.x / kWave] = sum;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int32_t t = 0;
+#pragma unroll
+    for (int w = 0; w < kPrepBlock / kWave; ++w) t += s_wave[w];
+    totals[blockIdx.x] = t;
   }
 }
 
-__global__ void invert_perm(int32_t n, const int32_t *__restrict__ src,
-                            int32_t *__restrict__ dst) {
-  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
-       i < n; i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    dst[src[i]] = static_cast<int32_t>(i);
+// delta[c] = old2new[c] - c as 16 bits, for the column remap: a permutation
+// that moves every index by less than 2^15 (csg's, whose chains stay inside
+// chunks of at most 32768 rows, among them) gets a table half the size of
+// old2new, which stays in L2 where the 4-byte table at n = 2^20 fills it.  Any
+// larger move sets ctl->wide, and permute_rows then reads old2new.
+__global__ void __launch_bounds__(256)
+    narrow_map(int32_t n, const int32_t *__restrict__ old2new, int16_t *__restrict__ delta,
+               Ctl *__restrict__ ctl) {
+  __shared__ int32_t s_far;
+  if (threadIdx.x == 0) s_far = 0;
+  __syncthreads();
+  bool far = false;
+  for (int64_t c = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; c < n;
+       c += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int32_t d = old2new[c] - static_cast<int32_t>(c);
+    far |= d < -32768 || d > 32767;
+    delta[c] = static_cast<int16_t>(d);
   }
+  if (far) s_far = 1;
+  __syncthreads();
+  // One atomic per workgroup (the grid is a few per CU): a random permutation
+  // sets the flag from every workgroup, and per-wave atomics on one word
+  // would serialise.
+  if (threadIdx.x == 0 && s_far != 0) atomicOr(&ctl->wide, 1);
 }
 
 // Appends `value` for every lane with `take` to list[*count ...]: one atomic
@@ -76,125 +139,167 @@ __device__ __forceinline__ void wave_append(bool take, int32_t value, int32_t *l
   if (take) list[base + __popcll(m & ((1ull << lane_id()) - 1ull))] = value;
 }
 
-// G lanes per new row (64/G rows per wave).  Copies old row new2old[p] to row
-// p, mapping columns through col_map when given.  With col_map (SYMMETRIC) a
-// row of at most G entries is also sorted in registers (bitonic network over
-// the group's lanes) and written in final order; a longer row is written
-// unsorted to key_tmp/val_tmp and appended to the list of the stage that
-// sorts it: lists[0] (up to kWaveSortCap entries, sort_rows_wave), lists[1]
-// (up to kBlockSortCap, sort_rows_block), lists[2] (longer, the device-wide
-// sort), with counts in counts[0..2].  Without col_map (ROWS) rows are copied
-// verbatim.  Rows past kBigRow entries are registered for copy_big_rows
-// instead of copied here.  All list and registry appends take one atomic per
-// wave.  With val_new set and val_old NULL the values written are 0.0f, as in
-// the reference's gather_rows (reorder.cu:37-45).
-template <int G>
+// G lanes per new row; a wave takes U groups of 64/G rows per iteration, and
+// their loads are issued together, so U gather chains (row entries, then the
+// column map) are in flight per wave instead of one.  Copies old row
+// new2old[p] (which starts at src_new[p]) to row p, mapping columns through
+// col_map when given.  With col_map (SYMMETRIC) a row of at most G entries is
+// also sorted in registers (bitonic network over the group's lanes) and
+// written in final order; a longer row is appended to the list of the stage
+// that sorts it, with counts in ctl->counts[0..2]: lists[0] (up to
+// kWaveSortCap entries, sort_rows_wave, which reads the row written here
+// unsorted to key_tmp/val_tmp), lists[1] (up to kBlockSortCap,
+// sort_rows_block, which gathers the old row itself), lists[2] (longer, the
+// device-wide sort, whose rows are registered for copy_big_rows).  Without
+// col_map (ROWS) rows are copied verbatim, and rows past kBigRow entries are
+// registered for copy_big_rows.  All list and registry appends take one
+// atomic per wave.  With val_new set and val_old NULL the values written are
+// 0.0f, as in the reference's gather_rows (reorder.cu:37-45).
+template <int G, int U>
 __global__ void __launch_bounds__(256)
-    permute_rows(int32_t n, const int32_t *__restrict__ ptr_old,
+    permute_rows(int32_t n, const int32_t *__restrict__ src_new,
                  const int32_t *__restrict__ ind_old, const float *__restrict__ val_old,
-                 const int32_t *__restrict__ new2old, const int32_t *__restrict__ col_map,
-                 const int32_t *__restrict__ ptr_new, int32_t *__restrict__ ind_new,
-                 float *__restrict__ val_new, int32_t *__restrict__ key_tmp,
-                 float *__restrict__ val_tmp, int32_t *__restrict__ lists,
-                 int32_t *__restrict__ counts, int32_t list_stride, BigCtl *big_ctl,
+                 const int32_t *__restrict__ col_map, const int16_t *__restrict__ delta,
+                 const int32_t *__restrict__ ptr_new,
+                 int32_t *__restrict__ ind_new, float *__restrict__ val_new,
+                 int32_t *__restrict__ key_tmp, float *__restrict__ val_tmp,
+                 int32_t *__restrict__ lists, int32_t list_stride, Ctl *__restrict__ ctl,
                  BigRow *big_rows, int32_t *big_owner) {
   constexpr int kRowsPerWave = kWave / G;
+  // The 16-bit remap when narrow_map found every move within its range.
+  const bool narrow = delta != nullptr && ctl->wide == 0;
+  constexpr int kRowsPerIter = kRowsPerWave * U;
   const int lane = lane_id();
   const int gl = lane % G;
   const int64_t wave0 = (blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x) / kWave;
   const int64_t nwaves = static_cast<int64_t>(gridDim.x) * blockDim.x / kWave;
-  for (int64_t pb = wave0 * kRowsPerWave; pb < n; pb += nwaves * kRowsPerWave) {
-    const int64_t p = pb + lane / G;
-    const bool row_ok = p < n;
-    int32_t src = 0, len = 0, dst = 0;
-    if (row_ok) {
-      const int32_t o = new2old[p];
-      src = ptr_old[o];
-      len = ptr_old[o + 1] - src;
-      dst = ptr_new[p];
+  for (int64_t pb = wave0 * kRowsPerIter; pb < n; pb += nwaves * kRowsPerIter) {
+    int32_t src[U], len[U], dst[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t p = pb + u * kRowsPerWave + lane / G;
+      const bool ok = p < n;
+      src[u] = ok ? src_new[p] : 0;
+      dst[u] = ok ? ptr_new[p] : 0;
+      len[u] = ok ? ptr_new[p + 1] - dst[u] : 0;
     }
-    const bool sort_here = col_map != nullptr && len <= G;
-    if (sort_here) {
-      const bool in = gl < len;
-      int32_t key = in ? col_map[ind_old[src + gl]] : 0x7fffffff;
-      float v = (in && val_old) ? val_old[src + gl] : 0.0f;
+    if (col_map != nullptr) {
+      // Rows of at most G entries: gather, remap, sort, store.
+      int32_t key[U];
+      float v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const bool in = gl < len[u] && len[u] <= G;
+        key[u] = in ? ind_old[src[u] + gl] : 0;
+        v[u] = (in && val_old) ? val_old[src[u] + gl] : 0.0f;
+      }
+      if (narrow) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const bool in = gl < len[u] && len[u] <= G;
+          key[u] = in ? key[u] + delta[key[u]] : 0x7fffffff;
+        }
+      } else {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const bool in = gl < len[u] && len[u] <= G;
+          key[u] = in ? col_map[key[u]] : 0x7fffffff;
+        }
+      }
 #pragma unroll
       for (int kk = 2; kk <= G; kk <<= 1) {
 #pragma unroll
         for (int j = kk >> 1; j > 0; j >>= 1) {
-          const int32_t ok = lane_xor_i32(key, j);
-          const float ov = lane_xor_f32(v, j);
           const bool ascending = (gl & kk) == 0;
           const bool lower = (gl & j) == 0;
-          if ((ascending == lower) ? (ok < key) : (ok > key)) {
-            key = ok;
-            v = ov;
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            const int32_t ok = lane_xor_i32(key[u], j);
+            const float ov = lane_xor_f32(v[u], j);
+            if ((ascending == lower) ? (ok < key[u]) : (ok > key[u])) {
+              key[u] = ok;
+              v[u] = ov;
+            }
           }
         }
       }
-      if (in) {
-        ind_new[dst + gl] = key;
-        if (val_new) val_new[dst + gl] = v;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (gl < len[u] && len[u] <= G) {
+          __builtin_nontemporal_store(key[u], ind_new + dst[u] + gl);
+          if (val_new) __builtin_nontemporal_store(v[u], val_new + dst[u] + gl);
+        }
       }
-    } else if (row_ok && len <= kBigRow) {
-      int32_t *ki = col_map ? key_tmp : ind_new;
-      float *vo = col_map ? val_tmp : val_new;
-      // Four entries per lane in flight: the column gather depends on the
-      // index load, so one at a time would serialise two latencies per entry.
-      for (int32_t q0 = gl; q0 < len; q0 += 4 * G) {
-        int32_t c[4];
-        float v[4];
+    }
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int32_t q = q0 + u * G;
-          c[u] = q < len ? ind_old[src + q] : 0;
-          v[u] = (q < len && val_old) ? val_old[src + q] : 0.0f;
-        }
+    for (int u = 0; u < U; ++u) {
+      const int64_t p = pb + u * kRowsPerWave + lane / G;
+      const bool row_ok = p < n;
+      const bool sort_here = col_map != nullptr && len[u] <= G;
+      // Rows sorted above need no bookkeeping; most waves have only those.
+      if (ballot(row_ok && !sort_here) == 0) continue;
+      const int32_t copy_cap = col_map ? kWaveSortCap : kBigRow;
+      if (row_ok && !sort_here && len[u] <= copy_cap) {
+        int32_t *ki = col_map ? key_tmp : ind_new;
+        float *vo = col_map ? val_tmp : val_new;
+        // Four entries per lane in flight: the column gather depends on the
+        // index load, so one at a time would serialise two latencies per entry.
+        for (int32_t q0 = gl; q0 < len[u]; q0 += 4 * G) {
+          int32_t c[4];
+          float w[4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int32_t q = q0 + u * G;
-          if (q < len) c[u] = col_map ? col_map[c[u]] : c[u];
-        }
+          for (int t = 0; t < 4; ++t) {
+            const int32_t q = q0 + t * G;
+            c[t] = q < len[u] ? ind_old[src[u] + q] : 0;
+            w[t] = (q < len[u] && val_old) ? val_old[src[u] + q] : 0.0f;
+          }
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int32_t q = q0 + u * G;
-          if (q < len) {
-            ki[dst + q] = c[u];
-            if (vo) vo[dst + q] = v[u];
+          for (int t = 0; t < 4; ++t) {
+            const int32_t q = q0 + t * G;
+            if (q < len[u]) {
+              c[t] = narrow ? c[t] + delta[c[t]] : (col_map ? col_map[c[t]] : c[t]);
+            }
+          }
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const int32_t q = q0 + t * G;
+            if (q < len[u]) {
+              ki[dst[u] + q] = c[t];
+              if (vo) vo[dst[u] + q] = w[t];
+            }
           }
         }
       }
-    }
-    // Rows sorted here need no bookkeeping; most waves have only those.
-    if (ballot(row_ok && !sort_here) == 0) continue;
-    // Registry of big rows for copy_big_rows: unit bases from a wave scan.
-    const bool big = row_ok && gl == 0 && len > kBigRow;
-    const uint64_t mb = ballot(big);
-    if (mb != 0) {
-      const int32_t units = big ? (len + kCopyUnit - 1) / kCopyUnit : 0;
-      const int32_t incl = wave_incl_scan(units);
-      const int leader = __builtin_ctzll(mb);
-      int32_t rbase = 0, ubase = 0;
-      if (lane == leader) {
-        rbase = atomicAdd(&big_ctl->rows, __popcll(mb));
-        ubase = atomicAdd(&big_ctl->units, readlane(incl, kWave - 1));
+      // Registry of big rows for copy_big_rows: unit bases from a wave scan.
+      const bool big = row_ok && gl == 0 && len[u] > (col_map ? kBlockSortCap : kBigRow);
+      const uint64_t mb = ballot(big);
+      if (mb != 0) {
+        const int32_t units = big ? (len[u] + kCopyUnit - 1) / kCopyUnit : 0;
+        const int32_t incl = wave_incl_scan(units);
+        const int leader = __builtin_ctzll(mb);
+        int32_t rbase = 0, ubase = 0;
+        if (lane == leader) {
+          rbase = atomicAdd(&ctl->big.rows, __popcll(mb));
+          ubase = atomicAdd(&ctl->big.units, readlane(incl, kWave - 1));
+        }
+        rbase = readlane(rbase, leader);
+        ubase = readlane(ubase, leader);
+        if (big) {
+          const int32_t id = rbase + __popcll(mb & ((1ull << lane) - 1ull));
+          const int32_t base = ubase + incl - units;
+          big_rows[id] = BigRow{src[u], len[u], dst[u], base};
+          for (int32_t k = 0; k < units; ++k) big_owner[base + k] = id;
+        }
       }
-      rbase = readlane(rbase, leader);
-      ubase = readlane(ubase, leader);
-      if (big) {
-        const int32_t id = rbase + __popcll(mb & ((1ull << lane) - 1ull));
-        const int32_t base = ubase + incl - units;
-        big_rows[id] = BigRow{src, len, dst, base};
-        for (int32_t u = 0; u < units; ++u) big_owner[base + u] = id;
+      if (col_map != nullptr) {
+        const bool listed = row_ok && gl == 0 && !sort_here;
+        const int32_t row = static_cast<int32_t>(p);
+        wave_append(listed && len[u] <= kWaveSortCap, row, lists, ctl->counts);
+        wave_append(listed && len[u] > kWaveSortCap && len[u] <= kBlockSortCap, row,
+                    lists + list_stride, ctl->counts + 1);
+        wave_append(listed && len[u] > kBlockSortCap, row, lists + 2 * list_stride,
+                    ctl->counts + 2);
       }
-    }
-    if (col_map != nullptr) {
-      const bool listed = row_ok && gl == 0 && !sort_here;
-      const int32_t row = static_cast<int32_t>(p);
-      wave_append(listed && len <= kWaveSortCap, row, lists, counts);
-      wave_append(listed && len > kWaveSortCap && len <= kBlockSortCap, row,
-                  lists + list_stride, counts + 1);
-      wave_append(listed && len > kBlockSortCap, row, lists + 2 * list_stride, counts + 2);
     }
   }
 }
@@ -204,10 +309,9 @@ __global__ void __launch_bounds__(256)
 // when given), grid-striding over the units.
 __global__ void __launch_bounds__(256)
     copy_big_rows(const int32_t *__restrict__ ind_old, const float *__restrict__ val_old,
-                  const int32_t *__restrict__ col_map, const BigCtl *__restrict__ big_ctl,
+                  const int32_t *__restrict__ col_map, int32_t units,
                   const BigRow *__restrict__ big_rows, const int32_t *__restrict__ big_owner,
                   int32_t *__restrict__ ind_out, float *__restrict__ val_out) {
-  const int32_t units = big_ctl->units;
   for (int32_t u = blockIdx.x; u < units; u += gridDim.x) {
     const BigRow b = big_rows[big_owner[u]];
     const int32_t q0 = (u - b.base) * kCopyUnit;
@@ -289,13 +393,12 @@ __device__ __forceinline__ void wave_sort_row(int32_t s, int32_t len,
 // registers (64, 128, 256 or 512 slots by the row's length; longer rows sort
 // faster in a workgroup's LDS).
 __global__ void __launch_bounds__(256)
-    sort_rows_wave(const int32_t *__restrict__ rows, const int32_t *__restrict__ row_count,
+    sort_rows_wave(const int32_t *__restrict__ rows, int32_t count,
                    const int32_t *__restrict__ ptr, const int32_t *__restrict__ key_in,
                    const float *__restrict__ val_in, int32_t *__restrict__ key_out,
                    float *__restrict__ val_out) {
   const int64_t wave0 = (blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x) / kWave;
   const int64_t nwaves = static_cast<int64_t>(gridDim.x) * blockDim.x / kWave;
-  const int64_t count = *row_count;
   for (int64_t t = wave0; t < count; t += nwaves) {
     const int32_t r = rows[t];
     const int32_t s = ptr[r], len = ptr[r + 1] - s;
@@ -311,40 +414,41 @@ __global__ void __launch_bounds__(256)
   }
 }
 
-// Listed rows of kWaveSortCap+1 .. kBlockSortCap entries: LDS bitonic sort,
-// one workgroup per row.
+// Listed rows of kWaveSortCap+1 .. kBlockSortCap entries, one workgroup per
+// row: the old row (starting at src_new[r]) is gathered with its columns
+// remapped (the 16-bit delta table when `narrow`, else col_map), sorted in
+// LDS (bitonic) and written to row r.
 __global__ void __launch_bounds__(kBlockSortThreads)
-    sort_rows_block(const int32_t *__restrict__ ptr,
-                    const int32_t *__restrict__ long_rows,
-                    const int32_t *__restrict__ long_count,
-                    const int32_t *__restrict__ key_in,
-                    const float *__restrict__ val_in, int32_t *__restrict__ key_out,
-                    float *__restrict__ val_out) {
+    sort_rows_block(const int32_t *__restrict__ ptr, const int32_t *__restrict__ long_rows,
+                    int32_t long_count, const int32_t *__restrict__ src_new,
+                    const int32_t *__restrict__ ind_old, const float *__restrict__ val_old,
+                    const int32_t *__restrict__ col_map, const int16_t *__restrict__ delta,
+                    bool narrow, int32_t *__restrict__ key_out, float *__restrict__ val_out) {
   __shared__ int32_t sk[kBlockSortCap];
   __shared__ float sv[kBlockSortCap];
-  const int32_t count = *long_count;
-  for (int32_t t = blockIdx.x; t < count; t += gridDim.x) {
-    int32_t r = long_rows[t];
-    int32_t s = ptr[r], e = ptr[r + 1], len = e - s;
+  for (int32_t t = blockIdx.x; t < long_count; t += gridDim.x) {
+    const int32_t r = long_rows[t];
+    const int32_t s = ptr[r], len = ptr[r + 1] - s, src = src_new[r];
     int32_t pow2 = 1;
     while (pow2 < len) pow2 <<= 1;
     for (int32_t i = threadIdx.x; i < pow2; i += blockDim.x) {
-      bool in = i < len;
-      sk[i] = in ? key_in[s + i] : 0x7fffffff;
-      sv[i] = (in && val_in) ? val_in[s + i] : 0.0f;
+      const bool in = i < len;
+      const int32_t c = in ? ind_old[src + i] : 0;
+      sk[i] = in ? (narrow ? c + delta[c] : col_map[c]) : 0x7fffffff;
+      sv[i] = (in && val_old) ? val_old[src + i] : 0.0f;
     }
     __syncthreads();
     for (int32_t kk = 2; kk <= pow2; kk <<= 1) {
       for (int32_t j = kk >> 1; j > 0; j >>= 1) {
         for (int32_t i = threadIdx.x; i < pow2; i += blockDim.x) {
-          int32_t partner = i ^ j;
+          const int32_t partner = i ^ j;
           if (partner > i) {
-            bool ascending = (i & kk) == 0;
-            int32_t a = sk[i], b = sk[partner];
+            const bool ascending = (i & kk) == 0;
+            const int32_t a = sk[i], b = sk[partner];
             if ((a > b) == ascending) {
               sk[i] = b;
               sk[partner] = a;
-              float fa = sv[i];
+              const float fa = sv[i];
               sv[i] = sv[partner];
               sv[partner] = fa;
             }
@@ -470,45 +574,48 @@ void sort_huge_rows(Context &ctx, int32_t n, const int32_t *ptr_new, const int32
 }
 
 template <int G>
-void launch_permute_g(Context &ctx, int32_t n, const int32_t *ptr_old, const int32_t *ind_old,
-                      const float *val_old, const int32_t *new2old, const int32_t *col_map,
+void launch_permute_g(Context &ctx, int32_t n, const int32_t *src_new, const int32_t *ind_old,
+                      const float *val_old, const int32_t *col_map, const int16_t *delta,
                       const int32_t *ptr_new, int32_t *ind_new, float *val_new,
-                      int32_t *key_tmp, float *val_tmp, int32_t *lists, int32_t *counts,
-                      int32_t list_stride, BigCtl *big_ctl, BigRow *big_rows,
-                      int32_t *big_owner) {
-  constexpr int rows_per_block = 4 * (kWave / G);
+                      int32_t *key_tmp, float *val_tmp, int32_t *lists, int32_t list_stride,
+                      Ctl *ctl, BigRow *big_rows, int32_t *big_owner) {
+  constexpr int U = G <= 16 ? 4 : 2;
+  constexpr int rows_per_block = 4 * (kWave / G) * U;
   const int g = ctx.grid_for(ceil_div64(n, rows_per_block), 256, 4);
-  permute_rows<G><<<g, 256, 0, ctx.stream>>>(n, ptr_old, ind_old, val_old, new2old, col_map,
-                                            ptr_new, ind_new, val_new, key_tmp, val_tmp,
-                                            lists, counts, list_stride, big_ctl, big_rows,
-                                            big_owner);
+  permute_rows<G, U><<<g, 256, 0, ctx.stream>>>(n, src_new, ind_old, val_old, col_map, delta,
+                                                ptr_new, ind_new, val_new, key_tmp, val_tmp,
+                                                lists, list_stride, ctl, big_rows, big_owner);
   SP_LAUNCH_CHECK();
 }
 
-void launch_permute(Context &ctx, int G, int32_t n, const int32_t *ptr_old,
-                    const int32_t *ind_old, const float *val_old, const int32_t *new2old,
-                    const int32_t *col_map, const int32_t *ptr_new, int32_t *ind_new,
+void launch_permute(Context &ctx, int G, int32_t n, const int32_t *src_new,
+                    const int32_t *ind_old, const float *val_old, const int32_t *col_map,
+                    const int16_t *delta, const int32_t *ptr_new, int32_t *ind_new,
                     float *val_new, int32_t *key_tmp, float *val_tmp, int32_t *lists,
-                    int32_t *counts, int32_t list_stride, int32_t nnz, BigCtl *big_ctl,
-                    BigRow *big_rows, int32_t *big_owner) {
-  fill_u32(ctx, big_ctl, sizeof(BigCtl) / 4, 0u);
+                    int32_t list_stride, Ctl *ctl, BigRow *big_rows, int32_t *big_owner) {
   switch (G) {
 #define SP_CASE(V)                                                                       \
   case V:                                                                                \
-    launch_permute_g<V>(ctx, n, ptr_old, ind_old, val_old, new2old, col_map, ptr_new,    \
-                        ind_new, val_new, key_tmp, val_tmp, lists, counts, list_stride,  \
-                        big_ctl, big_rows, big_owner);                                   \
+    launch_permute_g<V>(ctx, n, src_new, ind_old, val_old, col_map, delta, ptr_new,      \
+                        ind_new, val_new, key_tmp, val_tmp, lists, list_stride, ctl,     \
+                        big_rows, big_owner);                                            \
     break;
     SP_CASE(4) SP_CASE(8) SP_CASE(16) SP_CASE(32) SP_CASE(64)
 #undef SP_CASE
   default:
     SP_EXPECT(false, "internal: bad group width");
   }
-  // Big rows' units (none registered: every workgroup exits at once).
-  const int gb = ctx.grid_for(max_copy_units(nnz), 256, 4);
-  copy_big_rows<<<gb, 256, 0, ctx.stream>>>(ind_old, val_old, col_map, big_ctl, big_rows,
-                                            big_owner, col_map ? key_tmp : ind_new,
-                                            col_map ? val_tmp : val_new);
+}
+
+// Copies the units of the big rows permute_rows registered (the host knows
+// their count from the control words).
+void launch_copy_big(Context &ctx, int32_t units, const int32_t *ind_old, const float *val_old,
+                     const int32_t *col_map, const BigRow *big_rows, const int32_t *big_owner,
+                     int32_t *ind_out, float *val_out) {
+  if (units <= 0) return;
+  const int gb = ctx.grid_for(units, 256, 4);
+  copy_big_rows<<<gb, 256, 0, ctx.stream>>>(ind_old, val_old, col_map, units, big_rows,
+                                            big_owner, ind_out, val_out);
   SP_LAUNCH_CHECK();
 }
 
@@ -532,75 +639,98 @@ extern "C" void sporder_reorder(sporder_context_t h, int32_t n, int32_t nnz,
   const bool with_vals = d_val_old != nullptr && d_val_new != nullptr;
 
   size_t need = ws_bytes<int32_t>(scan_tmp_elems(static_cast<int64_t>(n) + 1)) +
-                ws_bytes<BigCtl>(1) + ws_bytes<BigRow>(static_cast<size_t>(max_big_rows(nnz))) +
-                ws_bytes<int32_t>(static_cast<size_t>(max_copy_units(nnz)));
+                ws_bytes<Ctl>(1) + ws_bytes<BigRow>(static_cast<size_t>(max_big_rows(nnz))) +
+                ws_bytes<int32_t>(static_cast<size_t>(max_copy_units(nnz))) + ws_bytes<int32_t>(n);
   if (symmetric) {
-    need += ws_bytes<int32_t>(n) + ws_bytes<int32_t>(nnz) + ws_bytes<float>(nnz) +
-            ws_bytes<int32_t>(3 * (static_cast<size_t>(n) + 2)) + ws_bytes<int32_t>(3);
+    need += ws_bytes<int32_t>(n) + ws_bytes<int16_t>(n) + ws_bytes<int32_t>(nnz) +
+            ws_bytes<float>(nnz) + ws_bytes<int32_t>(3 * (static_cast<size_t>(n) + 2));
   }
   ctx.reserve(need);
   int32_t *scan_tmp = ctx.take<int32_t>(scan_tmp_elems(static_cast<int64_t>(n) + 1));
-  BigCtl *big_ctl = ctx.take<BigCtl>(1);
+  Ctl *ctl = ctx.take<Ctl>(1);
   BigRow *big_rows = ctx.take<BigRow>(static_cast<size_t>(max_big_rows(nnz)));
   int32_t *big_owner = ctx.take<int32_t>(static_cast<size_t>(max_copy_units(nnz)));
+  int32_t *src_new = ctx.take<int32_t>(n);
+  int32_t *old2new = symmetric ? ctx.take<int32_t>(n) : nullptr;
 
   const int row_grid = ctx.grid_for(ceil_div64(n, 256), 256, 4);
-  const int wave_grid = ctx.grid_for(ceil_div64(n, 4), 256, 4);
 
-  gather_row_lengths<<<row_grid, 256, 0, ctx.stream>>>(n, d_ptr_old, d_new_order,
-                                                       d_ptr_new);
+  const int64_t scan_tiles = ceil_div64(static_cast<int64_t>(n) + 1, kScanTileElems);
+  prepare_rows<<<dim3(static_cast<unsigned>(scan_tiles)), kPrepBlock, 0, ctx.stream>>>(
+      n, d_ptr_old, d_new_order, d_ptr_new, src_new, old2new, scan_tmp, ctl);
   SP_LAUNCH_CHECK();
-  scan_i32(ctx, d_ptr_new, d_ptr_new, static_cast<int64_t>(n) + 1, true, scan_tmp);
+  scan_i32_from_totals(ctx, d_ptr_new, d_ptr_new, static_cast<int64_t>(n) + 1, true, scan_tmp);
 
   // Lanes per row: the average row length rounded up to a power of two,
   // between 4 and 64.
   int G = 4;
   while (G < 64 && static_cast<int64_t>(G) * n < nnz) G <<= 1;
 
-  if (!symmetric) {
-    launch_permute(ctx, G, n, d_ptr_old, d_ind_old, d_val_old, d_new_order, nullptr,
-                   d_ptr_new, d_ind_new, d_val_new, nullptr, nullptr, nullptr, nullptr, 0, nnz,
-                   big_ctl, big_rows, big_owner);
+  // The control words come back once, after the copy kernel; the stages after
+  // it are launched only when they have rows.
+  Ctl hc{};
+  auto read_ctl = [&] {
+    SP_HIP(hipMemcpyAsync(ctx.host_words, ctl, sizeof(Ctl), hipMemcpyDeviceToHost, ctx.stream));
     ctx.sync();
+    std::memcpy(&hc, ctx.host_words, sizeof(Ctl));
+  };
+
+  if (!symmetric) {
+    launch_permute(ctx, G, n, src_new, d_ind_old, d_val_old, nullptr, nullptr, d_ptr_new,
+                   d_ind_new, d_val_new, nullptr, nullptr, nullptr, 0, ctl, big_rows, big_owner);
+    read_ctl();
+    if (hc.big.units > 0) {
+      launch_copy_big(ctx, hc.big.units, d_ind_old, d_val_old, nullptr, big_rows, big_owner,
+                      d_ind_new, d_val_new);
+      ctx.sync();
+    }
     return;
   }
 
-  int32_t *old2new = ctx.take<int32_t>(n);
+  int16_t *delta = ctx.take<int16_t>(n);
   int32_t *unsorted = ctx.take<int32_t>(nnz);
   float *val_unsorted = ctx.take<float>(nnz);
   // Row lists of the three sort stages, one array with stride n + 2.
   const int32_t stride = n + 2;
   int32_t *lists = ctx.take<int32_t>(3 * static_cast<size_t>(stride));
   int32_t *list1 = lists, *long_rows = lists + stride, *huge_rows = lists + 2 * stride;
-  int32_t *counts = ctx.take<int32_t>(3);
+  const float *vo = with_vals ? d_val_old : nullptr;
+  float *vn = with_vals ? d_val_new : nullptr;
+  float *vt = with_vals ? val_unsorted : nullptr;
 
-  invert_perm<<<row_grid, 256, 0, ctx.stream>>>(n, d_new_order, old2new);
+  narrow_map<<<std::min(row_grid, 4 * ctx.num_cus), 256, 0, ctx.stream>>>(n, old2new, delta,
+                                                                          ctl);
   SP_LAUNCH_CHECK();
-  fill_u32(ctx, counts, 3, 0u);
   // Rows of at most G entries are remapped, sorted and written in one pass;
-  // longer rows are written unsorted to the temporaries and listed by length
-  // for the stage that sorts them.
-  launch_permute(ctx, G, n, d_ptr_old, d_ind_old, d_val_old, d_new_order, old2new,
-                 d_ptr_new, d_ind_new, with_vals ? d_val_new : nullptr, unsorted,
-                 with_vals ? val_unsorted : nullptr, lists, counts, stride, nnz, big_ctl,
-                 big_rows, big_owner);
-  sort_rows_wave<<<wave_grid, 256, 0, ctx.stream>>>(
-      list1, counts, d_ptr_new, unsorted, with_vals ? val_unsorted : nullptr, d_ind_new,
-      with_vals ? d_val_new : nullptr);
-  SP_LAUNCH_CHECK();
-  sort_rows_block<<<ctx.num_cus * 4, kBlockSortThreads, 0, ctx.stream>>>(
-      d_ptr_new, long_rows, counts + 1, unsorted, with_vals ? val_unsorted : nullptr,
-      d_ind_new, with_vals ? d_val_new : nullptr);
-  SP_LAUNCH_CHECK();
-
-  int32_t hcount = 0;
-  SP_HIP(hipMemcpyAsync(&hcount, counts + 2, sizeof(int32_t), hipMemcpyDeviceToHost,
-                        ctx.stream));
-  ctx.sync();
-  if (hcount > 0) {
-    sort_huge_rows(ctx, n, d_ptr_new, huge_rows, hcount, unsorted,
-                   with_vals ? val_unsorted : nullptr, d_ind_new,
-                   with_vals ? d_val_new : nullptr, list1, scan_tmp);
+  // longer rows are listed by length for the stage that sorts them.
+  launch_permute(ctx, G, n, src_new, d_ind_old, vo, old2new, delta, d_ptr_new, d_ind_new, vn,
+                 unsorted, vt, lists, stride, ctl, big_rows, big_owner);
+  read_ctl();
+  const bool narrow = hc.wide == 0;
+  bool queued = false;
+  if (hc.counts[0] > 0) {
+    const int g = std::min<int>(ctx.grid_for(ceil_div64(hc.counts[0], 4), 256, 4),
+                                4 * ctx.num_cus);
+    sort_rows_wave<<<g, 256, 0, ctx.stream>>>(list1, hc.counts[0], d_ptr_new, unsorted, vt,
+                                              d_ind_new, vn);
+    SP_LAUNCH_CHECK();
+    queued = true;
   }
-  ctx.sync();
+  if (hc.counts[1] > 0) {
+    sort_rows_block<<<std::min(hc.counts[1], ctx.num_cus * 4), kBlockSortThreads, 0,
+                      ctx.stream>>>(d_ptr_new, long_rows, hc.counts[1], src_new, d_ind_old, vo,
+                                    old2new, delta, narrow, d_ind_new, vn);
+    SP_LAUNCH_CHECK();
+    queued = true;
+  }
+  if (hc.counts[2] > 0) {
+    // Rows past kBlockSortCap: copied unsorted (their units registered by
+    // permute_rows), then one device-wide sort.
+    launch_copy_big(ctx, hc.big.units, d_ind_old, vo, old2new, big_rows, big_owner, unsorted,
+                    vt);
+    sort_huge_rows(ctx, n, d_ptr_new, huge_rows, hc.counts[2], unsorted, vt, d_ind_new, vn,
+                   list1, scan_tmp);
+    queued = true;
+  }
+  if (queued) ctx.sync();
 }

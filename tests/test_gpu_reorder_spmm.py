@@ -90,14 +90,31 @@ def mats():
 MATS = mats()
 
 
+def permutation(n, kind, seed=5):
+    """A uniform permutation, or one that shuffles rows only inside aligned
+    windows of 1024 (as csg's chains do inside their chunks), which moves
+    every index by less than 2^15 and so takes the 16-bit column remap."""
+    rng = np.random.default_rng(seed)
+    if kind == "uniform":
+        return rng.permutation(n).astype(np.int32)
+    perm = np.arange(n)
+    for w in range(0, n, 1024):
+        rng.shuffle(perm[w:w + 1024])
+    return perm.astype(np.int32)
+
+
 @pytest.mark.parametrize("name", sorted(MATS))
 @pytest.mark.parametrize("symmetric", [False, True])
 @pytest.mark.parametrize("with_val", [False, True])
-def test_reorder_bit_exact(sporder, name, symmetric, with_val):
+@pytest.mark.parametrize("kind", ["uniform", "windowed"])
+def test_reorder_bit_exact(sporder, name, symmetric, with_val, kind):
+    """Every size class of row (register, wave, workgroup and device-wide
+    sorts; big-row copies), both column remaps (32-bit when some index moves
+    by 2^15 or more, 16-bit deltas otherwise), with and without values."""
     ptr, ind, val = MATS[name]
     n = ptr.shape[0] - 1
-    perm = np.random.default_rng(5).permutation(n).astype(np.int32)
-    print(f"[reorder] {name} sym={symmetric} val={with_val}", flush=True)
+    perm = permutation(n, kind)
+    print(f"[reorder] {name} sym={symmetric} val={with_val} perm={kind}", flush=True)
     if with_val:
         gp, gi, gv = sporder.reorder(t(ptr), t(ind), t(perm), val=t(val), symmetric=symmetric)
         op, oi, ov = oracle.reorder(ptr, ind, perm, val=val, symmetric=symmetric)
@@ -168,3 +185,25 @@ def test_bench_hook(sporder):
     assert ms > 0.0
     with pytest.raises(ValueError):
         sporder.bench_cusparse_spmm(t(ptr), t(ind), 0)
+
+
+def test_reorder_row_offsets_past_direct_scan(sporder):
+    """More than 4096 scan tiles of 4096 offsets (n = 2^24 + 5000 rows of 0..2
+    entries): the offset scan takes its three-pass form, where each tile's
+    offset comes from one workgroup's scan of the tile totals.  Offsets equal
+    NumPy's cumulative sum, entries the gathered rows."""
+    n = (1 << 24) + 5000
+    rng = np.random.default_rng(12)
+    lens = rng.integers(0, 3, size=n).astype(np.int64)
+    ptr = np.zeros(n + 1, np.int64)
+    np.cumsum(lens, out=ptr[1:])
+    ind = rng.integers(0, n, size=int(ptr[-1])).astype(np.int32)
+    perm = rng.permutation(n).astype(np.int32)
+    gp, gi = sporder.reorder(t(ptr.astype(np.int32)), t(ind), t(perm))
+    want_ptr = np.zeros(n + 1, np.int64)
+    np.cumsum(lens[perm], out=want_ptr[1:])
+    assert np.array_equal(gp.cpu().numpy(), want_ptr.astype(np.int32))
+    starts = ptr[perm]
+    rows = np.repeat(np.arange(n), lens[perm])
+    want_ind = ind[starts[rows] + (np.arange(rows.size) - want_ptr[rows])]
+    assert np.array_equal(gi.cpu().numpy(), want_ind)
