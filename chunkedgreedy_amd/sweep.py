@@ -10,8 +10,13 @@ configuration's widths (warmup 5, median of 20 launch times, B = randn seed
 Algorithmic bytes of an SpMM launch: 4(n+1) + 8 nnz + 8 n N (A once, B once,
 C once).
 
+With ``--candidates`` (host only, no GPU): per configuration, how many rows'
+chunk-restricted candidate streams hold at most M distinct items (the
+space-saving sketch never evicts there) and how much of the stream work those
+rows hold, plus the longest streams' distinct counts (``candidate_stats``).
+
 Usage:  python -m chunkedgreedy_amd.sweep [--cfg C1,C2,C3,C4,C5] [--no-spmm]
-        [--algos row_split,merge_path] [--cg]
+        [--algos row_split,merge_path] [--cg] [--candidates]
 """
 
 from __future__ import annotations
@@ -109,6 +114,43 @@ def measure(name: str, *, spmm=True, algos=("row_split",), repeats=3, cg=False) 
     return rec
 
 
+def candidate_stats(ptr, ind, chunk: int, M: int) -> dict:
+    """Stream length and distinct candidates of every row's chunk-restricted
+    stream (reference sporder/src/common/chunk_similarity_top_k.cu:53-83:
+    for each column of row r, the other rows of r's chunk in that column).
+
+    Distinct candidates of row r = nonzeros of row r of A_q A_q^T without the
+    diagonal, A_q the rows of r's chunk; stream length = the sum over r's
+    columns of (rows of the chunk in that column) - 1."""
+    import scipy.sparse as sp
+
+    ptr = np.asarray(ptr, np.int64)
+    ind = np.asarray(ind, np.int64)
+    n, nnz = ptr.shape[0] - 1, ind.shape[0]
+    A = sp.csr_matrix((np.ones(nnz, np.int32), ind, ptr), shape=(n, n))
+    rows = np.repeat(np.arange(n), np.diff(ptr))
+    key = ind * ((n + chunk - 1) // chunk) + rows // chunk
+    _, inv, cnt = np.unique(key, return_inverse=True, return_counts=True)
+    length = np.bincount(rows, weights=cnt[inv] - 1, minlength=n).astype(np.int64)
+    distinct = np.zeros(n, np.int64)
+    for q0 in range(0, n, chunk):
+        sub = A[q0:min(q0 + chunk, n)]
+        prod = (sub @ sub.T).tocsr()
+        prod.setdiag(0)
+        prod.eliminate_zeros()
+        distinct[q0:q0 + sub.shape[0]] = np.diff(prod.indptr)
+    busy = length > 0
+    fits = busy & (distinct <= M)
+    top = np.argsort(length, kind="stable")[::-1][:5]
+    return {
+        "M": M, "rows_with_items": int(busy.sum()), "rows_within_M": int(fits.sum()),
+        "items": int(length.sum()), "items_within_M": int(length[fits].sum()),
+        "rows_at_M": int((distinct == M).sum()), "rows_at_M_plus_1": int((distinct == M + 1).sum()),
+        "longest": [{"row": int(r), "items": int(length[r]), "distinct": int(distinct[r])}
+                    for r in top],
+    }
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--cfg", default="C1,C2,C3,C4,C5")
@@ -116,7 +158,22 @@ def main(argv=None) -> int:
     ap.add_argument("--algos", default="row_split,merge_path")
     ap.add_argument("--repeats", type=int, default=3)
     ap.add_argument("--cg", action="store_true", help="also time sporder-cg once")
+    ap.add_argument("--candidates", action="store_true",
+                    help="host only: rows whose candidate streams fit the sketch")
     args = ap.parse_args(argv)
+
+    if args.candidates:
+        from chunkedgreedy_amd import synth
+
+        for name in args.cfg.split(","):
+            ptr, ind = getattr(synth, f"config{name[1:]}")()[:2]
+            n, nnz = ptr.shape[0] - 1, ind.shape[0]
+            k = min(256, max(16, nnz // n))  # csg defaults: k, oversampling 4, chunk 1024
+            M = ((4 * k + 31) // 32) * 32
+            rec = {"config": name, "n": n, "nnz": nnz, "k": k,
+                   **candidate_stats(ptr, ind, 1024, M)}
+            print(json.dumps(rec), flush=True)
+        return 0
 
     import torch
 

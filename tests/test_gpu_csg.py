@@ -490,3 +490,52 @@ def test_is_symmetric_one_chunk_similarity_graph(sporder):
             oracle.chunk_similarity_top_k(p, i, 16, n, 2.0, is_symmetric=True))
         assert np.array_equal(gi.cpu().numpy(), oi)
         assert np.array_equal(weight_bits(gw.cpu().numpy()), weight_bits(ow))
+
+
+def distinct_candidates_matrix(n, D):
+    """Row 0 holds columns n-1, n-2, n-3; row j in 1..D holds n-1, plus n-2
+    when j is odd and n-3 when j is a multiple of 3.  Row 0's stream is then
+    the D rows in ascending order, the odd rows, the multiples of 3: exactly D
+    distinct candidates with one, two or three occurrences and three Dice
+    weights (rows of one, two or three nonzeros).  The other rows are empty."""
+    rows, cols = [0, 0, 0], [n - 1, n - 2, n - 3]
+    for j in range(1, D + 1):
+        rows.append(j)
+        cols.append(n - 1)
+        if j % 2:
+            rows.append(j)
+            cols.append(n - 2)
+        if j % 3 == 0:
+            rows.append(j)
+            cols.append(n - 3)
+    rows, cols = np.array(rows), np.array(cols)
+    order = np.lexsort((cols, rows))
+    rows, cols = rows[order], cols[order]
+    ptr = np.zeros(n + 1, np.int64)
+    np.cumsum(np.bincount(rows, minlength=n), out=ptr[1:])
+    return ptr.astype(np.int32), cols.astype(np.int32)
+
+
+@pytest.mark.parametrize("k,ovs", [(16, 4.0), (24, 4.0), (32, 4.0)])
+@pytest.mark.parametrize("extra", [-1, 0, 1, 2])
+@pytest.mark.parametrize("chunk", [1024, 5000])
+def test_sketch_capacity_boundary(sporder, k, ovs, extra, chunk):
+    """Rows with M - 1, M, M + 1 and M + 2 distinct candidates (M = the
+    sketch capacity: 64, 96, 128): no eviction up to M, then the first
+    evictions, whose victim is the smallest weight with ties to the lowest
+    (cell, lane), and whose newcomer inherits its weight.  Chunks of 1024
+    rows take the chunk-local tier, chunks of 5000 the global path.  Tables
+    bit-exact against the oracle; row 0's distinct count checked on the
+    host."""
+    M = ((int(k * ovs) + 31) // 32) * 32
+    D = M + extra
+    n = 5000
+    ptr, ind = distinct_candidates_matrix(n, D)
+    # Row 0's stream on the host: the rows of each of its columns, minus itself.
+    stream = [r for c in ind[ptr[0]:ptr[1]]
+              for r in range(n) if r != 0 and c in ind[ptr[r]:ptr[r + 1]]]
+    assert len(set(stream)) == D and len(stream) == D + (D + 1) // 2 + D // 3
+    oi, ow = check_table(sporder, ptr, ind, k, ovs, chunk, False)
+    # Row 0 keeps its k heaviest candidates; the rows seen three times lead.
+    assert (oi[0] >= 0).sum() == k
+    assert set(oi[0, :3].tolist()) <= {j for j in range(1, D + 1) if j % 6 == 3}

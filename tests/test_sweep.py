@@ -19,3 +19,41 @@ def test_main_needs_a_gpu(monkeypatch):
 
     monkeypatch.setattr(torch.cuda, "is_available", lambda: False)
     assert sweep.main(["--cfg", "C1"]) == 1
+
+
+def test_candidate_stats_against_brute_force():
+    """Stream lengths and distinct candidates of every row, against a direct
+    enumeration of each row's chunk-restricted stream."""
+    import numpy as np
+
+    from chunkedgreedy_amd import synth
+
+    ptr, ind = synth.config1(3)[:2]
+    ptr, ind = ptr[:601].copy(), ind[:ptr[600]].copy()  # the first 600 rows
+    ind = ind % 600
+    order = np.lexsort((ind, np.repeat(np.arange(600), np.diff(ptr))))
+    ind = ind[order]
+    keep = np.ones(ind.size, bool)
+    rows = np.repeat(np.arange(600), np.diff(ptr))
+    keep[1:] = (ind[1:] != ind[:-1]) | (rows[1:] != rows[:-1])
+    lens = np.bincount(rows[keep], minlength=600)
+    ind = ind[keep]
+    ptr = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    chunk, M = 64, 8
+    st = sweep.candidate_stats(ptr, ind, chunk, M)
+    cols = [set(ind[ptr[r]:ptr[r + 1]].tolist()) for r in range(600)]
+    length, distinct = [], []
+    for r in range(600):
+        cs = (r // chunk) * chunk
+        items = [s for c in ind[ptr[r]:ptr[r + 1]] for s in range(cs, min(cs + chunk, 600))
+                 if s != r and c in cols[s]]
+        length.append(len(items))
+        distinct.append(len(set(items)))
+    length, distinct = np.array(length), np.array(distinct)
+    busy = length > 0
+    assert st["rows_with_items"] == busy.sum()
+    assert st["rows_within_M"] == (busy & (distinct <= M)).sum()
+    assert st["items"] == length.sum()
+    assert st["items_within_M"] == length[busy & (distinct <= M)].sum()
+    assert st["rows_at_M"] == (distinct == M).sum()
+    assert st["longest"][0]["items"] == length.max()
