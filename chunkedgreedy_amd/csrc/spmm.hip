@@ -29,6 +29,7 @@
 // atomics after the short rows are written directly.  The result equals the
 // row-split one up to the rounding of the split rows.
 #include "common.hpp"
+#include "philox.hpp"
 
 #include <mutex>
 
@@ -617,22 +618,6 @@ __global__ void spmm_merge_prepare(int32_t n, const int32_t *__restrict__ ptr,
       for (int32_t j = lane; j < N; j += kWave) C[row * N + j] = 0.0f;
     }
   }
-}
-
-// ---- Philox4x32-10 (Salmon, Moraes, Dror, Shaw, SC'11) -------------------------
-
-__device__ __forceinline__ uint4 philox4x32_10(uint4 ctr, uint2 key) {
-  const uint32_t M0 = 0xD2511F53u, M1 = 0xCD9E8D57u;
-  const uint32_t W0 = 0x9E3779B9u, W1 = 0xBB67AE85u;
-#pragma unroll
-  for (int r = 0; r < 10; ++r) {
-    uint32_t hi0 = __umulhi(M0, ctr.x), lo0 = M0 * ctr.x;
-    uint32_t hi1 = __umulhi(M1, ctr.z), lo1 = M1 * ctr.z;
-    ctr = make_uint4(hi1 ^ ctr.y ^ key.x, lo1, hi0 ^ ctr.w ^ key.y, lo0);
-    key.x += W0;
-    key.y += W1;
-  }
-  return ctr;
 }
 
 // vals[i] = U(0,1] from counter (i/4, stream) under key = seed.

@@ -51,7 +51,7 @@ def _normalize(value):
         return int(value) if value == int(value) else float(value)
     if isinstance(value, str):
         return value
-    raise TypeError(f"Unsupported param value type: {type(value)!r}")
+    raise TypeError(f"cannot hash a parameter of type {type(value).__name__}")
 
 
 def canonicalize_params(params: dict) -> str:
@@ -86,10 +86,10 @@ def validate_row_perm(row_perm, nrows: int) -> np.ndarray:
         raise ValueError(f"row_perm length {perm.shape[0]} != matrix rows {nrows}")
     seen = np.zeros(nrows, dtype=bool)
     if perm.size and (perm.min() < 0 or perm.max() >= nrows):
-        raise ValueError("row_perm is not a valid permutation of [0, nrows)")
+        raise ValueError("row_perm must hold each row index 0..nrows-1 exactly once")
     seen[perm] = True
     if not seen.all():
-        raise ValueError("row_perm is not a valid permutation of [0, nrows)")
+        raise ValueError("row_perm must hold each row index 0..nrows-1 exactly once")
     return perm
 
 

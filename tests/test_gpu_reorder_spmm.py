@@ -7,6 +7,8 @@ variants within 1e-5 relative of an fp64 reference (the tolerance north_star
 states for fp32 SpMM).
 """
 
+import time
+
 import numpy as np
 import pytest
 import torch
@@ -180,11 +182,34 @@ def test_spmm_merge_path_tolerance(sporder, name, N):
 
 
 def test_bench_hook(sporder):
+    """The hook's mean time per repeat: positive, the inputs untouched, growing
+    with the width (N = 256 against N = 16 on a 2^18-row matrix), and within a
+    factor of four of the same SpMM timed from outside."""
     ptr, ind, _ = MATS["C1"]
-    ms = sporder.bench_cusparse_spmm(t(ptr), t(ind), 32, warmup=1, repeat=3, seed=7)
+    dptr, dind = t(ptr), t(ind)
+    ms = sporder.bench_cusparse_spmm(dptr, dind, 32, warmup=1, repeat=3, seed=7)
     assert ms > 0.0
+    assert np.array_equal(dptr.cpu().numpy(), ptr) and np.array_equal(dind.cpu().numpy(), ind)
     with pytest.raises(ValueError):
-        sporder.bench_cusparse_spmm(t(ptr), t(ind), 0)
+        sporder.bench_cusparse_spmm(dptr, dind, 0)
+    p2, i2, v2 = synth.planted(1 << 18, 4096, 16, 31)
+    dp, di = t(p2), t(i2)
+    narrow = sporder.bench_cusparse_spmm(dp, di, 16, warmup=3, repeat=20, seed=1)
+    wide = sporder.bench_cusparse_spmm(dp, di, 256, warmup=3, repeat=20, seed=1)
+    assert wide > narrow > 0.0
+    B = torch.rand((p2.shape[0] - 1, 256), device=DEV)
+    out = torch.empty_like(B)
+    dv = t(v2)
+    for _ in range(3):
+        sporder.spmm_csr(dp, di, dv, B, out=out)
+    # Each call ends in a synchronize of the library stream: host wall time.
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(20):
+        sporder.spmm_csr(dp, di, dv, B, out=out)
+    torch.cuda.synchronize()
+    outside = (time.perf_counter() - t0) * 1e3 / 20
+    assert 0.25 < wide / outside < 4.0, (wide, outside)
 
 
 def test_reorder_row_offsets_past_direct_scan(sporder):
