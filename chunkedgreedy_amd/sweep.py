@@ -15,6 +15,9 @@ chunk-restricted candidate streams hold at most M distinct items (the
 space-saving sketch never evicts there) and how much of the stream work those
 rows hold, plus the longest streams' distinct counts (``candidate_stats``).
 
+Configurations: C1..C5 (synth.CONFIGS) and the inputs with in-chunk locality
+C2r, C4n, RGG20 (synth.LOCALITY).
+
 Usage:  python -m chunkedgreedy_amd.sweep [--cfg C1,C2,C3,C4,C5] [--no-spmm]
         [--algos row_split,merge_path] [--cg] [--candidates]
 """
@@ -30,7 +33,15 @@ import time
 import numpy as np
 
 WIDTHS = {"C1": [32], "C2": [32, 128], "C3": [32, 64, 256], "C4": [16, 32, 64, 128, 256],
-          "C5": [128]}
+          "C5": [128],
+          # inputs with in-chunk locality (synth.LOCALITY)
+          "C2r": [128], "C4n": [32], "RGG20": [32, 128]}
+
+
+def generators() -> dict:
+    from chunkedgreedy_amd import synth
+
+    return {**synth.CONFIGS, **synth.LOCALITY}
 
 
 def spmm_bytes(n: int, nnz: int, N: int) -> int:
@@ -52,8 +63,7 @@ def measure(name: str, *, spmm=True, algos=("row_split",), repeats=3, cg=False) 
 
     from chunkedgreedy_amd import sporder, synth
 
-    gens = {"C1": synth.config1, "C2": synth.config2, "C3": synth.config3,
-            "C4": synth.config4, "C5": synth.config5}
+    gens = generators()
     dev = torch.device("cuda:0")
     ctx = sporder.Context()
     t0 = time.time()
@@ -163,10 +173,9 @@ def main(argv=None) -> int:
     args = ap.parse_args(argv)
 
     if args.candidates:
-        from chunkedgreedy_amd import synth
-
+        gens = generators()
         for name in args.cfg.split(","):
-            ptr, ind = getattr(synth, f"config{name[1:]}")()[:2]
+            ptr, ind = gens[name]()[:2]
             n, nnz = ptr.shape[0] - 1, ind.shape[0]
             k = min(256, max(16, nnz // n))  # csg defaults: k, oversampling 4, chunk 1024
             M = ((4 * k + 31) // 32) * 32

@@ -28,7 +28,8 @@ def _rng(seed: int) -> np.random.Generator:
 
 
 def _coo_to_csr(n: int, rows: np.ndarray, cols: np.ndarray, vals: np.ndarray) -> Csr:
-    order = np.lexsort((cols, rows))
+    # Stable sort by (row, column) on one int64 key: the order np.lexsort gives.
+    order = np.argsort(rows.astype(np.int64) * n + cols, kind="stable")
     rows, cols, vals = rows[order], cols[order], vals[order]
     counts = np.bincount(rows, minlength=n)
     ptr = np.zeros(n + 1, np.int64)
@@ -39,7 +40,7 @@ def _coo_to_csr(n: int, rows: np.ndarray, cols: np.ndarray, vals: np.ndarray) ->
 def _sort_rows(ptr: np.ndarray, ind: np.ndarray, val: np.ndarray) -> Csr:
     n = ptr.shape[0] - 1
     rows = np.repeat(np.arange(n, dtype=np.int64), np.diff(ptr.astype(np.int64)))
-    order = np.lexsort((ind, rows))
+    order = np.argsort(rows * n + ind, kind="stable")
     return ptr.astype(np.int32), ind[order].astype(np.int32), val[order].astype(np.float32)
 
 
@@ -189,29 +190,63 @@ def config4(seed: int = 4, g: int = 160) -> Csr:
     return stencil7(g, seed)
 
 
+def _alias_table(w: np.ndarray):
+    """Walker's alias table (Vose's construction) for sampling index i with
+    probability w[i] / sum(w) in O(1): draw i uniformly, keep it with
+    probability prob[i], else take alias[i]."""
+    n = w.shape[0]
+    p = (w * (n / w.sum())).tolist()
+    prob = [1.0] * n
+    alias = list(range(n))
+    small = [i for i in range(n) if p[i] < 1.0]
+    large = [i for i in range(n) if p[i] >= 1.0]
+    while small and large:
+        s = small.pop()
+        g = large.pop()
+        prob[s] = p[s]
+        alias[s] = g
+        p[g] = p[g] + p[s] - 1.0
+        (small if p[g] < 1.0 else large).append(g)
+    return np.array(prob), np.array(alias, np.int64)
+
+
 def chung_lu(n: int, exponent: float, avg_degree: float, seed: int) -> Csr:
     """Chung-Lu graph with expected degrees w_i proportional to
-    (i + 1)^(-1/(exponent-1)), scaled to `avg_degree`: n*avg_degree/2 edges with
-    both endpoints drawn proportional to w; symmetrized, deduplicated, self
-    loops replaced by the identity; values D^-1/2 (A + I) D^-1/2."""
+    (i + 1)^(-1/(exponent-1)): edges with both endpoints drawn proportional to
+    w, symmetrized and deduplicated, drawn in rounds until the mean number of
+    distinct neighbours (self loops excluded) reaches `avg_degree` (the hubs
+    draw many duplicates, so n*avg_degree/2 draws alone fall short); then the
+    identity added and values D^-1/2 (A + I) D^-1/2."""
     rng = _rng(seed)
     w = (np.arange(n, dtype=np.float64) + 1.0) ** (-1.0 / (exponent - 1.0))
-    cdf = np.cumsum(w)
-    cdf /= cdf[-1]
+    prob, alias = _alias_table(w)
+    target = int(round(n * avg_degree))  # directed off-diagonal entries
+    k = np.zeros(0, np.int64)
     m = int(n * avg_degree / 2)
-    keys = []
     step = 1 << 22
-    for e0 in range(0, m, step):
-        cnt = min(step, m - e0)
-        u = np.searchsorted(cdf, rng.random(cnt), side="right")
-        v = np.searchsorted(cdf, rng.random(cnt), side="right")
-        u = np.minimum(u, n - 1)
-        v = np.minimum(v, n - 1)
-        keep = u != v
-        u, v = u[keep], v[keep]
-        keys += [u * n + v, v * n + u]
-    keys.append(np.arange(n, dtype=np.int64) * (n + 1))  # self loops
-    k = np.unique(np.concatenate(keys))
+
+    def draw(cnt):
+        i = rng.integers(0, n, cnt)
+        return np.where(rng.random(cnt) < prob[i], i, alias[i])
+
+    while True:
+        keys = [k]
+        for e0 in range(0, m, step):
+            cnt = min(step, m - e0)
+            u = draw(cnt)
+            v = draw(cnt)
+            keep = u != v
+            u, v = u[keep], v[keep]
+            keys += [u * n + v, v * n + u]
+        before = k.shape[0]
+        k = np.unique(np.concatenate(keys))
+        if k.shape[0] >= target:
+            break
+        # Draw the shortfall again, scaled by this round's yield of new
+        # entries per draw (it falls as the hubs fill up).
+        per_draw = max((k.shape[0] - before) / m, 1e-3)
+        m = max(1024, int((target - k.shape[0]) / per_draw * 1.05))
+    k = np.union1d(k, np.arange(n, dtype=np.int64) * (n + 1))  # self loops
     # Scramble vertex ids so that degree does not follow the index.
     p = rng.permutation(n)
     rows, cols = p[k // n], p[k % n]
@@ -223,6 +258,41 @@ def chung_lu(n: int, exponent: float, avg_degree: float, seed: int) -> Csr:
 
 def config5(seed: int = 5, n: int = 2_449_029) -> Csr:
     return chung_lu(n, 2.1, 25.0, seed)
+
+
+def rgg(n: int, avg_degree: float, seed: int) -> Csr:
+    """Random geometric graph: n points uniform in the unit square, an edge
+    between two points closer than r = sqrt(avg_degree / (pi n)) (no self
+    loops), values 1.  Points are numbered cell by cell over a grid of cells
+    of side >= r (row-major cells, points in a cell in draw order), so
+    neighbours are near in index: a stand-in with the locality of the
+    rgg_n_2_20 graphs the reference's reorder benchmark reports."""
+    rng = _rng(seed)
+    r = float(np.sqrt(avg_degree / (np.pi * n)))
+    g = max(1, int(1.0 / r))
+    pts = rng.random((n, 2))
+    cell = np.minimum((pts * g).astype(np.int64), g - 1)
+    cid = cell[:, 1] * g + cell[:, 0]
+    order = np.argsort(cid, kind="stable")
+    pts, cell, cid = pts[order], cell[order], cid[order]
+    cstart = np.searchsorted(cid, np.arange(g * g + 1))
+    rows, cols = [], []
+    for dy in (-1, 0, 1):
+        for dx in (-1, 0, 1):
+            ox, oy = cell[:, 0] + dx, cell[:, 1] + dy
+            ok = (ox >= 0) & (ox < g) & (oy >= 0) & (oy < g)
+            src = np.nonzero(ok)[0]
+            nb = oy[src] * g + ox[src]
+            lo, hi = cstart[nb], cstart[nb + 1]
+            cnt = hi - lo
+            a = np.repeat(src, cnt)
+            b = np.repeat(lo - np.cumsum(np.concatenate([[0], cnt[:-1]])), cnt) + np.arange(cnt.sum())
+            d = pts[a] - pts[b]
+            keep = (a != b) & ((d * d).sum(axis=1) < r * r)
+            rows.append(a[keep])
+            cols.append(b[keep])
+    rows, cols = np.concatenate(rows), np.concatenate(cols)
+    return _coo_to_csr(n, rows, cols, np.ones(rows.shape[0], np.float32))
 
 
 def band(n: int, half_width: int = 2) -> Csr:
@@ -254,4 +324,15 @@ CONFIGS = {
     "C3": config3,
     "C4": config4,
     "C5": config5,
+}
+
+# Inputs whose rows carry locality inside each chunk (the reorder benchmark's
+# SuiteSparse and DIMACS matrices do; C2 and C4 as configured are scrambled, so
+# their chunk-restricted candidate streams are nearly empty): C2 with its rows
+# in planted block order, C4 in natural grid order, and a random geometric
+# graph of 2^20 points with mean degree 13.
+LOCALITY = {
+    "C2r": lambda: config2(planted_rows=True),
+    "C4n": lambda: stencil7(160, 4, scramble=False),
+    "RGG20": lambda: rgg(1 << 20, 13.0, 20),
 }

@@ -11,7 +11,9 @@ def test_spmm_bytes_matches_c2_figures():
 
 def test_widths_cover_every_config():
     assert sweep.WIDTHS == {"C1": [32], "C2": [32, 128], "C3": [32, 64, 256],
-                            "C4": [16, 32, 64, 128, 256], "C5": [128]}
+                            "C4": [16, 32, 64, 128, 256], "C5": [128],
+                            "C2r": [128], "C4n": [32], "RGG20": [32, 128]}
+    assert set(sweep.generators()) == set(sweep.WIDTHS)
 
 
 def test_main_needs_a_gpu(monkeypatch):
