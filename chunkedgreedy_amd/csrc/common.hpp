@@ -60,12 +60,12 @@ struct Context {
   size_t lds_per_block = 0;
   Workspace ws;
   Workspace aux; // second grow-only buffer, for temporaries sized mid-call
-  // Three more streams (default priority) for independent kernels of one
-  // call, forked from and joined back into `stream` with the events below, so
-  // a synchronize of `stream` also waits for their work.
-  hipStream_t side[3] = {};
+  // Two more streams (default priority) for independent kernels of one call,
+  // forked from and joined back into `stream` with the events below, so a
+  // synchronize of `stream` also waits for their work.
+  hipStream_t side[2] = {};
   hipEvent_t fork_ev = nullptr;
-  hipEvent_t join_ev[3] = {};
+  hipEvent_t join_ev[2] = {};
   hipEvent_t prep_ev = nullptr; // a stage's preparation done (csg's global path)
   // Pinned host words for small device-to-host readbacks.
   int32_t *host_words = nullptr;
@@ -203,7 +203,9 @@ void csr2csc(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
 // recorded once the run search is done and before the sketch launch.
 // d_row_valid, when given, receives each computed row's number of valid table
 // entries (the non-empty prefix of its table row, written with the row); rows
-// not computed are left as they are.
+// not computed are left as they are.  `mirror`, when given, receives (atomic
+// adds) the mirror_term of every nonzero of the computed rows; the local
+// variant below does the same for its rows.
 size_t chunk_sketch_ws_bytes(int32_t n, int32_t nnz, int32_t chunk_size);
 void chunk_sketch_top_k(Context &ctx, int32_t n, int32_t nnz, int32_t k, int32_t chunk_size,
                         int32_t m_capacity, const int32_t *d_ptr,
@@ -211,7 +213,8 @@ void chunk_sketch_top_k(Context &ctx, int32_t n, int32_t nnz, int32_t k, int32_t
                         const int32_t *d_row_ind, uint64_t *d_table,
                         const int32_t *d_chunks = nullptr,
                         const int32_t *d_chunk_count = nullptr,
-                        hipEvent_t prepared = nullptr, int32_t *d_row_valid = nullptr);
+                        hipEvent_t prepared = nullptr, int32_t *d_row_valid = nullptr,
+                        unsigned long long *mirror = nullptr);
 
 // Chunk-local variant: one workgroup per chunk with the chunk's transpose in
 // LDS.  Applicable when chunk_local_supported(n, chunk_size).
@@ -230,7 +233,8 @@ void chunk_local_sketch_top_k(Context &ctx, int32_t n, int32_t k, int32_t chunk_
                               int32_t m_capacity, const int32_t *d_ptr, const int32_t *d_ind,
                               uint64_t *d_table, const int32_t *d_lists,
                               const int32_t *d_counts, int tiers,
-                              int32_t *d_row_valid = nullptr);
+                              int32_t *d_row_valid = nullptr,
+                              unsigned long long *mirror = nullptr);
 
 // Degree / weight totals of a top-k table (reference
 // sporder/src/common/similarity_top_k.cu:120-172).
@@ -374,6 +378,22 @@ __device__ __forceinline__ int32_t wave_incl_max(int32_t v) {
 
 __device__ __forceinline__ int32_t wave_sum(int32_t v) {
   return __builtin_amdgcn_readlane(wave_incl_scan(v), 63);
+}
+
+// Term of nonzero (r, c) in the is_symmetric mirror check: sign(c - r) times
+// a multiply-xorshift mix of the packed pair (min, max) (one round of the
+// splitmix64 finalizer of Steele, Lea and Flood, OOPSLA 2014), 0 on the
+// diagonal.  Summed mod 2^64 over a pattern that is symmetric as a multiset,
+// the terms cancel exactly; an asymmetric one leaves
+// (count(a, b) - count(b, a)) * H(a, b) terms, which cancel only when its
+// unmatched pairs' mixes happen to sum to zero mod 2^64.
+__device__ __forceinline__ uint64_t mirror_term(int32_t r, int32_t c) {
+  if (r == c) return 0;
+  const uint32_t a = static_cast<uint32_t>(r < c ? r : c), b = static_cast<uint32_t>(r < c ? c : r);
+  uint64_t x = ((static_cast<uint64_t>(a) << 32) | b) ^ 0x9e3779b97f4a7c15ull;
+  x = (x ^ (x >> 31)) * 0xbf58476d1ce4e5b9ull;
+  x ^= x >> 29;
+  return c > r ? x : 0ull - x;
 }
 
 // weighted_index packing (reference sporder/src/common/weighted_index.h:15-27).

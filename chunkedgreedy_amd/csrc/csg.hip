@@ -756,66 +756,14 @@ void validate_sketch_args(int32_t k, float oversampling, int32_t chunk_size) {
 // chunk-local sketch transposes each chunk's rows instead.  For input that
 // meets the reference's precondition of sorted columns within each row
 // (sporder/include/sporder.h:27) the two agree exactly when the pattern is
-// symmetric as a multiset (as many (r, c) as (c, r) for every pair).
-// mirror_check_kernel sums sign(c - r) * H(min(r, c), max(r, c)) mod 2^64 over
-// the nonzeros, with H the splitmix64 finalizer (Steele, Lea and Flood,
-// OOPSLA 2014) of the packed pair.  A symmetric pattern sums to exactly zero;
-// an asymmetric one leaves (count(a, b) - count(b, a)) * H(a, b) terms, which
-// cancel only through a 64-bit hash collision.  A call whose sum is not zero
-// is run again with every chunk on the global path, which reads the CSR as
-// the CSC like the reference.
+// symmetric as a multiset (as many (r, c) as (c, r) for every pair).  The
+// sketch kernels that read the rows (the chunk-local tiers and the global
+// path) add every nonzero's mirror_term (common.hpp) into one word; the sum is
+// zero for a symmetric pattern.  A call whose sum is not zero is run again
+// with every chunk on the global path, which reads the CSR as the CSC like the
+// reference.
 
-__device__ __forceinline__ uint64_t mirror_hash(uint32_t a, uint32_t b) {
-  uint64_t x = ((static_cast<uint64_t>(a) << 32) | b) + 0x9e3779b97f4a7c15ull;
-  x = (x ^ (x >> 30)) * 0xbf58476d1ce4e5b9ull;
-  x = (x ^ (x >> 27)) * 0x94d049bb133111ebull;
-  return x ^ (x >> 31);
-}
-
-// One wave per 64 rows (grid-stride); lane l holds the end of row r0 + l and
-// each nonzero finds its row by a binary search over those ends (bpermute
-// reads, taken with every lane active).  *out gathers the signed hash sum.
-__global__ void __launch_bounds__(256)
-    mirror_check_kernel(int32_t n, const int32_t *__restrict__ ptr,
-                        const int32_t *__restrict__ ind, unsigned long long *out) {
-  const int lane = threadIdx.x & (kWave - 1);
-  const int64_t groups = ceil_div64(n, kWave);
-  const int64_t step = static_cast<int64_t>(gridDim.x) * (blockDim.x / kWave);
-  uint64_t sum = 0;
-  for (int64_t gi = blockIdx.x * static_cast<int64_t>(blockDim.x / kWave) + threadIdx.x / kWave;
-       gi < groups; gi += step) {
-    const int32_t r0 = static_cast<int32_t>(gi * kWave);
-    const int32_t rows = static_cast<int32_t>(min<int64_t>(kWave, n - r0));
-    const int32_t p0 = ptr[r0], p1 = ptr[r0 + rows];
-    // Lanes past the last row repeat its end, so the ends stay non-decreasing.
-    const int32_t e = lane < rows ? ptr[r0 + lane + 1] : p1;
-    for (int32_t base = p0; base < p1; base += kWave) {
-      const int32_t p = base + lane;
-      // Offset of p's row: the number of lanes whose row ends at or before p
-      // (at most rows - 1 for p < p1, since lane rows - 1 ends at p1).
-      int lo = 0;
-#pragma unroll
-      for (int s = kWave / 2; s > 0; s >>= 1) {
-        if (__shfl(e, lo + s - 1) <= p) lo += s;
-      }
-      if (p < p1) {
-        const int32_t r = r0 + lo, c = ind[p];
-        if (c != r) {
-          const uint64_t h = mirror_hash(static_cast<uint32_t>(min(r, c)),
-                                         static_cast<uint32_t>(max(r, c)));
-          sum += c > r ? h : 0ull - h;
-        }
-      }
-    }
-  }
-#pragma unroll
-  for (int o = kWave / 2; o > 0; o >>= 1) {
-    sum += __shfl_xor(static_cast<unsigned long long>(sum), o);
-  }
-  if (lane == 0 && sum != 0) atomicAdd(out, static_cast<unsigned long long>(sum));
-}
-
-// A queued mirror check: its device words and whether it was queued.
+// A mirror check's device word and whether this call summed into it.
 struct MirrorCheck {
   unsigned long long *dev = nullptr;
   bool queued = false;
@@ -823,25 +771,10 @@ struct MirrorCheck {
 
 constexpr int kMirrorHostWord = 8; // host_words[8..9] receive the sum
 
-// Queues the check on side stream 2, forked from the library stream so it
-// runs beside the sketch; mirror_collect joins it back.
-void mirror_check(Context &ctx, int32_t n, const int32_t *d_ptr, const int32_t *d_ind,
-                  MirrorCheck *m) {
-  m->dev = ctx.take<unsigned long long>(1);
-  fork_side(ctx, 2);
-  OnStream on(ctx, ctx.side[2]);
-  zero_words(ctx, m->dev, sizeof(unsigned long long));
-  const int g = ctx.grid_for(ceil_div64(ceil_div64(n, kWave), 4), 256, 2);
-  mirror_check_kernel<<<g, 256, 0, ctx.stream>>>(n, d_ptr, d_ind, m->dev);
-  SP_LAUNCH_CHECK();
-  m->queued = true;
-}
-
-// Joins the check into the library stream and queues the copy of its result;
-// the caller's synchronize makes mirror_failed valid.
+// Queues the copy of the sum; the caller's synchronize makes mirror_failed
+// valid.
 void mirror_collect(Context &ctx, const MirrorCheck &m) {
   if (!m.queued) return;
-  join_side(ctx, 2);
   SP_HIP(hipMemcpyAsync(ctx.host_words + kMirrorHostWord, m.dev, sizeof(unsigned long long),
                         hipMemcpyDeviceToHost, ctx.stream));
 }
@@ -874,8 +807,9 @@ size_t table_ws_bytes(int32_t n, int32_t nnz, int32_t k, int32_t chunk_size,
 // with each row's number of valid entries.  Records the transpose and
 // similarity spans when the spans are enabled.  With `allow_local` false every
 // chunk takes the global path.  When is_symmetric chunks go to the chunk-local
-// sketch, the mirror check is queued into `mirror`; the caller collects it and,
-// if it failed, builds the table again with `allow_local` false.
+// sketch, the sketch kernels sum the mirror check into `mirror`; the caller
+// collects it and, if it failed, builds the table again with `allow_local`
+// false.
 void build_table(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
                  const int32_t *d_ind, bool is_symmetric, int32_t k, int32_t m_cap,
                  int32_t chunk_size, uint64_t *table, EventSpan *t_csc,
@@ -885,8 +819,14 @@ void build_table(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
   int32_t *lists = ctx.take<int32_t>(2 * static_cast<size_t>(chunks));
   int32_t *counts = ctx.take<int32_t>(2);
   const bool local = allow_local && chunk_local_supported(n, chunk_size);
-  // Forked before any sketch work so that it waits on nothing of this call.
-  if (local && is_symmetric) mirror_check(ctx, n, d_ptr, d_ind, mirror);
+  const bool check_mirror = local && is_symmetric;
+  unsigned long long *msum = nullptr;
+  if (check_mirror) {
+    msum = ctx.take<unsigned long long>(1);
+    zero_words(ctx, msum, sizeof(unsigned long long));
+    mirror->dev = msum;
+    mirror->queued = true;
+  }
 
   auto global_csc = [&](const int32_t **cp, const int32_t **ri) {
     // Reference: sporder/src/common/csr2csc.h:49-59.
@@ -936,7 +876,7 @@ void build_table(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
     fork_side(ctx, 1);
     OnStream on(ctx, ctx.side[1]);
     chunk_local_sketch_top_k(ctx, n, k, chunk_size, m_cap, d_ptr, d_ind, table, lists, counts,
-                             2, row_valid);
+                             2, row_valid, msum);
   }
   if (run_global) {
     fork_side(ctx, 0);
@@ -946,14 +886,14 @@ void build_table(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
     global_csc(&cp, &ri);
     t_csc->end(ctx.stream);
     chunk_sketch_top_k(ctx, n, nnz, k, chunk_size, m_cap, d_ptr, d_ind, cp, ri, table,
-                       lists + chunks, counts + 1, ctx.prep_ev, row_valid);
+                       lists + chunks, counts + 1, ctx.prep_ev, row_valid, msum);
   } else {
     t_csc->begin(ctx.stream);
     t_csc->end(ctx.stream);
   }
   if (run_global) SP_HIP(hipStreamWaitEvent(ctx.stream, ctx.prep_ev, 0));
   chunk_local_sketch_top_k(ctx, n, k, chunk_size, m_cap, d_ptr, d_ind, table, lists, counts, 1,
-                           row_valid);
+                           row_valid, msum);
   if (run_t2) join_side(ctx, 1);
   if (run_global) join_side(ctx, 0);
   t_sim->end(ctx.stream);

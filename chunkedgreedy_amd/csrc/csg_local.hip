@@ -134,7 +134,8 @@ __global__ void __launch_bounds__(kLocalThreads, (local_min_waves<CELLS, KEYCAP>
                               const int32_t *__restrict__ chunk_list_count,
                               int32_t *__restrict__ overflow,
                               int32_t *__restrict__ overflow_count,
-                              int32_t *__restrict__ row_valid) {
+                              int32_t *__restrict__ row_valid,
+                              unsigned long long *__restrict__ mirror) {
   constexpr int NB = 1 << NB_LOG2;
   static_assert(KEYCAP / (kSmallBucket + 1) <= ROWCAP, "large-bucket list must fit s_order");
   static_assert(NB <= kMultiMark && ROWCAP <= kMultiMark, "kMultiMark must be unused");
@@ -149,6 +150,7 @@ __global__ void __launch_bounds__(kLocalThreads, (local_min_waves<CELLS, KEYCAP>
   __shared__ int32_t s_slice_total[kLocalWaves]; // step 1's scan
   __shared__ int32_t s_class[kClasses + 1]; // counts, then cursors, per class
   __shared__ int32_t s_next_row;            // next entry of s_order to claim
+  __shared__ unsigned long long s_mirror;   // this workgroup's mirror-check terms
 
   const int tid = threadIdx.x;
   const int lane = lane_id();
@@ -158,6 +160,7 @@ __global__ void __launch_bounds__(kLocalThreads, (local_min_waves<CELLS, KEYCAP>
   const int64_t work = chunk_list ? *chunk_list_count : num_chunks;
 
   for (int32_t r = threadIdx.x; r < ROWCAP; r += kLocalThreads) s_order[r] = 0;
+  if (threadIdx.x == 0) s_mirror = 0;
   __syncthreads();
   for (int64_t t = blockIdx.x; t < work; t += gridDim.x) {
     const int32_t chunk = chunk_list ? chunk_list[t] : static_cast<int32_t>(t);
@@ -223,6 +226,7 @@ __global__ void __launch_bounds__(kLocalThreads, (local_min_waves<CELLS, KEYCAP>
     __syncthreads();
     // 2a. Scatter: one thread per row writes its keys; the bucket cursor
     //     moves s_bend[b] from the start to the end of bucket b.
+    unsigned long long msum = 0; // this thread's rows' mirror-check terms, when asked
     for (int32_t r = tid; r < rows; r += kLocalThreads) {
       const int32_t rb = row_ptr[cs + r];
       const int32_t len = s_size[r];
@@ -231,7 +235,14 @@ __global__ void __launch_bounds__(kLocalThreads, (local_min_waves<CELLS, KEYCAP>
         const uint32_t c = static_cast<uint32_t>(col_ind[rb + q]);
         const int32_t slot = atomicAdd(&s_bend[bucket_of(c, nbl)], 1);
         s_keys[slot] = (c << lb) | static_cast<uint32_t>(r);
+        if (mirror != nullptr) msum += mirror_term(cs + r, static_cast<int32_t>(c));
       }
+    }
+    if (mirror != nullptr) {
+      // One LDS atomic per wave: per-thread atomics on one LDS word serialise.
+#pragma unroll
+      for (int o = kWave / 2; o > 0; o >>= 1) msum += __shfl_xor(msum, o);
+      if (lane == 0 && msum != 0) atomicAdd(&s_mirror, msum);
     }
     __syncthreads();
     // 2b. Sort each bucket: up to 16 keys by one thread in registers (a
@@ -384,6 +395,9 @@ __global__ void __launch_bounds__(kLocalThreads, (local_min_waves<CELLS, KEYCAP>
     }
     __syncthreads(); // LDS is reused by the next chunk of this workgroup
   }
+  // One global atomic per workgroup (the last barrier above ordered every
+  // row's LDS atomic before this read).
+  if (mirror != nullptr && threadIdx.x == 0 && s_mirror != 0) atomicAdd(mirror, s_mirror);
 }
 
 // Tier parameters: (key capacity, row capacity, log2 buckets).
@@ -487,7 +501,8 @@ template <int CELLS, int KEYCAP, int ROWCAP, int NB_LOG2>
 void launch_tier(Context &ctx, int32_t n, int32_t k, int32_t chunk_size, int32_t lb,
                  const int32_t *d_ptr, const int32_t *d_ind, uint64_t *d_table,
                  const int32_t *list, const int32_t *list_count, int32_t *ovf,
-                 int32_t *ovf_count, int per_cu, int32_t *d_row_valid) {
+                 int32_t *ovf_count, int per_cu, int32_t *d_row_valid,
+                 unsigned long long *mirror) {
   const int64_t chunks = ceil_div64(n, chunk_size);
   // A fixed grid striding over the work: no launch per chunk of an empty list.
   int64_t grid = list ? std::min<int64_t>(chunks, static_cast<int64_t>(ctx.num_cus) * per_cu)
@@ -495,7 +510,7 @@ void launch_tier(Context &ctx, int32_t n, int32_t k, int32_t chunk_size, int32_t
   chunk_local_sketch_kernel<CELLS, KEYCAP, ROWCAP, NB_LOG2>
       <<<dim3(static_cast<unsigned>(grid)), kLocalThreads, 0, ctx.stream>>>(
           n, k, chunk_size, lb, d_ptr, d_ind, d_table, list, list_count, ovf, ovf_count,
-          d_row_valid);
+          d_row_valid, mirror);
   SP_LAUNCH_CHECK();
 }
 
@@ -503,16 +518,16 @@ template <int CELLS>
 void launch_local(Context &ctx, int32_t n, int32_t k, int32_t chunk_size, int32_t lb,
                   const int32_t *d_ptr, const int32_t *d_ind, uint64_t *d_table,
                   const int32_t *lists, const int32_t *counts, int tiers,
-                  int32_t *d_row_valid) {
+                  int32_t *d_row_valid, unsigned long long *mirror) {
   if (tiers & 2) {
     launch_tier<CELLS, kT2Keys, kT2Rows, kT2Nb>(ctx, n, k, chunk_size, lb, d_ptr, d_ind,
                                                 d_table, lists, counts, nullptr, nullptr, 1,
-                                                d_row_valid);
+                                                d_row_valid, mirror);
   }
   if ((tiers & 1) && chunk_size <= kT1Rows) {
     launch_tier<CELLS, kT1Keys, kT1Rows, kT1Nb>(ctx, n, k, chunk_size, lb, d_ptr, d_ind,
                                                 d_table, nullptr, nullptr, nullptr, nullptr, 2,
-                                                d_row_valid);
+                                                d_row_valid, mirror);
   }
 }
 
@@ -540,7 +555,8 @@ void chunk_local_classify(Context &ctx, int32_t n, int32_t chunk_size, const int
 void chunk_local_sketch_top_k(Context &ctx, int32_t n, int32_t k, int32_t chunk_size,
                               int32_t m_capacity, const int32_t *d_ptr, const int32_t *d_ind,
                               uint64_t *d_table, const int32_t *d_lists,
-                              const int32_t *d_counts, int tiers, int32_t *d_row_valid) {
+                              const int32_t *d_counts, int tiers, int32_t *d_row_valid,
+                              unsigned long long *mirror) {
   SP_EXPECT(k <= 512, "k must be <= 512");
   SP_EXPECT(chunk_local_supported(n, chunk_size), "chunk-local sketch not applicable");
   const int32_t lb = bits_for(chunk_size - 1);
@@ -548,7 +564,7 @@ void chunk_local_sketch_top_k(Context &ctx, int32_t n, int32_t k, int32_t chunk_
 #define SP_CASE(C)                                                                       \
   case C:                                                                                \
     launch_local<C>(ctx, n, k, chunk_size, lb, d_ptr, d_ind, d_table, d_lists, d_counts, \
-                    tiers, d_row_valid);                                                 \
+                    tiers, d_row_valid, mirror);                                         \
     break;
     SP_CASE(1) SP_CASE(2) SP_CASE(3) SP_CASE(4) SP_CASE(5) SP_CASE(6)
     SP_CASE(7) SP_CASE(8) SP_CASE(9) SP_CASE(10) SP_CASE(11) SP_CASE(12)

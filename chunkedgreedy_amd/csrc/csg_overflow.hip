@@ -250,8 +250,13 @@ __global__ void __launch_bounds__(kOvfBlock)
                       const int2 *__restrict__ pairs, uint64_t *__restrict__ table,
                       const int32_t *__restrict__ list,
                       const int32_t *__restrict__ list_count, uint32_t *__restrict__ claim,
-                      int32_t *__restrict__ row_valid) {
+                      int32_t *__restrict__ row_valid, const int32_t *__restrict__ col_ind,
+                      unsigned long long *__restrict__ mirror) {
   __shared__ RunLookup s_lookup[kOvfWaves];
+  __shared__ unsigned long long s_mirror;
+  if (threadIdx.x == 0) s_mirror = 0;
+  __syncthreads();
+  unsigned long long msum = 0; // mirror-check terms of this lane's nonzeros
   const int lane = lane_id();
   RunLookup *lk = &s_lookup[threadIdx.x / kWave];
   // work < 2^32: list_len * chunk_size <= n + chunk_size - 1.
@@ -273,6 +278,9 @@ __global__ void __launch_bounds__(kOvfBlock)
     uint64_t *out = table + static_cast<size_t>(row) * k;
     const int32_t rs = row_ptr[row], re = row_ptr[row + 1];
     const int32_t deg = re - rs;
+    if (mirror != nullptr) {
+      for (int32_t q = rs + lane; q < re; q += kWave) msum += mirror_term(row, col_ind[q]);
+    }
     if (deg == 0) {
       for (int32_t j = lane; j < k; j += kWave) out[j] = 0;
       if (row_valid != nullptr && lane == 0) row_valid[row] = 0;
@@ -303,18 +311,27 @@ __global__ void __launch_bounds__(kOvfBlock)
     store.select_top_k(k, out);
     if (row_valid != nullptr && lane == 0) row_valid[row] = min(k, store.filled);
   }
+  if (mirror != nullptr) {
+    // Wave sums into LDS, then one global atomic per workgroup.
+#pragma unroll
+    for (int o = kWave / 2; o > 0; o >>= 1) msum += __shfl_xor(msum, o);
+    if (lane == 0 && msum != 0) atomicAdd(&s_mirror, msum);
+    __syncthreads();
+    if (threadIdx.x == 0 && s_mirror != 0) atomicAdd(mirror, s_mirror);
+  }
 }
 
 template <int CELLS>
 void launch_ovf_sketch(Context &ctx, int32_t n, int32_t k, int32_t chunk_size,
                        const int32_t *d_ptr, const int2 *runs, const int2 *pairs,
                        uint64_t *d_table, const int32_t *list, const int32_t *list_count,
-                       uint32_t *claim, int32_t *d_row_valid) {
+                       uint32_t *claim, int32_t *d_row_valid, const int32_t *d_ind,
+                       unsigned long long *mirror) {
   const int g = ctx.grid_for(ceil_div64(n, kOvfWaves), kOvfBlock, 4);
   fill_u32(ctx, claim, 1, 0u);
   ovf_sketch_kernel<CELLS><<<g, kOvfBlock, 0, ctx.stream>>>(n, k, chunk_size, d_ptr, runs,
                                                             pairs, d_table, list, list_count,
-                                                            claim, d_row_valid);
+                                                            claim, d_row_valid, d_ind, mirror);
   SP_LAUNCH_CHECK();
 }
 
@@ -331,7 +348,7 @@ void chunk_sketch_top_k(Context &ctx, int32_t n, int32_t nnz, int32_t k, int32_t
                         const int32_t *d_col_ptr, const int32_t *d_row_ind,
                         uint64_t *d_table, const int32_t *d_chunks,
                         const int32_t *d_chunk_count, hipEvent_t prepared,
-                        int32_t *d_row_valid) {
+                        int32_t *d_row_valid, unsigned long long *mirror) {
   SP_EXPECT(k <= 512, "k must be <= 512");
   SP_EXPECT(m_capacity % 32 == 0 && m_capacity >= 32 && m_capacity <= 512,
             "sketch capacity must be a multiple of 32 in [32, 512]");
@@ -360,7 +377,7 @@ void chunk_sketch_top_k(Context &ctx, int32_t n, int32_t nnz, int32_t k, int32_t
 #define SP_CASE(C)                                                                       \
   case C:                                                                                \
     launch_ovf_sketch<C>(ctx, n, k, chunk_size, d_ptr, runs, pairs, d_table, d_chunks,   \
-                         d_chunk_count, claim, d_row_valid);                             \
+                         d_chunk_count, claim, d_row_valid, d_ind, mirror);              \
     break;
     SP_CASE(1) SP_CASE(2) SP_CASE(3) SP_CASE(4) SP_CASE(5) SP_CASE(6)
     SP_CASE(7) SP_CASE(8) SP_CASE(9) SP_CASE(10) SP_CASE(11) SP_CASE(12)
