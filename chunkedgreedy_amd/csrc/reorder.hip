@@ -43,14 +43,12 @@ struct BigCtl {
   int32_t units;
 };
 // One call's control words, zeroed by prepare_rows and read back once after
-// permute_rows: the count of rows past kBlockSortCap (listed for the
-// device-wide sort), the wide-remap flag, the big-row registry's counts and
-// the longest row (SYMMETRIC; narrow_map reduces it from the tile maxima).
+// permute_rows: the three sort-list counts, the wide-remap flag, the big-row
+// registry's counts.
 struct Ctl {
-  int32_t huge;
+  int32_t counts[3];
   int32_t wide;
   BigCtl big;
-  int32_t max_len;
 };
 
 int64_t max_big_rows(int32_t nnz) { return nnz / (kBigRow + 1) + 1; }
@@ -68,15 +66,13 @@ __global__ void __launch_bounds__(kPrepBlock)
     prepare_rows(int32_t n, const int32_t *__restrict__ ptr_old,
                  const int32_t *__restrict__ new2old, int32_t *__restrict__ ptr_new,
                  int32_t *__restrict__ src_new, int32_t *__restrict__ old2new,
-                 int32_t *__restrict__ totals, int32_t *__restrict__ tile_max,
-                 Ctl *__restrict__ ctl) {
+                 int32_t *__restrict__ totals, Ctl *__restrict__ ctl) {
   __shared__ int32_t s_wave[kPrepBlock / kWave];
-  __shared__ int32_t s_wmax[kPrepBlock / kWave];
   if (blockIdx.x == 0 && threadIdx.x < sizeof(Ctl) / 4) {
     reinterpret_cast<int32_t *>(ctl)[threadIdx.x] = 0;
   }
   const int64_t base = static_cast<int64_t>(blockIdx.x) * kScanTileElems;
-  int32_t sum = 0, longest = 0;
+  int32_t sum = 0;
 #pragma unroll 4
   for (int r = 0; r < kScanTileElems / kPrepBlock; ++r) {
     const int64_t i = base + r * kPrepBlock + threadIdx.x;
@@ -91,25 +87,16 @@ __global__ void __launch_bounds__(kPrepBlock)
       ptr_new[i] = len;
       if (old2new) old2new[o] = static_cast<int32_t>(p);
       sum += len;
-      longest = max(longest, len);
     }
   }
   sum = wave_sum(sum);
-  longest = __builtin_amdgcn_readlane(wave_incl_max(longest), kWave - 1);
-  if (lane_id() == 0) {
-    s_wave[threadIdx.x / kWave] = sum;
-    s_wmax[threadIdx.x / kWave] = longest;
-  }
+  if (lane_id() == 0) s_wave[threadIdx.x / kWave] = sum;
   __syncthreads();
   if (threadIdx.x == 0) {
-    int32_t t = 0, m = 0;
+    int32_t t = 0;
 #pragma unroll
-    for (int w = 0; w < kPrepBlock / kWave; ++w) {
-      t += s_wave[w];
-      m = max(m, s_wmax[w]);
-    }
+    for (int w = 0; w < kPrepBlock / kWave; ++w) t += s_wave[w];
     totals[blockIdx.x] = t;
-    tile_max[blockIdx.x] = m;
   }
 }
 
@@ -120,20 +107,10 @@ __global__ void __launch_bounds__(kPrepBlock)
 // larger move sets ctl->wide, and permute_rows then reads old2new.
 __global__ void __launch_bounds__(256)
     narrow_map(int32_t n, const int32_t *__restrict__ old2new, int16_t *__restrict__ delta,
-               const int32_t *__restrict__ tile_max, int32_t tiles, Ctl *__restrict__ ctl) {
+               Ctl *__restrict__ ctl) {
   __shared__ int32_t s_far;
-  __shared__ int32_t s_max;
-  if (threadIdx.x == 0) {
-    s_far = 0;
-    s_max = 0;
-  }
+  if (threadIdx.x == 0) s_far = 0;
   __syncthreads();
-  // Workgroup 0 also reduces prepare_rows' tile maxima to the longest row.
-  if (blockIdx.x == 0) {
-    int32_t m = 0;
-    for (int32_t t = threadIdx.x; t < tiles; t += blockDim.x) m = max(m, tile_max[t]);
-    atomicMax(&s_max, m);
-  }
   bool far = false;
   for (int64_t c = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; c < n;
        c += static_cast<int64_t>(gridDim.x) * blockDim.x) {
@@ -147,7 +124,6 @@ __global__ void __launch_bounds__(256)
   // sets the flag from every workgroup, and per-wave atomics on one word
   // would serialise.
   if (threadIdx.x == 0 && s_far != 0) atomicOr(&ctl->wide, 1);
-  if (blockIdx.x == 0 && threadIdx.x == 0) ctl->max_len = s_max;
 }
 
 // Appends `value` for every lane with `take` to list[*count ...]: one atomic
@@ -226,18 +202,19 @@ __device__ __forceinline__ void group_sort2(int32_t &key, float &v, int32_t &key
 // new2old[p] (which starts at src_new[p]) to row p, mapping columns through
 // col_map when given.  With col_map (SYMMETRIC) a row of at most 2G entries is
 // also sorted in registers (bitonic network over the group's lanes, one or two
-// registers each) and written in final order; a longer row is sorted by a
-// later stage, which finds
-// it by its length: up to kWaveSortCap entries by sort_rows_wave, which reads
-// the row written here unsorted to key_tmp/val_tmp; up to kBlockSortCap by
-// sort_rows_block, which gathers the old row itself; longer rows are listed
-// (`huge`, counted in ctl->huge) for the device-wide sort and registered for
-// copy_big_rows.  Without col_map (ROWS) rows are copied verbatim, and rows
-// past kBigRow entries are registered for copy_big_rows.  The huge-row list
-// and the registry take one atomic per wave that has such a row (few rows;
-// per-wave atomics on one word from every wave serialise).  With val_new set
-// and val_old NULL the values written are 0.0f, as in the reference's
-// gather_rows (reorder.cu:37-45).
+// registers each) and written in final order; a longer row is appended to the
+// list of the stage that sorts it, with counts in ctl->counts[0..2]: lists[0]
+// (up to kWaveSortCap entries, sort_rows_wave, which reads the row written
+// here unsorted to key_tmp/val_tmp), lists[1] (up to kBlockSortCap,
+// sort_rows_block, which gathers the old row itself), lists[2] (longer, the
+// device-wide sort, whose rows are registered for copy_big_rows).  Without
+// col_map (ROWS) rows are copied verbatim, and rows past kBigRow entries are
+// registered for copy_big_rows.  List and registry appends take one atomic
+// per wave that has such rows: rows past 2G entries are a minority even on
+// power-law inputs, while a list of every row past G entries (a fifth of the
+// rows of a mean-13 random geometric graph) serialised on its counter.  With
+// val_new set and val_old NULL the values written are 0.0f, as in the
+// reference's gather_rows (reorder.cu:37-45).
 template <int G, int U>
 __global__ void __launch_bounds__(256)
     permute_rows(int32_t n, const int32_t *__restrict__ src_new,
@@ -246,8 +223,8 @@ __global__ void __launch_bounds__(256)
                  const int32_t *__restrict__ ptr_new,
                  int32_t *__restrict__ ind_new, float *__restrict__ val_new,
                  int32_t *__restrict__ key_tmp, float *__restrict__ val_tmp,
-                 int32_t *__restrict__ huge, Ctl *__restrict__ ctl, BigRow *big_rows,
-                 int32_t *big_owner) {
+                 int32_t *__restrict__ lists, int32_t list_stride, Ctl *__restrict__ ctl,
+                 BigRow *big_rows, int32_t *big_owner) {
   constexpr int kRowsPerWave = kWave / G;
   // The 16-bit remap when narrow_map found every move within its range.
   const bool narrow = delta != nullptr && ctl->wide == 0;
@@ -377,8 +354,13 @@ __global__ void __launch_bounds__(256)
         }
       }
       if (col_map != nullptr) {
-        wave_append(row_ok && gl == 0 && len[u] > kBlockSortCap, static_cast<int32_t>(p), huge,
-                    &ctl->huge);
+        const bool listed = row_ok && gl == 0 && !sort_here;
+        const int32_t row = static_cast<int32_t>(p);
+        wave_append(listed && len[u] <= kWaveSortCap, row, lists, ctl->counts);
+        wave_append(listed && len[u] > kWaveSortCap && len[u] <= kBlockSortCap, row,
+                    lists + list_stride, ctl->counts + 1);
+        wave_append(listed && len[u] > kBlockSortCap, row, lists + 2 * list_stride,
+                    ctl->counts + 2);
       }
     }
   }
@@ -469,108 +451,78 @@ __device__ __forceinline__ void wave_sort_row(int32_t s, int32_t len,
   }
 }
 
-// Rows of lo+1 .. kWaveSortCap entries (lo = the register-sorted length),
-// found by their length: each wave takes 64 consecutive rows and sorts each
-// of its rows in that class in registers (64, 128, 256 or 512 slots by the
-// row's length; longer rows sort faster in a workgroup's LDS).
+// Listed rows of up to kWaveSortCap entries, one wave per row, sorted in
+// registers (64, 128, 256 or 512 slots by the row's length; longer rows sort
+// faster in a workgroup's LDS).
 __global__ void __launch_bounds__(256)
-    sort_rows_wave(int32_t n, int32_t lo, const int32_t *__restrict__ ptr,
-                   const int32_t *__restrict__ key_in, const float *__restrict__ val_in,
-                   int32_t *__restrict__ key_out, float *__restrict__ val_out) {
-  const int lane = lane_id();
+    sort_rows_wave(const int32_t *__restrict__ rows, int32_t count,
+                   const int32_t *__restrict__ ptr, const int32_t *__restrict__ key_in,
+                   const float *__restrict__ val_in, int32_t *__restrict__ key_out,
+                   float *__restrict__ val_out) {
   const int64_t wave0 = (blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x) / kWave;
   const int64_t nwaves = static_cast<int64_t>(gridDim.x) * blockDim.x / kWave;
-  for (int64_t r0 = wave0 * kWave; r0 < n; r0 += nwaves * kWave) {
-    const int64_t r = r0 + lane;
-    int32_t s = 0, len = 0;
-    if (r < n) {
-      s = ptr[r];
-      len = ptr[r + 1] - s;
-    }
-    uint64_t m = ballot(len > lo && len <= kWaveSortCap);
-    while (m != 0) {
-      const int l = __builtin_ctzll(m);
-      m &= m - 1;
-      const int32_t rs = readlane(s, l), rl = readlane(len, l);
-      if (rl <= kWave) {
-        wave_sort_row<1>(rs, rl, key_in, val_in, key_out, val_out);
-      } else if (rl <= 2 * kWave) {
-        wave_sort_row<2>(rs, rl, key_in, val_in, key_out, val_out);
-      } else if (rl <= 4 * kWave) {
-        wave_sort_row<4>(rs, rl, key_in, val_in, key_out, val_out);
-      } else {
-        wave_sort_row<8>(rs, rl, key_in, val_in, key_out, val_out);
-      }
+  for (int64_t t = wave0; t < count; t += nwaves) {
+    const int32_t r = rows[t];
+    const int32_t s = ptr[r], len = ptr[r + 1] - s;
+    if (len <= kWave) {
+      wave_sort_row<1>(s, len, key_in, val_in, key_out, val_out);
+    } else if (len <= 2 * kWave) {
+      wave_sort_row<2>(s, len, key_in, val_in, key_out, val_out);
+    } else if (len <= 4 * kWave) {
+      wave_sort_row<4>(s, len, key_in, val_in, key_out, val_out);
+    } else {
+      wave_sort_row<8>(s, len, key_in, val_in, key_out, val_out);
     }
   }
 }
 
-// Rows of kWaveSortCap+1 .. kBlockSortCap entries, found by their length
-// (each workgroup scans 256 rows at a time), one workgroup per row: the old
-// row (starting at src_new[r]) is gathered with its columns remapped (the
-// 16-bit delta table when `narrow`, else col_map), sorted in LDS (bitonic) and
-// written to row r.
+// Listed rows of kWaveSortCap+1 .. kBlockSortCap entries, one workgroup per
+// row: the old row (starting at src_new[r]) is gathered with its columns
+// remapped (the 16-bit delta table when `narrow`, else col_map), sorted in
+// LDS (bitonic) and written to row r.
 __global__ void __launch_bounds__(kBlockSortThreads)
-    sort_rows_block(int32_t n, const int32_t *__restrict__ ptr,
-                    const int32_t *__restrict__ src_new, const int32_t *__restrict__ ind_old,
-                    const float *__restrict__ val_old, const int32_t *__restrict__ col_map,
-                    const int16_t *__restrict__ delta, bool narrow,
-                    int32_t *__restrict__ key_out, float *__restrict__ val_out) {
+    sort_rows_block(const int32_t *__restrict__ ptr, const int32_t *__restrict__ long_rows,
+                    int32_t long_count, const int32_t *__restrict__ src_new,
+                    const int32_t *__restrict__ ind_old, const float *__restrict__ val_old,
+                    const int32_t *__restrict__ col_map, const int16_t *__restrict__ delta,
+                    bool narrow, int32_t *__restrict__ key_out, float *__restrict__ val_out) {
   __shared__ int32_t sk[kBlockSortCap];
   __shared__ float sv[kBlockSortCap];
-  __shared__ int32_t s_rows[kBlockSortThreads];
-  __shared__ int32_t s_cnt;
-  for (int64_t base = blockIdx.x * static_cast<int64_t>(kBlockSortThreads); base < n;
-       base += static_cast<int64_t>(gridDim.x) * kBlockSortThreads) {
-    if (threadIdx.x == 0) s_cnt = 0;
-    __syncthreads();
-    const int64_t rr = base + threadIdx.x;
-    if (rr < n) {
-      const int32_t l = ptr[rr + 1] - ptr[rr];
-      if (l > kWaveSortCap && l <= kBlockSortCap) {
-        s_rows[atomicAdd(&s_cnt, 1)] = static_cast<int32_t>(rr);
-      }
+  for (int32_t t = blockIdx.x; t < long_count; t += gridDim.x) {
+    const int32_t r = long_rows[t];
+    const int32_t s = ptr[r], len = ptr[r + 1] - s, src = src_new[r];
+    int32_t pow2 = 1;
+    while (pow2 < len) pow2 <<= 1;
+    for (int32_t i = threadIdx.x; i < pow2; i += blockDim.x) {
+      const bool in = i < len;
+      const int32_t c = in ? ind_old[src + i] : 0;
+      sk[i] = in ? (narrow ? c + delta[c] : col_map[c]) : 0x7fffffff;
+      sv[i] = (in && val_old) ? val_old[src + i] : 0.0f;
     }
     __syncthreads();
-    const int32_t cnt = s_cnt;
-    for (int32_t t = 0; t < cnt; ++t) {
-      const int32_t r = s_rows[t];
-      const int32_t s = ptr[r], len = ptr[r + 1] - s, src = src_new[r];
-      int32_t pow2 = 1;
-      while (pow2 < len) pow2 <<= 1;
-      for (int32_t i = threadIdx.x; i < pow2; i += blockDim.x) {
-        const bool in = i < len;
-        const int32_t c = in ? ind_old[src + i] : 0;
-        sk[i] = in ? (narrow ? c + delta[c] : col_map[c]) : 0x7fffffff;
-        sv[i] = (in && val_old) ? val_old[src + i] : 0.0f;
-      }
-      __syncthreads();
-      for (int32_t kk = 2; kk <= pow2; kk <<= 1) {
-        for (int32_t j = kk >> 1; j > 0; j >>= 1) {
-          for (int32_t i = threadIdx.x; i < pow2; i += blockDim.x) {
-            const int32_t partner = i ^ j;
-            if (partner > i) {
-              const bool ascending = (i & kk) == 0;
-              const int32_t a = sk[i], b = sk[partner];
-              if ((a > b) == ascending) {
-                sk[i] = b;
-                sk[partner] = a;
-                const float fa = sv[i];
-                sv[i] = sv[partner];
-                sv[partner] = fa;
-              }
+    for (int32_t kk = 2; kk <= pow2; kk <<= 1) {
+      for (int32_t j = kk >> 1; j > 0; j >>= 1) {
+        for (int32_t i = threadIdx.x; i < pow2; i += blockDim.x) {
+          const int32_t partner = i ^ j;
+          if (partner > i) {
+            const bool ascending = (i & kk) == 0;
+            const int32_t a = sk[i], b = sk[partner];
+            if ((a > b) == ascending) {
+              sk[i] = b;
+              sk[partner] = a;
+              const float fa = sv[i];
+              sv[i] = sv[partner];
+              sv[partner] = fa;
             }
           }
-          __syncthreads();
         }
+        __syncthreads();
       }
-      for (int32_t i = threadIdx.x; i < len; i += blockDim.x) {
-        key_out[s + i] = sk[i];
-        if (val_out) val_out[s + i] = sv[i];
-      }
-      __syncthreads();
     }
-    // Every thread has read this tile's count before the next tile resets it.
+    for (int32_t i = threadIdx.x; i < len; i += blockDim.x) {
+      key_out[s + i] = sk[i];
+      if (val_out) val_out[s + i] = sv[i];
+    }
     __syncthreads();
   }
 }
@@ -687,28 +639,28 @@ template <int G>
 void launch_permute_g(Context &ctx, int32_t n, const int32_t *src_new, const int32_t *ind_old,
                       const float *val_old, const int32_t *col_map, const int16_t *delta,
                       const int32_t *ptr_new, int32_t *ind_new, float *val_new,
-                      int32_t *key_tmp, float *val_tmp, int32_t *huge, Ctl *ctl,
-                      BigRow *big_rows, int32_t *big_owner) {
+                      int32_t *key_tmp, float *val_tmp, int32_t *lists, int32_t list_stride,
+                      Ctl *ctl, BigRow *big_rows, int32_t *big_owner) {
   constexpr int U = G <= 16 ? 4 : 2;
   constexpr int rows_per_block = 4 * (kWave / G) * U;
   const int g = ctx.grid_for(ceil_div64(n, rows_per_block), 256, 4);
   permute_rows<G, U><<<g, 256, 0, ctx.stream>>>(n, src_new, ind_old, val_old, col_map, delta,
                                                 ptr_new, ind_new, val_new, key_tmp, val_tmp,
-                                                huge, ctl, big_rows, big_owner);
+                                                lists, list_stride, ctl, big_rows, big_owner);
   SP_LAUNCH_CHECK();
 }
 
 void launch_permute(Context &ctx, int G, int32_t n, const int32_t *src_new,
                     const int32_t *ind_old, const float *val_old, const int32_t *col_map,
                     const int16_t *delta, const int32_t *ptr_new, int32_t *ind_new,
-                    float *val_new, int32_t *key_tmp, float *val_tmp, int32_t *huge, Ctl *ctl,
-                    BigRow *big_rows, int32_t *big_owner) {
+                    float *val_new, int32_t *key_tmp, float *val_tmp, int32_t *lists,
+                    int32_t list_stride, Ctl *ctl, BigRow *big_rows, int32_t *big_owner) {
   switch (G) {
 #define SP_CASE(V)                                                                       \
   case V:                                                                                \
     launch_permute_g<V>(ctx, n, src_new, ind_old, val_old, col_map, delta, ptr_new,      \
-                        ind_new, val_new, key_tmp, val_tmp, huge, ctl, big_rows,         \
-                        big_owner);                                                      \
+                        ind_new, val_new, key_tmp, val_tmp, lists, list_stride, ctl,     \
+                        big_rows, big_owner);                                            \
     break;
     SP_CASE(4) SP_CASE(8) SP_CASE(16) SP_CASE(32) SP_CASE(64)
 #undef SP_CASE
@@ -752,10 +704,9 @@ extern "C" void sporder_reorder(sporder_context_t h, int32_t n, int32_t nnz,
                 ws_bytes<Ctl>(1) + ws_bytes<BigRow>(static_cast<size_t>(max_big_rows(nnz))) +
                 ws_bytes<int32_t>(static_cast<size_t>(max_copy_units(nnz))) + ws_bytes<int32_t>(n);
   const int64_t scan_tiles = ceil_div64(static_cast<int64_t>(n) + 1, kScanTileElems);
-  need += ws_bytes<int32_t>(static_cast<size_t>(scan_tiles));
   if (symmetric) {
     need += ws_bytes<int32_t>(n) + ws_bytes<int16_t>(n) + ws_bytes<int32_t>(nnz) +
-            ws_bytes<float>(nnz) + ws_bytes<int32_t>(2 * (static_cast<size_t>(n) + 2));
+            ws_bytes<float>(nnz) + ws_bytes<int32_t>(3 * (static_cast<size_t>(n) + 2));
   }
   ctx.reserve(need);
   int32_t *scan_tmp = ctx.take<int32_t>(scan_tmp_elems(static_cast<int64_t>(n) + 1));
@@ -763,13 +714,12 @@ extern "C" void sporder_reorder(sporder_context_t h, int32_t n, int32_t nnz,
   BigRow *big_rows = ctx.take<BigRow>(static_cast<size_t>(max_big_rows(nnz)));
   int32_t *big_owner = ctx.take<int32_t>(static_cast<size_t>(max_copy_units(nnz)));
   int32_t *src_new = ctx.take<int32_t>(n);
-  int32_t *tile_max = ctx.take<int32_t>(static_cast<size_t>(scan_tiles));
   int32_t *old2new = symmetric ? ctx.take<int32_t>(n) : nullptr;
 
   const int row_grid = ctx.grid_for(ceil_div64(n, 256), 256, 4);
 
   prepare_rows<<<dim3(static_cast<unsigned>(scan_tiles)), kPrepBlock, 0, ctx.stream>>>(
-      n, d_ptr_old, d_new_order, d_ptr_new, src_new, old2new, scan_tmp, tile_max, ctl);
+      n, d_ptr_old, d_new_order, d_ptr_new, src_new, old2new, scan_tmp, ctl);
   SP_LAUNCH_CHECK();
   scan_i32_from_totals(ctx, d_ptr_new, d_ptr_new, static_cast<int64_t>(n) + 1, true, scan_tmp);
 
@@ -789,7 +739,8 @@ extern "C" void sporder_reorder(sporder_context_t h, int32_t n, int32_t nnz,
 
   if (!symmetric) {
     launch_permute(ctx, G, n, src_new, d_ind_old, d_val_old, nullptr, nullptr, d_ptr_new,
-                   d_ind_new, d_val_new, nullptr, nullptr, nullptr, ctl, big_rows, big_owner);
+                   d_ind_new, d_val_new, nullptr, nullptr, nullptr, 0, ctl, big_rows,
+                   big_owner);
     read_ctl();
     if (hc.big.units > 0) {
       launch_copy_big(ctx, hc.big.units, d_ind_old, d_val_old, nullptr, big_rows, big_owner,
@@ -802,48 +753,47 @@ extern "C" void sporder_reorder(sporder_context_t h, int32_t n, int32_t nnz,
   int16_t *delta = ctx.take<int16_t>(n);
   int32_t *unsorted = ctx.take<int32_t>(nnz);
   float *val_unsorted = ctx.take<float>(nnz);
-  // Rows past kBlockSortCap (listed by permute_rows) and the device-wide
-  // sort's offsets.
-  int32_t *huge_rows = ctx.take<int32_t>(static_cast<size_t>(n) + 2);
-  int32_t *huge_off = ctx.take<int32_t>(static_cast<size_t>(n) + 2);
+  // Row lists of the three sort stages, one array with stride n + 2.
+  const int32_t stride = n + 2;
+  int32_t *lists = ctx.take<int32_t>(3 * static_cast<size_t>(stride));
+  int32_t *list1 = lists, *long_rows = lists + stride, *huge_rows = lists + 2 * stride;
   const float *vo = with_vals ? d_val_old : nullptr;
   float *vn = with_vals ? d_val_new : nullptr;
   float *vt = with_vals ? val_unsorted : nullptr;
 
-  narrow_map<<<std::min(row_grid, 4 * ctx.num_cus), 256, 0, ctx.stream>>>(
-      n, old2new, delta, tile_max, static_cast<int32_t>(scan_tiles), ctl);
+  narrow_map<<<std::min(row_grid, 4 * ctx.num_cus), 256, 0, ctx.stream>>>(n, old2new, delta,
+                                                                          ctl);
   SP_LAUNCH_CHECK();
   // Rows of at most 2G entries are remapped, sorted and written in one pass;
-  // the stages below sort the longer ones, each finding its rows by length,
-  // and launch only when the longest row reaches them.
+  // longer rows are listed by length for the stage that sorts them, and the
+  // stages launch only when their lists have rows.
   launch_permute(ctx, G, n, src_new, d_ind_old, vo, old2new, delta, d_ptr_new, d_ind_new, vn,
-                 unsorted, vt, huge_rows, ctl, big_rows, big_owner);
+                 unsorted, vt, lists, stride, ctl, big_rows, big_owner);
   read_ctl();
   const bool narrow = hc.wide == 0;
   bool queued = false;
-  if (hc.max_len > 2 * G) {
-    const int g = std::min<int>(ctx.grid_for(ceil_div64(n, 4 * kWave), 256, 4),
-                                8 * ctx.num_cus);
-    sort_rows_wave<<<g, 256, 0, ctx.stream>>>(n, 2 * G, d_ptr_new, unsorted, vt, d_ind_new,
-                                              vn);
-    SP_LAUNCH_CHECK();
-    queued = true;
-  }
-  if (hc.max_len > kWaveSortCap) {
-    const int g = std::min<int>(static_cast<int>(ceil_div64(n, kBlockSortThreads)),
+  if (hc.counts[0] > 0) {
+    const int g = std::min<int>(ctx.grid_for(ceil_div64(hc.counts[0], 4), 256, 4),
                                 4 * ctx.num_cus);
-    sort_rows_block<<<g, kBlockSortThreads, 0, ctx.stream>>>(
-        n, d_ptr_new, src_new, d_ind_old, vo, old2new, delta, narrow, d_ind_new, vn);
+    sort_rows_wave<<<g, 256, 0, ctx.stream>>>(list1, hc.counts[0], d_ptr_new, unsorted, vt,
+                                              d_ind_new, vn);
     SP_LAUNCH_CHECK();
     queued = true;
   }
-  if (hc.huge > 0) {
+  if (hc.counts[1] > 0) {
+    sort_rows_block<<<std::min(hc.counts[1], ctx.num_cus * 4), kBlockSortThreads, 0,
+                      ctx.stream>>>(d_ptr_new, long_rows, hc.counts[1], src_new, d_ind_old, vo,
+                                    old2new, delta, narrow, d_ind_new, vn);
+    SP_LAUNCH_CHECK();
+    queued = true;
+  }
+  if (hc.counts[2] > 0) {
     // Rows past kBlockSortCap: copied unsorted (their units registered by
     // permute_rows), then one device-wide sort.
     launch_copy_big(ctx, hc.big.units, d_ind_old, vo, old2new, big_rows, big_owner, unsorted,
                     vt);
-    sort_huge_rows(ctx, n, d_ptr_new, huge_rows, hc.huge, unsorted, vt, d_ind_new, vn,
-                   huge_off, scan_tmp);
+    sort_huge_rows(ctx, n, d_ptr_new, huge_rows, hc.counts[2], unsorted, vt, d_ind_new, vn,
+                   list1, scan_tmp);
     queued = true;
   }
   if (queued) ctx.sync();
