@@ -326,13 +326,17 @@ def main():
 
     # Gather ceiling of the same kernel at the same shape (n rows, 16 nonzeros
     # per row, N = 128): columns drawn uniformly from the first 8192 rows (the
-    # 4 MiB of B that one XCD's L2 holds) and from all n rows (C2's pattern:
-    # every B row gather misses L2).
+    # 4 MiB of B that one XCD's L2 holds), from the first 65536 and 262144 rows
+    # (32 and 128 MiB of B: past the L2s, inside the 256 MB Infinity Cache) and
+    # from all n rows (C2's pattern: 512 MiB of B, every gather misses L2).
     ceiling = {}
     gen = torch.Generator(device=dev).manual_seed(7)
     cptr = torch.arange(0, nnz + 1, 16, dtype=torch.int32, device=dev)
     cval = torch.rand(nnz, generator=gen, device=dev)
-    for label, col_span in (("l2_resident_cols", 8192), ("uniform_cols", n)):
+    spans = (("l2_resident_cols", 8192), ("b_32mib_cols", 65536), ("b_128mib_cols", 262144),
+             ("uniform_cols", n))
+    for label, col_span in spans:
+        col_span = min(col_span, n)
         cind = torch.randint(0, col_span, (nnz,), generator=gen, device=dev, dtype=torch.int32)
         cind = cind.view(n, 16).sort(dim=1).values.reshape(-1).contiguous()
         t_c = spmm_ms(cptr, cind, cval, B128)
