@@ -211,7 +211,7 @@ __device__ __forceinline__ void feed_batch(WaveSketch<CELLS> &store, int2 pr, in
   uint64_t mask = ballot(item);
   while (mask) {
     const int i = __builtin_ctzll(mask);
-    store.add(readlane(pr.x, i), readlane_f(alpha, i));
+    store.template add<true>(readlane(pr.x, i), readlane_f(alpha, i));
     mask &= mask - 1;
   }
 }

@@ -44,6 +44,16 @@ __device__ __forceinline__ int32_t gallop_lower_bound(const int32_t *a, int32_t 
   return lower_bound_dev(a, lo + (b >> 1), lo + b < hi ? lo + b : hi, t);
 }
 
+// Per lane: `a` where the lane's bit of the wave mask is set, else `b`.  One
+// v_cndmask with the mask as its lane condition, written out so that the
+// compiler keeps it a select: left to itself it may turn a select on a
+// sparse mask into an execution-masked region behind a branch.
+__device__ __forceinline__ int32_t mask_select(uint64_t mask, int32_t a, int32_t b) {
+  int32_t r;
+  asm("v_cndmask_b32_e64 %0, %2, %1, %3" : "=v"(r) : "v"(a), "v"(b), "s"(mask));
+  return r;
+}
+
 // Space-saving sketch of capacity 32*CELLS spread over one wave64.
 template <int CELLS> struct WaveSketch {
   static constexpr int LC = (CELLS + 1) / 2; // cells held per physical lane
@@ -68,62 +78,79 @@ template <int CELLS> struct WaveSketch {
   }
 
   // Apply one item; k and w are wave-uniform.
+  //
+  // Every slot write below is a select whose per-lane condition is a wave
+  // mask (inverse ballot): the hit masks from the key compares, and for a
+  // miss the one-hot mask of the slot's lane, so the slot written costs two
+  // selects per cell and no lane compare.
+  //
+  // HIT_FIRST adds a hit's weight before testing for a miss: one branch per
+  // hit, for a wave whose single long stream is the critical path (one row's
+  // items are a dependent chain, and every taken branch lengthens it).
+  // Without it the adds run only on hits, behind a branch: fewer vector
+  // instructions per miss, for kernels where many waves share a SIMD and
+  // issue slots, not one chain, set the time.
+  template <bool HIT_FIRST = false>
   __device__ __forceinline__ void add(int32_t k, float w) {
-    bool hit = false;
+    uint64_t hit[LC];
+    uint64_t any = 0;
 #pragma unroll
     for (int j = 0; j < LC; ++j) {
-      if (key[j] == k) {
-        wt[j] += w;
-        hit = true;
-      }
+      // An unused cell holds key -1, which no item (a row index) equals.
+      hit[j] = ballot(key[j] == k);
+      any |= hit[j];
+      if (HIT_FIRST) wt[j] = __builtin_amdgcn_inverse_ballot_w64(hit[j]) ? wt[j] + w : wt[j];
     }
-    if (ballot(hit)) {
+    if (any) {
+      if (!HIT_FIRST) {
+#pragma unroll
+        for (int j = 0; j < LC; ++j) {
+          if (__builtin_amdgcn_inverse_ballot_w64(hit[j])) wt[j] += w;
+        }
+      }
       return;
     }
+    // A miss writes (k, wn) into one slot: the lane of the one-hot mask
+    // sel[j] in local cell j.
+    uint64_t sel[LC];
+    float wn;
     if (filled < M) {
       // Slot s = L*CELLS + c: logical lane L, cell c -> physical lane
       // L + 32*(c & 1), local cell c >> 1.
+      const uint32_t f = static_cast<uint32_t>(filled);
+      const uint32_t L = f / CELLS, c = f - L * CELLS;
+      const uint64_t bit = 1ull << (L + 32u * (c & 1u));
+#pragma unroll
+      for (int j = 0; j < LC; ++j) sel[j] = (static_cast<uint32_t>(j) == (c >> 1)) ? bit : 0;
+      wn = w;
+      filled += 1;
+    } else {
+      // Evict the argmin of (weight, c*32 + L).  With c = 2j + (p >> 5) and
+      // L = p & 31, c*32 + L = 64j + p, so ties go to the smallest cell index
+      // j and then the lowest physical lane p.  Weights are positive floats
+      // (sums of 2/(a+b)), so their bit patterns order like the values.
       const int lane = lane_id();
-      int L = filled / CELLS, c = filled - L * CELLS;
-      int owner = L + 32 * (c & 1), jj = c >> 1;
+      uint32_t lmin = 0xFFFFFFFFu;
 #pragma unroll
       for (int j = 0; j < LC; ++j) {
-        if (lane == owner && j == jj) {
-          key[j] = k;
-          wt[j] = w;
-        }
+        if (cell_valid(j, lane)) lmin = min(lmin, __float_as_uint(wt[j]));
       }
-      filled += 1;
-      return;
+      const uint32_t wmin = wave_min_u32(lmin);
+      // The evicted slot holds exactly wmin, so the weight it inherits,
+      // wmin + w, is the same value in every lane.
+      wn = __uint_as_float(wmin) + w;
+      bool found = false;
+#pragma unroll
+      for (int j = 0; j < LC; ++j) {
+        const uint64_t m = ballot(cell_valid(j, lane) && __float_as_uint(wt[j]) == wmin);
+        sel[j] = found ? 0 : (m & (~m + 1)); // lowest set lane
+        found = found || m != 0;
+      }
     }
-    // Evict the argmin of (weight, c*32 + L).  With c = 2j + (p >> 5) and
-    // L = p & 31, c*32 + L = 64j + p, so ties go to the smallest cell index j
-    // and then the lowest physical lane p.  Weights are positive floats (sums
-    // of 2/(a+b)), so their bit patterns order like the values.
-    const int lane = lane_id();
-    uint32_t lmin = 0xFFFFFFFFu;
 #pragma unroll
     for (int j = 0; j < LC; ++j) {
-      if (cell_valid(j, lane)) lmin = min(lmin, __float_as_uint(wt[j]));
-    }
-    const uint32_t wmin = wave_min_u32(lmin);
-    int jj = LC - 1;
-    uint64_t m = 0;
-#pragma unroll
-    for (int j = LC - 1; j >= 0; --j) {
-      const uint64_t mj = ballot(cell_valid(j, lane) && __float_as_uint(wt[j]) == wmin);
-      if (mj) {
-        m = mj;
-        jj = j;
-      }
-    }
-    const int owner = __builtin_ctzll(m);
-#pragma unroll
-    for (int j = 0; j < LC; ++j) {
-      if (lane == owner && j == jj) {
-        key[j] = k;
-        wt[j] += w; // inherits the evicted weight
-      }
+      key[j] = mask_select(sel[j], k, key[j]);
+      wt[j] = __int_as_float(mask_select(sel[j], __float_as_int(wn), __float_as_int(wt[j])));
     }
   }
 
