@@ -47,10 +47,18 @@ __device__ __forceinline__ int32_t gallop_lower_bound(const int32_t *a, int32_t 
 // Per lane: `a` where the lane's bit of the wave mask is set, else `b`.  One
 // v_cndmask with the mask as its lane condition, written out so that the
 // compiler keeps it a select: left to itself it may turn a select on a
-// sparse mask into an execution-masked region behind a branch.
+// sparse mask into an execution-masked region behind a branch.  The mask is
+// wave-uniform (built from ballots); readfirstlane states that to the
+// compiler, which drops it where it already holds the mask in scalar
+// registers.
 __device__ __forceinline__ int32_t mask_select(uint64_t mask, int32_t a, int32_t b) {
+  const uint64_t m =
+      static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int32_t>(mask))) |
+      (static_cast<uint64_t>(static_cast<uint32_t>(
+           __builtin_amdgcn_readfirstlane(static_cast<int32_t>(mask >> 32))))
+       << 32);
   int32_t r;
-  asm("v_cndmask_b32_e64 %0, %2, %1, %3" : "=v"(r) : "v"(a), "v"(b), "s"(mask));
+  asm("v_cndmask_b32_e64 %0, %2, %1, %3" : "=v"(r) : "v"(a), "v"(b), "s"(m));
   return r;
 }
 
