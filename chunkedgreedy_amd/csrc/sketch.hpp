@@ -100,24 +100,7 @@ template <int CELLS> struct WaveSketch {
   // issue slots, not one chain, set the time.
   template <bool HIT_FIRST = false>
   __device__ __forceinline__ void add(int32_t k, float w) {
-    uint64_t hit[LC];
-    uint64_t any = 0;
-#pragma unroll
-    for (int j = 0; j < LC; ++j) {
-      // An unused cell holds key -1, which no item (a row index) equals.
-      hit[j] = ballot(key[j] == k);
-      any |= hit[j];
-      if (HIT_FIRST) wt[j] = __builtin_amdgcn_inverse_ballot_w64(hit[j]) ? wt[j] + w : wt[j];
-    }
-    if (any) {
-      if (!HIT_FIRST) {
-#pragma unroll
-        for (int j = 0; j < LC; ++j) {
-          if (__builtin_amdgcn_inverse_ballot_w64(hit[j])) wt[j] += w;
-        }
-      }
-      return;
-    }
+    if (hit_update<HIT_FIRST>(k, w)) return;
     // A miss writes (k, wn) into one slot: the lane of the one-hot mask
     // sel[j] in local cell j.
     uint64_t sel[LC];
@@ -160,6 +143,82 @@ template <int CELLS> struct WaveSketch {
       key[j] = mask_select(sel[j], k, key[j]);
       wt[j] = __int_as_float(mask_select(sel[j], __float_as_int(wn), __float_as_int(wt[j])));
     }
+  }
+
+  // Apply the items of the lanes set in `mask`, in lane order: item i is
+  // (readlane(other, i), readlane(alpha, i)).  The same updates as add() item
+  // by item, in two loops: while slots are free a miss fills the next one,
+  // afterwards every miss evicts, so neither loop tests the capacity per
+  // item; and an eviction looks for the tied minimum only in the first cell
+  // that holds the minimum (ties go to the smallest cell index, then lane).
+  template <bool HIT_FIRST = false>
+  __device__ __forceinline__ void feed(uint64_t mask, int32_t other, float alpha) {
+    const int lane = lane_id();
+    while (mask != 0 && filled < M) {
+      const int i = __builtin_ctzll(mask);
+      mask &= mask - 1;
+      const int32_t k = readlane(other, i);
+      const float w = readlane_f(alpha, i);
+      if (hit_update<HIT_FIRST>(k, w)) continue;
+      const uint32_t f = static_cast<uint32_t>(filled);
+      const uint32_t L = f / CELLS, c = f - L * CELLS;
+      const uint64_t bit = 1ull << (L + 32u * (c & 1u));
+#pragma unroll
+      for (int j = 0; j < LC; ++j) {
+        const uint64_t sel = (static_cast<uint32_t>(j) == (c >> 1)) ? bit : 0;
+        key[j] = mask_select(sel, k, key[j]);
+        wt[j] = __int_as_float(mask_select(sel, __float_as_int(w), __float_as_int(wt[j])));
+      }
+      filled += 1;
+    }
+    while (mask != 0) {
+      const int i = __builtin_ctzll(mask);
+      mask &= mask - 1;
+      const int32_t k = readlane(other, i);
+      const float w = readlane_f(alpha, i);
+      if (hit_update<HIT_FIRST>(k, w)) continue;
+      uint32_t lmin = 0xFFFFFFFFu;
+#pragma unroll
+      for (int j = 0; j < LC; ++j) {
+        if (cell_valid(j, lane)) lmin = min(lmin, __float_as_uint(wt[j]));
+      }
+      const uint32_t wmin = wave_min_u32(lmin);
+      const float wn = __uint_as_float(wmin) + w; // the evicted slot holds wmin
+      bool found = false;
+#pragma unroll
+      for (int j = 0; j < LC; ++j) {
+        if (!found) {
+          const uint64_t m = ballot(cell_valid(j, lane) && __float_as_uint(wt[j]) == wmin);
+          if (m != 0) {
+            const uint64_t sel = 1ull << __builtin_ctzll(m);
+            key[j] = mask_select(sel, k, key[j]);
+            wt[j] = __int_as_float(mask_select(sel, __float_as_int(wn), __float_as_int(wt[j])));
+            found = true;
+          }
+        }
+      }
+    }
+  }
+
+  // The hit test of add(): true (and the weight added) when k is held.
+  template <bool HIT_FIRST>
+  __device__ __forceinline__ bool hit_update(int32_t k, float w) {
+    uint64_t hit[LC];
+    uint64_t any = 0;
+#pragma unroll
+    for (int j = 0; j < LC; ++j) {
+      hit[j] = ballot(key[j] == k);
+      any |= hit[j];
+      if (HIT_FIRST) wt[j] = __builtin_amdgcn_inverse_ballot_w64(hit[j]) ? wt[j] + w : wt[j];
+    }
+    if (any == 0) return false;
+    if (!HIT_FIRST) {
+#pragma unroll
+      for (int j = 0; j < LC; ++j) {
+        if (__builtin_amdgcn_inverse_ballot_w64(hit[j])) wt[j] += w;
+      }
+    }
+    return true;
   }
 
   // Reference select_top_k: per-logical-lane selection sort (strict '>',
