@@ -155,9 +155,12 @@ def chunk_similarity_top_k(ptr, ind, *, k, oversampling, chunk_size, is_symmetri
 
 def spmm_plan(ptr, ind, *, ctx=None):
     """(new) Analyse a CSR pattern for the planned SpMM (the harness's untimed
-    prepare step): tiles of rows that share few columns get those rows of B
-    staged in LDS.  Returns an SpmmPlan whose ``info`` dict counts the staged
-    tiles, rows, nonzeros and columns."""
+    prepare step): a 64-row tile whose 8-row blocks hold at most half as many
+    distinct columns as nonzeros is "blocked", and the planned SpMM loads each
+    such column's row of B once per block for every row of the block that
+    holds it.  Returns an SpmmPlan whose ``info`` dict counts the tiles, the
+    blocked tiles, their rows and nonzeros, and the (column, row mask)
+    entries."""
     return SpmmPlan(ptr, ind, ctx=ctx)
 
 
@@ -169,7 +172,8 @@ def spmm_csr(ptr, ind, val, B, *, out=None, algo="row_split", ctx=None, plan=Non
     in 512-nonzero segments added left to right (bit-reproducible);
     "merge_path" splits the nonzeros evenly across waves and adds the partial
     sums of cut rows with atomics.  With ``plan`` (spmm_plan of this pattern)
-    the staged tiles read B from LDS; the result equals "row_split" bit for
+    the blocked tiles load each distinct column's B row once per 8-row block
+    and the others run the row-split; the result equals "row_split" bit for
     bit.  Returns (C, kernel_ms)."""
     return _spmm_csr(ptr, ind, val, B, out=out, algo=algo, ctx=ctx, plan=plan)
 

@@ -301,9 +301,10 @@ def chunk_similarity_top_k(ptr, ind, k, oversampling, chunk_size, is_symmetric=F
 
 
 class SpmmPlan:
-    """An SpMM plan of one CSR pattern (new export): the tiles of rows whose
-    shared B rows the planned SpMM stages in LDS.  Owns device memory on the
-    context's device until closed or collected."""
+    """An SpMM plan of one CSR pattern (new export): the blocked tiles, whose
+    8-row blocks load each distinct column's B row once, and their (column,
+    row mask) entries.  Owns device memory on the context's device until
+    closed or collected."""
 
     def __init__(self, ptr, ind, ctx=None):
         ptr = _gpu_in(ptr, torch.int32, "ptr")

@@ -19,7 +19,7 @@ Configurations: C1..C5 (synth.CONFIGS) and the inputs with in-chunk locality
 C2r, C4n, RGG20 (synth.LOCALITY).
 
 Usage:  python -m chunkedgreedy_amd.sweep [--cfg C1,C2,C3,C4,C5] [--no-spmm]
-        [--algos row_split,merge_path] [--cg] [--candidates]
+        [--algos row_split,merge_path,plan] [--cg] [--candidates]
 """
 
 from __future__ import annotations
@@ -49,13 +49,20 @@ def spmm_bytes(n: int, nnz: int, N: int) -> int:
 
 
 def _spmm_ms(sporder, ctx, ptr, ind, val, B, algo, iters=20):
+    """Median launch time; algo "plan" times the planned SpMM, the plan made
+    beforehand and untimed (the harness's prepare step)."""
     import torch
 
+    plan = sporder.spmm_plan(ptr, ind, ctx=ctx) if algo == "plan" else None
+    kw = {"plan": plan} if plan is not None else {"algo": algo}
     out = torch.empty(B.shape, dtype=torch.float32, device=B.device)
     for _ in range(5):
-        sporder.spmm_csr(ptr, ind, val, B, out=out, algo=algo, ctx=ctx)
-    return statistics.median(
-        sporder.spmm_csr(ptr, ind, val, B, out=out, algo=algo, ctx=ctx)[1] for _ in range(iters))
+        sporder.spmm_csr(ptr, ind, val, B, out=out, ctx=ctx, **kw)
+    ms = statistics.median(
+        sporder.spmm_csr(ptr, ind, val, B, out=out, ctx=ctx, **kw)[1] for _ in range(iters))
+    if plan is not None:
+        plan.close()
+    return ms
 
 
 def measure(name: str, *, spmm=True, algos=("row_split",), repeats=3, cg=False) -> dict:
@@ -107,6 +114,13 @@ def measure(name: str, *, spmm=True, algos=("row_split",), repeats=3, cg=False) 
     rec["permute_ms"] = (time.perf_counter() - t1) * 1e3
 
     if spmm:
+        if "plan" in algos:
+            # Blocked tiles of each pattern's plan (tiles of 64 rows).
+            rec["plan"] = {}
+            for tag, (pp, ii) in (("orig", (ptr, ind)), ("reordered", (p2, i2))):
+                plan = sporder.spmm_plan(pp, ii, ctx=ctx)
+                rec["plan"][tag] = dict(plan.info)
+                plan.close()
         rec["spmm"] = {}
         for N in WIDTHS[name]:
             gen = torch.Generator(device=dev).manual_seed(42)
@@ -165,7 +179,7 @@ def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--cfg", default="C1,C2,C3,C4,C5")
     ap.add_argument("--no-spmm", action="store_true")
-    ap.add_argument("--algos", default="row_split,merge_path")
+    ap.add_argument("--algos", default="row_split,merge_path,plan")
     ap.add_argument("--repeats", type=int, default=3)
     ap.add_argument("--cg", action="store_true", help="also time sporder-cg once")
     ap.add_argument("--candidates", action="store_true",
