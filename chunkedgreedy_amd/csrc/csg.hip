@@ -194,38 +194,58 @@ constexpr int kGreedyCompactRows = 4096;
 
 // Walk modes of greedy_compact_kernel.
 constexpr int kWalkTable = 0, kWalkSingle = 1, kWalkAhead = 2;
+// Packed rows (no statistics): a slice of up to kPackedCap in-chunk entries
+// whose rows have at most kPackedMaxK table entries is held as 16-bit local
+// indices in preference order; the walk needs no weights.
+constexpr int32_t kPackedCap = 16384;
+constexpr int32_t kPackedMaxK = 32;
 // Compacted rows: the offsets array becomes row headers, the offset in the low
-// kOffBits bits (entries are at most 32 * kGreedyBlock) and the local index of
-// the row's first (preferred) entry above it (below kGreedyCompactRows).
-constexpr int kOffBits = 14;
+// kOffBits bits (at most 32 * kGreedyBlock entries, or kPackedCap packed ones)
+// and the local index of the row's first (preferred) entry above it (below
+// kGreedyCompactRows).
+constexpr int kOffBits = 15;
 constexpr int32_t kOffMask = (1 << kOffBits) - 1;
-static_assert(32 * kGreedyBlock <= kOffMask && kGreedyCompactRows <= 4096 &&
-                  kOffBits + 12 <= 31,
+static_assert(32 * kGreedyBlock <= kOffMask && kPackedCap <= kOffMask &&
+                  kGreedyCompactRows <= 4096 && kOffBits + 12 <= 31,
               "row header fields");
 
-// Dynamic LDS layout: entries u64[entry_cap] | offsets i32[rows_cap + 1] |
+// 64-bit words of the entries region: entry_cap staged entries, or packed_cap
+// 16-bit ones in the same bytes.
+__host__ __device__ inline int32_t greedy_entry_words(int32_t entry_cap, int32_t packed_cap) {
+  return entry_cap > (packed_cap + 3) / 4 ? entry_cap : (packed_cap + 3) / 4;
+}
+
+// Dynamic LDS layout: entries u64[greedy_entry_words] | offsets i32[rows_cap + 1] |
 // bitmap u32[ceil(rows_cap / 32)] | valid counts u8[rows_cap].  A staged entry is (weight bits << 32) |
 // (slice position << 12) | local index: positions are below 4096 * 256 = 2^20
 // and local indices below 4096.
-size_t greedy_compact_lds(int32_t rows_cap, int32_t entry_cap) {
-  return static_cast<size_t>(entry_cap) * 8u + static_cast<size_t>(rows_cap + 1) * 4u +
+size_t greedy_compact_lds(int32_t rows_cap, int32_t entry_cap, int32_t packed_cap = 0) {
+  return static_cast<size_t>(greedy_entry_words(entry_cap, packed_cap)) * 8u +
+         static_cast<size_t>(rows_cap + 1) * 4u +
          static_cast<size_t>((rows_cap + 31) / 32) * 4u + static_cast<size_t>(rows_cap);
 }
 
 // kStagePer: staged entries each thread moves to their rows (entry_cap is at
-// most kStagePer * kGreedyBlock).
+// most kStagePer * kGreedyBlock).  packed_cap: 16-bit entries the region holds
+// for the packed form (0 when statistics are collected or k > kPackedMaxK).
+// With band_hi > band_lo the chain is split over two launches by the slice's
+// valid entries S (the sketch's counts, row_valid): the launch with in_band
+// set takes the chunks with band_lo < S <= band_hi, the other the rest.
 template <int kStagePer>
 __global__ void __launch_bounds__(kGreedyBlock)
     greedy_compact_kernel(int32_t n, int32_t k, int32_t chunk_size,
                           const uint64_t *__restrict__ table, int32_t *__restrict__ order,
                           ChainCounters *counters, int32_t rows_cap, int32_t entry_cap,
+                          int32_t packed_cap, int32_t band_lo, int32_t band_hi, int32_t in_band,
                           const int32_t *__restrict__ row_valid) {
   extern __shared__ uint64_t smem_u64[];
   __shared__ int32_t s_total;
   __shared__ int32_t s_staged;
   __shared__ int32_t s_valid;
   uint64_t *s_ent = smem_u64;
-  int32_t *s_off = reinterpret_cast<int32_t *>(smem_u64 + entry_cap);
+  uint16_t *s_e16 = reinterpret_cast<uint16_t *>(smem_u64); // the packed form
+  int32_t *s_off =
+      reinterpret_cast<int32_t *>(smem_u64 + greedy_entry_words(entry_cap, packed_cap));
   uint32_t *s_bm = reinterpret_cast<uint32_t *>(s_off + rows_cap + 1);
   uint8_t *s_rv = reinterpret_cast<uint8_t *>(s_bm + (rows_cap + 31) / 32);
 
@@ -262,6 +282,10 @@ __global__ void __launch_bounds__(kGreedyBlock)
     if (lane == 0 && vsum != 0) atomicAdd(&s_valid, vsum);
   }
   __syncthreads();
+  if (band_hi > band_lo && row_valid != nullptr &&
+      (band_lo < s_valid && s_valid <= band_hi) != (in_band != 0)) {
+    return; // the other launch's chunk (uniform across the workgroup)
+  }
   // A slice with under a quarter of its entries valid is read row by row, only
   // each row's valid prefix (rows without entries cost no table traffic and a
   // thread waits on one load per row); a denser one is swept whole, coalesced.
@@ -361,6 +385,53 @@ __global__ void __launch_bounds__(kGreedyBlock)
   __syncthreads();
   const int32_t total = s_total;
   const bool compact = total <= entry_cap;
+  // Past the staging capacity, rows of at most kPackedMaxK entries are
+  // re-read from the slice (now in cache) and packed: each row's in-chunk
+  // entries in table order (weight descending), then each run of equal
+  // weight sorted by local index, which is the preference order.
+  const bool packed = !compact && total <= packed_cap;
+  if (packed) {
+    for (int32_t r = tid; r < size; r += kGreedyBlock) {
+      const int32_t a = s_off[r], b = s_off[r + 1];
+      if (b == a) continue;
+      const int32_t rv = row_valid != nullptr ? s_rv[r] : k;
+      const uint64_t *row = slice + static_cast<size_t>(r) * k;
+      uint32_t starts = 0u; // bit t: entry a + t begins a run of equal weight
+      uint32_t prev_w = 0u; // weights are positive: 0 matches none
+      int32_t o = a;
+      for (int32_t j = 0; j < rv && o < b; ++j) {
+        const uint64_t e = row[j];
+        const int32_t c = wi_index(e);
+        if (c < 0) break;
+        if (c >= start && c < end) {
+          const uint32_t wb = static_cast<uint32_t>(e >> 32);
+          if (wb != prev_w) starts |= 1u << (o - a);
+          prev_w = wb;
+          s_e16[o++] = static_cast<uint16_t>(c - start);
+        }
+      }
+      int32_t rs = a;
+      for (int32_t i = a + 1; i < b; ++i) {
+        if ((starts >> (i - a)) & 1u) {
+          rs = i;
+          continue;
+        }
+        const uint16_t x = s_e16[i];
+        int32_t j = i;
+        while (j > rs && s_e16[j - 1] > x) {
+          s_e16[j] = s_e16[j - 1];
+          --j;
+        }
+        s_e16[j] = x;
+      }
+    }
+    __syncthreads();
+    for (int32_t r = tid; r < size; r += kGreedyBlock) {
+      const int32_t a = s_off[r], b = s_off[r + 1] & kOffMask;
+      if (b > a) s_off[r] = a | (static_cast<int32_t>(s_e16[a]) << kOffBits);
+    }
+    __syncthreads();
+  }
   if (compact) {
     // Entry j of row r moves from its staging slot to s_off[r] + (its rank
     // among the row's in-chunk entries): j itself unless the row is flagged as
@@ -452,8 +523,9 @@ __global__ void __launch_bounds__(kGreedyBlock)
   //                lane-read path;
   //   kWalkAhead   compacted, rows of several entries: the next row's offsets
   //                are read during the visited test.
-  auto walk = [&](auto mode_tag) {
+  auto walk = [&](auto mode_tag, auto packed_tag) {
     constexpr int kMode = decltype(mode_tag)::value;
+    constexpr bool kPacked = decltype(packed_tag)::value; // 16-bit entries, no weights
     constexpr bool kSorted = kMode != kWalkTable; // rows compacted and sorted in LDS
     constexpr bool kSingle = kMode == kWalkSingle;
     constexpr bool kAhead = kMode == kWalkAhead;
@@ -497,7 +569,7 @@ __global__ void __launch_bounds__(kGreedyBlock)
           // visited (most rows that have any on scrambled inputs have one).
           if (first_free) {
             best_c = c0;
-            if (counters != nullptr) best_w = wi_weight(s_ent[d0]);
+            if (!kPacked && counters != nullptr) best_w = wi_weight(s_ent[d0]);
           }
         } else if (kSorted) {
           // The row's in-chunk entries in LDS, in preference order: the step
@@ -511,9 +583,13 @@ __global__ void __launch_bounds__(kGreedyBlock)
             int32_t cl = -1, o0 = 0, o1 = 0;
             float w = 0.0f;
             if (j < len) {
-              const uint64_t e = s_ent[d0 + j];
-              cl = static_cast<int32_t>(static_cast<uint32_t>(e));
-              w = wi_weight(e);
+              if constexpr (kPacked) {
+                cl = s_e16[d0 + j];
+              } else {
+                const uint64_t e = s_ent[d0 + j];
+                cl = static_cast<int32_t>(static_cast<uint32_t>(e));
+                w = wi_weight(e);
+              }
               if constexpr (kAhead) {
                 o0 = s_off[cl];
                 o1 = s_off[cl + 1];
@@ -641,12 +717,20 @@ __global__ void __launch_bounds__(kGreedyBlock)
       cur = nxt;
     }
   };
-  if (!compact) {
-    walk(std::integral_constant<int, kWalkTable>{});
+  using Words64 = std::false_type;
+  using Words16 = std::true_type;
+  if (!compact && !packed) {
+    walk(std::integral_constant<int, kWalkTable>{}, Words64{});
   } else if (2 * single_rows >= entry_rows) {
-    walk(std::integral_constant<int, kWalkSingle>{});
+    if (packed) {
+      walk(std::integral_constant<int, kWalkSingle>{}, Words16{});
+    } else {
+      walk(std::integral_constant<int, kWalkSingle>{}, Words64{});
+    }
+  } else if (packed) {
+    walk(std::integral_constant<int, kWalkAhead>{}, Words16{});
   } else {
-    walk(std::integral_constant<int, kWalkAhead>{});
+    walk(std::integral_constant<int, kWalkAhead>{}, Words64{});
   }
   if (counters != nullptr && lane == 0) {
     atomicAdd(&counters->restarts, restarts);
@@ -947,6 +1031,15 @@ SeriationOut seriate_pass(Context &ctx, int32_t n, int32_t nnz, const int32_t *d
   // table row, from the counts the sketch writes (held as bytes in LDS); a
   // launch of a few chunks is latency-bound and does not use them.
   const bool use_row_valid = compact && !wide && k <= 255;
+  // Packed walks (no statistics: the walk then needs no weights) hold up to
+  // kPackedCap entries in a region of 32 KiB at chain_chunk 1024, k 16, which
+  // would cost the other chunks occupancy: the chain is split over two
+  // launches by each slice's valid entries, the packed one taking the slices
+  // past the 64-bit staging capacity that it can hold.
+  const int32_t packed_cap =
+      (use_row_valid && !want_stats && k <= kPackedMaxK)
+          ? static_cast<int32_t>(std::min<int64_t>(static_cast<int64_t>(rows_max) * k, kPackedCap))
+          : 0;
   if (use_row_valid) need += ws_bytes<int32_t>(static_cast<size_t>(n));
   if (!compact && !bitmap_lds) need += ws_bytes<uint32_t>(static_cast<size_t>(num_chunks) * words);
   ctx.reserve(need);
@@ -977,16 +1070,33 @@ SeriationOut seriate_pass(Context &ctx, int32_t n, int32_t nnz, const int32_t *d
   if (compact) {
     const int32_t entry_cap = wide ? kWideCap : kNarrowCap;
     const dim3 grid(static_cast<unsigned>(num_chunks));
-    const size_t lds = greedy_compact_lds(rows_max, entry_cap);
     ChainCounters *cnt = want_stats ? counters : nullptr;
     if (wide) {
-      greedy_compact_kernel<32><<<grid, kGreedyBlock, lds, ctx.stream>>>(
-          n, k, chain_chunk, table, d_new_order, cnt, rows_max, entry_cap, row_valid);
+      greedy_compact_kernel<32><<<grid, kGreedyBlock, greedy_compact_lds(rows_max, entry_cap),
+                                  ctx.stream>>>(n, k, chain_chunk, table, d_new_order, cnt,
+                                                rows_max, entry_cap, 0, 0, 0, 0, row_valid);
+      SP_LAUNCH_CHECK();
     } else {
-      greedy_compact_kernel<8><<<grid, kGreedyBlock, lds, ctx.stream>>>(
-          n, k, chain_chunk, table, d_new_order, cnt, rows_max, entry_cap, row_valid);
+      // The packed launch runs on a side stream beside the narrow one (its
+      // workgroups need more LDS, so it is queued first); each takes its own
+      // chunks and skips the others' after summing their valid counts.
+      const bool split = packed_cap > entry_cap;
+      const int32_t band_hi = split ? packed_cap : 0;
+      if (split) {
+        fork_side(ctx, 0);
+        greedy_compact_kernel<8>
+            <<<grid, kGreedyBlock, greedy_compact_lds(rows_max, entry_cap, packed_cap),
+               ctx.side[0]>>>(n, k, chain_chunk, table, d_new_order, cnt, rows_max, entry_cap,
+                              packed_cap, entry_cap, band_hi, 1, row_valid);
+        SP_LAUNCH_CHECK();
+      }
+      greedy_compact_kernel<8><<<grid, kGreedyBlock, greedy_compact_lds(rows_max, entry_cap),
+                                 ctx.stream>>>(n, k, chain_chunk, table, d_new_order, cnt,
+                                               rows_max, entry_cap, 0, entry_cap, band_hi, 0,
+                                               row_valid);
+      SP_LAUNCH_CHECK();
+      if (split) join_side(ctx, 0);
     }
-    SP_LAUNCH_CHECK();
   } else {
     int64_t blocks = ceil_div64(num_chunks, general_wpb);
     size_t lds = bitmap_lds ? static_cast<size_t>(general_wpb) * words * 4u : 0;

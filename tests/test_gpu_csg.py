@@ -399,8 +399,11 @@ def in_chunk_totals(ptr, ind, k, chunk):
 @pytest.mark.parametrize("case", ["few_chunks", "many_chunks"])
 def test_greedy_staging_capacity(sporder, case):
     """Slices of 2049 to 8192 in-chunk entries: with at most two chunks per CU
-    the chain stages up to 8192 entries in LDS, with more chunks it stages
-    2048 and reads longer slices from global memory.  Same order either way."""
+    the chain stages up to 8192 entries in LDS; with more chunks it stages
+    2048 64-bit entries, and past that walks a packed slice (16-bit local
+    indices in preference order, runs of equal weight sorted by index) when
+    no statistics are asked for, or reads the rows from global memory when
+    they are.  Same order every way, and the same restart count."""
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     if case == "few_chunks":
         chunk, n, block = 1024, 8 * 1024, 6
@@ -411,10 +414,72 @@ def test_greedy_staging_capacity(sporder, case):
     tot = in_chunk_totals(ptr, ind, 16, chunk)
     assert tot.min() > 2048 and tot.max() <= 8192
     dptr, dind = dev_csr(ptr, ind)
+    o, os_ = oracle.chunk_similarity_greedy(ptr, ind, is_symmetric=True, k=16, oversampling=4.0,
+                                            chunk_size=chunk)
+    g = sporder.chunk_similarity_greedy(dptr, dind, is_symmetric=True, k=16, oversampling=4.0,
+                                        chunk_size=chunk)
+    assert np.array_equal(g.cpu().numpy(), o)
+    g2, s = sporder.chunk_similarity_greedy(dptr, dind, is_symmetric=True, k=16,
+                                            oversampling=4.0, chunk_size=chunk, with_stats=True)
+    assert np.array_equal(g2.cpu().numpy(), o)
+    assert s["chain_restarts"] == os_["chain_restarts"]
+
+
+def two_halves(n, seed):
+    """A dense block-local half (slices past 2048 in-chunk entries at
+    chunk 256, k 16) above a sparse one (slices well under it)."""
+    h = n // 2
+    p1, i1 = block_random(h, 32, 5, seed)
+    p2, i2 = block_random(n - h, 4, 1, seed + 1)
+    ptr = np.concatenate([p1, p2[1:] + p1[-1]]).astype(np.int32)
+    ind = np.concatenate([i1, i2 + h]).astype(np.int32)
+    return ptr, ind
+
+
+def test_greedy_split_launches(sporder):
+    """Chunks on both sides of the packed band in one call: the chain's two
+    launches (packed slices, and the rest) each take exactly their own chunks
+    (by the slice's valid-entry sum) and skip the others'."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    chunk = 256
+    n = chunk * (2 * cus + 40)
+    ptr, ind = two_halves(n, 53)
+    tot = in_chunk_totals(ptr, ind, 16, chunk)
+    print(f"[split] n={n} slices {tot.min()}..{tot.max()}", flush=True)
+    assert (tot <= 2048).sum() > 100 and (tot > 2048).sum() > 100
+    dptr, dind = dev_csr(ptr, ind)
     g = sporder.chunk_similarity_greedy(dptr, dind, is_symmetric=True, k=16, oversampling=4.0,
                                         chunk_size=chunk)
     o, _ = oracle.chunk_similarity_greedy(ptr, ind, is_symmetric=True, k=16, oversampling=4.0,
                                           chunk_size=chunk)
+    assert np.array_equal(g.cpu().numpy(), o)
+
+
+@pytest.mark.parametrize("k", [16, 32])
+def test_greedy_packed_slices(sporder, k):
+    """Many chunks whose slices pass the 2048-entry staging capacity, on
+    patterns with many equal weights (block-local random rows: rows of one
+    block share columns, and degrees repeat): the packed walk (no
+    statistics) must order each run of equal weight by local index.  Also
+    sporder-cg, whose global table mixes out-of-chunk entries into the rows
+    (filtered when the slice is packed).  Bit-exact against the oracle."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    chunk = 256
+    n = chunk * (2 * cus + 40)
+    ptr, ind = block_random(n, 32, 5, 52)
+    tot = in_chunk_totals(ptr, ind, k, chunk)
+    print(f"[packed] n={n} k={k} in-chunk entries per slice {tot.min()}..{tot.max()}", flush=True)
+    assert tot.min() > 2048
+    dptr, dind = dev_csr(ptr, ind)
+    g = sporder.chunk_similarity_greedy(dptr, dind, is_symmetric=True, k=k, oversampling=2.0,
+                                        chunk_size=chunk)
+    o, _ = oracle.chunk_similarity_greedy(ptr, ind, is_symmetric=True, k=k, oversampling=2.0,
+                                          chunk_size=chunk)
+    assert np.array_equal(g.cpu().numpy(), o)
+    g = sporder.chunk_greedy(dptr, dind, is_symmetric=True, k=k, oversampling=2.0,
+                             chunk_size=chunk)
+    o, _ = oracle.chunk_greedy(ptr, ind, is_symmetric=True, k=k, oversampling=2.0,
+                               chunk_size=chunk)
     assert np.array_equal(g.cpu().numpy(), o)
 
 
