@@ -35,7 +35,7 @@
 namespace {
 
 constexpr int W = 64;
-constexpr int kOffBits = 14;
+constexpr int kOffBits = 15;
 constexpr int32_t kOffMask = (1 << kOffBits) - 1;
 constexpr int kSortedRow = 64;      // variant 10: rows longer than this stay unsorted
 constexpr int16_t kUnsortedRow = -2;
