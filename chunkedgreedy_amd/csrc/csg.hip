@@ -1077,25 +1077,25 @@ SeriationOut seriate_pass(Context &ctx, int32_t n, int32_t nnz, const int32_t *d
                                                 rows_max, entry_cap, 0, 0, 0, 0, row_valid);
       SP_LAUNCH_CHECK();
     } else {
-      // The packed launch runs on a side stream beside the narrow one (its
-      // workgroups need more LDS, so it is queued first); each takes its own
-      // chunks and skips the others' after summing their valid counts.
+      // The packed launch follows the narrow one; each takes its own chunks
+      // and skips the others' after summing their valid counts.  (Run beside
+      // each other on two streams, the pair was 0.25-0.35 ms faster on C3 and
+      // C5, whose chunks fall on both sides, but as much slower on C4n, whose
+      // chunks are all packed, and the fork cost every call about 15 us.)
       const bool split = packed_cap > entry_cap;
       const int32_t band_hi = split ? packed_cap : 0;
-      if (split) {
-        fork_side(ctx, 0);
-        greedy_compact_kernel<8>
-            <<<grid, kGreedyBlock, greedy_compact_lds(rows_max, entry_cap, packed_cap),
-               ctx.side[0]>>>(n, k, chain_chunk, table, d_new_order, cnt, rows_max, entry_cap,
-                              packed_cap, entry_cap, band_hi, 1, row_valid);
-        SP_LAUNCH_CHECK();
-      }
       greedy_compact_kernel<8><<<grid, kGreedyBlock, greedy_compact_lds(rows_max, entry_cap),
                                  ctx.stream>>>(n, k, chain_chunk, table, d_new_order, cnt,
                                                rows_max, entry_cap, 0, entry_cap, band_hi, 0,
                                                row_valid);
       SP_LAUNCH_CHECK();
-      if (split) join_side(ctx, 0);
+      if (split) {
+        greedy_compact_kernel<8>
+            <<<grid, kGreedyBlock, greedy_compact_lds(rows_max, entry_cap, packed_cap),
+               ctx.stream>>>(n, k, chain_chunk, table, d_new_order, cnt, rows_max, entry_cap,
+                             packed_cap, entry_cap, band_hi, 1, row_valid);
+        SP_LAUNCH_CHECK();
+      }
     }
   } else {
     int64_t blocks = ceil_div64(num_chunks, general_wpb);
