@@ -1077,23 +1077,28 @@ SeriationOut seriate_pass(Context &ctx, int32_t n, int32_t nnz, const int32_t *d
                                                 rows_max, entry_cap, 0, 0, 0, 0, row_valid);
       SP_LAUNCH_CHECK();
     } else {
-      // The packed launch follows the narrow one; each takes its own chunks
-      // and skips the others' after summing their valid counts.  (Run beside
-      // each other on two streams, the pair was 0.25-0.35 ms faster on C3 and
-      // C5, whose chunks fall on both sides, but as much slower on C4n, whose
+      // The narrow launch packs slices up to what its own entry region holds
+      // as 16-bit entries (4 * entry_cap); the packed launch, with the larger
+      // region, follows it and takes the slices between that and packed_cap.
+      // Each launch skips the other's chunks after summing their valid
+      // counts.  (Run beside each other on two streams, the pair was faster
+      // on inputs whose chunks fall on both sides but slower on those whose
       // chunks are all packed, and the fork cost every call about 15 us.)
-      const bool split = packed_cap > entry_cap;
+      const int32_t narrow_packed = std::min(packed_cap, 4 * entry_cap);
+      const bool split = packed_cap > narrow_packed;
+      const int32_t band_lo = std::max(entry_cap, narrow_packed);
       const int32_t band_hi = split ? packed_cap : 0;
-      greedy_compact_kernel<8><<<grid, kGreedyBlock, greedy_compact_lds(rows_max, entry_cap),
+      greedy_compact_kernel<8><<<grid, kGreedyBlock,
+                                 greedy_compact_lds(rows_max, entry_cap, narrow_packed),
                                  ctx.stream>>>(n, k, chain_chunk, table, d_new_order, cnt,
-                                               rows_max, entry_cap, 0, entry_cap, band_hi, 0,
-                                               row_valid);
+                                               rows_max, entry_cap, narrow_packed, band_lo,
+                                               band_hi, 0, row_valid);
       SP_LAUNCH_CHECK();
       if (split) {
         greedy_compact_kernel<8>
             <<<grid, kGreedyBlock, greedy_compact_lds(rows_max, entry_cap, packed_cap),
                ctx.stream>>>(n, k, chain_chunk, table, d_new_order, cnt, rows_max, entry_cap,
-                             packed_cap, entry_cap, band_hi, 1, row_valid);
+                             packed_cap, band_lo, band_hi, 1, row_valid);
         SP_LAUNCH_CHECK();
       }
     }

@@ -425,32 +425,40 @@ def test_greedy_staging_capacity(sporder, case):
     assert s["chain_restarts"] == os_["chain_restarts"]
 
 
-def two_halves(n, seed):
-    """A dense block-local half (slices past 2048 in-chunk entries at
-    chunk 256, k 16) above a sparse one (slices well under it)."""
-    h = n // 2
-    p1, i1 = block_random(h, 32, 5, seed)
-    p2, i2 = block_random(n - h, 4, 1, seed + 1)
-    ptr = np.concatenate([p1, p2[1:] + p1[-1]]).astype(np.int32)
-    ind = np.concatenate([i1, i2 + h]).astype(np.int32)
-    return ptr, ind
+def block_parts(n, seed, specs):
+    """Equal row ranges of block-local random patterns, (block, degree) each,
+    stacked on the diagonal: slices of very different density in one matrix."""
+    sizes = [n // len(specs)] * len(specs)
+    sizes[-1] = n - sum(sizes[:-1])
+    ptr, inds, nnz, off = [np.zeros(1, np.int64)], [], 0, 0
+    for (block, deg), h in zip(specs, sizes):
+        p, i = block_random(h, block, deg, seed)
+        seed += 1
+        ptr.append(p[1:].astype(np.int64) + nnz)
+        inds.append(i.astype(np.int64) + off)
+        nnz += int(p[-1])
+        off += h
+    return np.concatenate(ptr).astype(np.int32), np.concatenate(inds).astype(np.int32)
 
 
 def test_greedy_split_launches(sporder):
-    """Chunks on both sides of the packed band in one call: the chain's two
-    launches (packed slices, and the rest) each take exactly their own chunks
-    (by the slice's valid-entry sum) and skip the others'."""
+    """One call whose 1024-row slices hold S valid entries in every range the
+    chain tells apart (k 24): S <= 2048 (64-bit staging), 2048 < S <= 8192
+    (packed within the first launch's LDS), 8192 < S <= 16384 (the second,
+    packed launch) and S > 16384 (rows read from the table).  Each launch takes
+    exactly its own chunks and skips the other's."""
     cus = torch.cuda.get_device_properties(0).multi_processor_count
-    chunk = 256
+    chunk, k = 1024, 24
     n = chunk * (2 * cus + 40)
-    ptr, ind = two_halves(n, 53)
-    tot = in_chunk_totals(ptr, ind, 16, chunk)
+    ptr, ind = block_parts(n, 60, [(64, 12), (16, 3), (12, 2), (4, 1)])
+    tot = in_chunk_totals(ptr, ind, k, chunk)
     print(f"[split] n={n} slices {tot.min()}..{tot.max()}", flush=True)
-    assert (tot <= 2048).sum() > 100 and (tot > 2048).sum() > 100
+    for lo, hi in ((0, 2048), (2048, 8192), (8192, 16384), (16384, 1 << 30)):
+        assert ((tot > lo) & (tot <= hi)).sum() > 50, (lo, hi)
     dptr, dind = dev_csr(ptr, ind)
-    g = sporder.chunk_similarity_greedy(dptr, dind, is_symmetric=True, k=16, oversampling=4.0,
+    g = sporder.chunk_similarity_greedy(dptr, dind, is_symmetric=True, k=k, oversampling=4.0,
                                         chunk_size=chunk)
-    o, _ = oracle.chunk_similarity_greedy(ptr, ind, is_symmetric=True, k=16, oversampling=4.0,
+    o, _ = oracle.chunk_similarity_greedy(ptr, ind, is_symmetric=True, k=k, oversampling=4.0,
                                           chunk_size=chunk)
     assert np.array_equal(g.cpu().numpy(), o)
 
