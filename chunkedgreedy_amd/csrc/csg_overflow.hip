@@ -208,7 +208,7 @@ __device__ __forceinline__ void feed_batch(WaveSketch<CELLS> &store, int2 pr, in
                                            int lane) {
   const bool item = f0 + lane < total && pr.x != row;
   const float alpha = 2.0f / static_cast<float>(deg + pr.y);
-  store.template feed<true>(ballot(item), pr.x, alpha);
+  store.feed(ballot(item), pr.x, alpha);
 }
 
 // One block of 64 runs through the sketch, item batches two at a time with

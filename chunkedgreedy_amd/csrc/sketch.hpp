@@ -90,17 +90,12 @@ template <int CELLS> struct WaveSketch {
   // Every slot write below is a select whose per-lane condition is a wave
   // mask (inverse ballot): the hit masks from the key compares, and for a
   // miss the one-hot mask of the slot's lane, so the slot written costs two
-  // selects per cell and no lane compare.
-  //
-  // HIT_FIRST adds a hit's weight before testing for a miss: one branch per
-  // hit, for a wave whose single long stream is the critical path (one row's
-  // items are a dependent chain, and every taken branch lengthens it).
-  // Without it the adds run only on hits, behind a branch: fewer vector
-  // instructions per miss, for kernels where many waves share a SIMD and
-  // issue slots, not one chain, set the time.
-  template <bool HIT_FIRST = false>
+  // selects per cell and no lane compare.  A hit's weight is added only after
+  // the hit test, behind a branch: fewer vector instructions per miss, for
+  // kernels where many waves share a SIMD and issue slots, not one chain, set
+  // the time (the chunk tiers).
   __device__ __forceinline__ void add(int32_t k, float w) {
-    if (hit_update<HIT_FIRST>(k, w)) return;
+    if (hit_update<false>(k, w)) return;
     // A miss writes (k, wn) into one slot: the lane of the one-hot mask
     // sel[j] in local cell j.
     uint64_t sel[LC];
@@ -151,7 +146,10 @@ template <int CELLS> struct WaveSketch {
   // afterwards every miss evicts, so neither loop tests the capacity per
   // item; and an eviction looks for the tied minimum only in the first cell
   // that holds the minimum (ties go to the smallest cell index, then lane).
-  template <bool HIT_FIRST = false>
+  // A hit's weight is added before the miss test: one taken branch per hit,
+  // for a wave whose single long stream is the critical path (one row's items
+  // are a dependent chain, and every taken branch lengthens it: the global
+  // path's hub rows).
   __device__ __forceinline__ void feed(uint64_t mask, int32_t other, float alpha) {
     const int lane = lane_id();
     while (mask != 0 && filled < M) {
@@ -159,7 +157,7 @@ template <int CELLS> struct WaveSketch {
       mask &= mask - 1;
       const int32_t k = readlane(other, i);
       const float w = readlane_f(alpha, i);
-      if (hit_update<HIT_FIRST>(k, w)) continue;
+      if (hit_update<true>(k, w)) continue;
       const uint32_t f = static_cast<uint32_t>(filled);
       const uint32_t L = f / CELLS, c = f - L * CELLS;
       const uint64_t bit = 1ull << (L + 32u * (c & 1u));
@@ -176,7 +174,7 @@ template <int CELLS> struct WaveSketch {
       mask &= mask - 1;
       const int32_t k = readlane(other, i);
       const float w = readlane_f(alpha, i);
-      if (hit_update<HIT_FIRST>(k, w)) continue;
+      if (hit_update<true>(k, w)) continue;
       uint32_t lmin = 0xFFFFFFFFu;
 #pragma unroll
       for (int j = 0; j < LC; ++j) {
@@ -200,7 +198,9 @@ template <int CELLS> struct WaveSketch {
     }
   }
 
-  // The hit test of add(): true (and the weight added) when k is held.
+  // The hit test: true (and the weight added) when k is held.  HIT_FIRST adds
+  // the weight with selects before the result is known (feed), otherwise
+  // behind the branch on it (add).
   template <bool HIT_FIRST>
   __device__ __forceinline__ bool hit_update(int32_t k, float w) {
     uint64_t hit[LC];
