@@ -297,20 +297,23 @@ __device__ __forceinline__ uint32_t dpp_u32(uint32_t v, uint32_t ident) {
 // (permlane16_swap exchanges rows 0<->1 and 2<->3, permlane32_swap the two
 // halves; of the pair returned for (v, v), element 0 holds the partner value
 // in the upper row / half and element 1 in the lower).  j is a compile-time
-// constant after unrolling at every call site.
+// constant after unrolling at every call site.  The controls for 1, 2 and 8
+// write every lane from a lane of the same row, so their moves need no prior
+// value (mov_dpp: no copy of v into the destination first); for 4 the first
+// move's unwritten banks are written by the second.
 __device__ __forceinline__ uint32_t lane_xor_u32(uint32_t v, int j) {
   const int x = static_cast<int>(v);
   switch (j) {
   case 1:
-    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(x, x, 0xB1, 0xf, 0xf, false));
+    return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(x, 0xB1, 0xf, 0xf, false));
   case 2:
-    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(x, x, 0x4E, 0xf, 0xf, false));
+    return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(x, 0x4E, 0xf, 0xf, false));
   case 4: {
-    const int t = __builtin_amdgcn_update_dpp(x, x, 0x104, 0xf, 0x5, false);
+    const int t = __builtin_amdgcn_mov_dpp(x, 0x104, 0xf, 0x5, false);
     return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(t, x, 0x114, 0xf, 0xA, false));
   }
   case 8:
-    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(x, x, 0x128, 0xf, 0xf, false));
+    return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(x, 0x128, 0xf, 0xf, false));
   case 16: {
     const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
     return (__lane_id() & 16) ? r[0] : r[1];

@@ -13,7 +13,9 @@
 //     weight bits, then ballots in tie order; the new key inherits the evicted
 //     weight;
 //   - output merges the per-logical-lane selection-sorted lists, largest head
-//     weight first (DPP maximum), ties to the smaller logical lane.
+//     weight first (DPP maximum), ties to the smaller logical lane; with at
+//     most two cells per logical lane that order is (weight descending, slot
+//     ascending), produced by one bitonic sort over the wave.
 #pragma once
 
 #include "common.hpp"
@@ -60,6 +62,41 @@ __device__ __forceinline__ int32_t mask_select(uint64_t mask, int32_t a, int32_t
   int32_t r;
   asm("v_cndmask_b32_e64 %0, %2, %1, %3" : "=v"(r) : "v"(a), "v"(b), "s"(m));
   return r;
+}
+
+// Lanes that keep the smaller key of their pair in step (kk, j) of an
+// ascending bitonic sort over the wave (partner lane ^ j): the lower lane of
+// a pair in an ascending block ((lane & kk) == 0), the upper lane in a
+// descending one.  For kk = 64 every block ascends.
+constexpr uint64_t bitonic_keep_min(int kk, int j) {
+  uint64_t m = 0;
+  for (int l = 0; l < 64; ++l) {
+    if (((l & j) != 0) == ((l & kk) != 0)) m |= 1ull << l;
+  }
+  return m;
+}
+
+// Step (KK, J) of that sort on one 64-bit key per lane, held as (hi, lo).  A
+// lane takes its partner's key when the partner is larger and the lane keeps
+// the maximum, or is not larger and the lane keeps the minimum (taking an
+// equal key changes nothing): one compare and the step's constant mask.
+template <int KK, int J>
+__device__ __forceinline__ void bitonic_step64(uint32_t &hi, uint32_t &lo) {
+  const uint32_t ph = lane_xor_u32(hi, J), pl = lane_xor_u32(lo, J);
+  const uint64_t mine = (static_cast<uint64_t>(hi) << 32) | lo;
+  const uint64_t other = (static_cast<uint64_t>(ph) << 32) | pl;
+  constexpr uint64_t kKeepMin = bitonic_keep_min(KK, J);
+  const uint64_t take = ballot(other > mine) ^ kKeepMin;
+  hi = static_cast<uint32_t>(mask_select(take, static_cast<int32_t>(ph), static_cast<int32_t>(hi)));
+  lo = static_cast<uint32_t>(mask_select(take, static_cast<int32_t>(pl), static_cast<int32_t>(lo)));
+}
+
+// Merge stage KK of the sort: steps J = KK/2, ..., 1.  After the stages up to
+// KK, every aligned block of KK lanes is sorted, the first one ascending.
+template <int KK, int J = KK / 2>
+__device__ __forceinline__ void bitonic_stage64(uint32_t &hi, uint32_t &lo) {
+  bitonic_step64<KK, J>(hi, lo);
+  if constexpr (J > 1) bitonic_stage64<KK, J / 2>(hi, lo);
 }
 
 // Space-saving sketch of capacity 32*CELLS spread over one wave64.
@@ -226,6 +263,10 @@ template <int CELLS> struct WaveSketch {
   // largest head weight (ties -> smaller lane; exhausted lanes show 0.0f).
   // Writes all k entries of `out` (unused ones as the zero entry).
   __device__ __forceinline__ void select_top_k(int32_t k, uint64_t *out) {
+    if constexpr (CELLS <= 2) {
+      select_top_k_sorted(k, out);
+      return;
+    }
     const int lane = lane_id();
     // Gather logical lane L's cells into physical lane L (< 32).
     int32_t fk[CELLS];
@@ -311,6 +352,62 @@ template <int CELLS> struct WaveSketch {
       const int32_t idx = r * 64 + lane;
       if (idx < k) out[idx] = outv[r];
     }
+  }
+
+  // select_top_k for CELLS <= 2 (one cell per physical lane).  The merge
+  // emits the live slots in (weight descending, slot ascending) order: a
+  // logical lane's cells leave the selection sort in (weight descending, cell
+  // ascending) order, as it swaps on a strictly larger weight only, and the
+  // merge takes equal head weights from the smaller logical lane first, so
+  // equal weights come out by (L, c), that is by slot s = L*CELLS + c.  One
+  // bitonic network over the wave sorts the keys (~weight bits, s) ascending
+  // and lane i writes output entry i: a fixed number of steps per row instead
+  // of a wave maximum per emitted entry.
+  __device__ __forceinline__ void select_top_k_sorted(int32_t k, uint64_t *out) {
+    static_assert(CELLS <= 2, "one cell per physical lane");
+    const int lane = lane_id();
+    // Slot `lane` into this lane: CELLS == 2 keeps slot s in physical lane
+    // (s >> 1) + 32*(s & 1); CELLS == 1 keeps it in lane s < 32.
+    int32_t sk = key[0];
+    float sw = wt[0];
+    if constexpr (CELLS == 2) {
+      const int src = (lane >> 1) | ((lane & 1) << 5);
+      sk = __shfl(sk, src, kWave);
+      sw = __shfl(sw, src, kWave);
+    } else {
+      if (lane >= 32) sk = -1;
+    }
+    const bool live = sk != -1;
+    const uint64_t lm = ballot(live);
+    const int n_live = __popcll(lm);
+    // Empty slots sort last.  Live slots are a prefix (slots fill in order and
+    // never empty again), so after the stages up to the first block size that
+    // covers the highest live slot, lanes [0, n_live) hold the live keys in
+    // order; the later stages would only move the empty ones.
+    uint32_t hi = live ? ~__float_as_uint(sw) : 0xFFFFFFFFu;
+    uint32_t lo = live ? static_cast<uint32_t>(lane) : 0xFFFFFFFFu;
+    const int span = lm ? 64 - __builtin_clzll(lm) : 0;
+    if (span > 1) {
+      bitonic_stage64<2>(hi, lo);
+      if (span > 2) {
+        bitonic_stage64<4>(hi, lo);
+        if (span > 4) {
+          bitonic_stage64<8>(hi, lo);
+          if (span > 8) {
+            bitonic_stage64<16>(hi, lo);
+            if (span > 16) {
+              bitonic_stage64<32>(hi, lo);
+              if constexpr (CELLS == 2) {
+                if (span > 32) bitonic_stage64<64>(hi, lo);
+              }
+            }
+          }
+        }
+      }
+    }
+    const int32_t idx = __shfl(sk, static_cast<int>(lo & 63u), kWave);
+    const uint64_t v = lane < n_live ? pack_wi(idx, __uint_as_float(~hi)) : 0ull;
+    if (lane < k) out[lane] = v;
   }
 };
 
