@@ -13,9 +13,10 @@
 //     weight bits, then ballots in tie order; the new key inherits the evicted
 //     weight;
 //   - output merges the per-logical-lane selection-sorted lists, largest head
-//     weight first (DPP maximum), ties to the smaller logical lane; with at
-//     most two cells per logical lane that order is (weight descending, slot
-//     ascending), produced by one bitonic sort over the wave.
+//     weight first (DPP maximum), ties to the smaller logical lane.  That
+//     order is (weight descending, logical lane, list position); for at most
+//     four cells per logical lane it is produced by one bitonic sort of
+//     (weight, position) keys over one or two registers of the wave.
 #pragma once
 
 #include "common.hpp"
@@ -64,39 +65,98 @@ __device__ __forceinline__ int32_t mask_select(uint64_t mask, int32_t a, int32_t
   return r;
 }
 
-// Lanes that keep the smaller key of their pair in step (kk, j) of an
-// ascending bitonic sort over the wave (partner lane ^ j): the lower lane of
-// a pair in an ascending block ((lane & kk) == 0), the upper lane in a
-// descending one.  For kk = 64 every block ascends.
-constexpr uint64_t bitonic_keep_min(int kk, int j) {
+// Bitonic sort of 64-bit keys held as (hi, lo) pairs, one per lane and
+// register: element x = 64*q + lane sits in register q.  Step (kk, j) pairs x
+// with x ^ j; the smaller key goes to the lower x of a pair in an ascending
+// block ((x & kk) == 0) and to the upper x in a descending one.
+//
+// Lanes of register q (base = 64*q) that keep the smaller key in step (kk, j)
+// for j < 64, where the partner is lane ^ j of the same register.
+constexpr uint64_t bitonic_keep_min(int kk, int j, int base) {
   uint64_t m = 0;
   for (int l = 0; l < 64; ++l) {
-    if (((l & j) != 0) == ((l & kk) != 0)) m |= 1ull << l;
+    if (((l & j) != 0) == (((base + l) & kk) != 0)) m |= 1ull << l;
   }
   return m;
 }
 
-// Step (KK, J) of that sort on one 64-bit key per lane, held as (hi, lo).  A
-// lane takes its partner's key when the partner is larger and the lane keeps
-// the maximum, or is not larger and the lane keeps the minimum (taking an
-// equal key changes nothing): one compare and the step's constant mask.
-template <int KK, int J>
+// Step (KK, J < 64) on the register of base BASE.  A lane takes its
+// partner's key when the partner is larger and the lane keeps the maximum,
+// or is not larger and the lane keeps the minimum (taking an equal key
+// changes nothing): one compare and the step's constant mask.
+template <int KK, int J, int BASE>
 __device__ __forceinline__ void bitonic_step64(uint32_t &hi, uint32_t &lo) {
   const uint32_t ph = lane_xor_u32(hi, J), pl = lane_xor_u32(lo, J);
   const uint64_t mine = (static_cast<uint64_t>(hi) << 32) | lo;
   const uint64_t other = (static_cast<uint64_t>(ph) << 32) | pl;
-  constexpr uint64_t kKeepMin = bitonic_keep_min(KK, J);
+  constexpr uint64_t kKeepMin = bitonic_keep_min(KK, J, BASE);
   const uint64_t take = ballot(other > mine) ^ kKeepMin;
   hi = static_cast<uint32_t>(mask_select(take, static_cast<int32_t>(ph), static_cast<int32_t>(hi)));
   lo = static_cast<uint32_t>(mask_select(take, static_cast<int32_t>(pl), static_cast<int32_t>(lo)));
 }
 
-// Merge stage KK of the sort: steps J = KK/2, ..., 1.  After the stages up to
-// KK, every aligned block of KK lanes is sorted, the first one ascending.
-template <int KK, int J = KK / 2>
-__device__ __forceinline__ void bitonic_stage64(uint32_t &hi, uint32_t &lo) {
-  bitonic_step64<KK, J>(hi, lo);
-  if constexpr (J > 1) bitonic_stage64<KK, J / 2>(hi, lo);
+// Steps J = J0, J0/2, ..., 1 (all below 64) of stage KK on one register.
+template <int KK, int J0, int BASE>
+__device__ __forceinline__ void bitonic_steps64(uint32_t &hi, uint32_t &lo) {
+  bitonic_step64<KK, J0, BASE>(hi, lo);
+  if constexpr (J0 > 1) bitonic_steps64<KK, J0 / 2, BASE>(hi, lo);
+}
+
+// Ascending sort of the first `span` elements of one register, whose lanes
+// at or past `span` hold the largest key: the stages run up to the first
+// block size that covers span (blocks of every stage up to kk are sorted,
+// the first one ascending), so lanes [0, span) end in order.  span is
+// wave-uniform; MAXKK (32 or 64) is the largest stage the caller needs.
+template <int MAXKK>
+__device__ __forceinline__ void bitonic_sort_prefix64(uint32_t &hi, uint32_t &lo, int span) {
+  if (span > 1) {
+    bitonic_steps64<2, 1, 0>(hi, lo);
+    if (span > 2) {
+      bitonic_steps64<4, 2, 0>(hi, lo);
+      if (span > 4) {
+        bitonic_steps64<8, 4, 0>(hi, lo);
+        if (span > 8) {
+          bitonic_steps64<16, 8, 0>(hi, lo);
+          if (span > 16) {
+            bitonic_steps64<32, 16, 0>(hi, lo);
+            if constexpr (MAXKK > 32) {
+              if (span > 32) bitonic_steps64<64, 32, 0>(hi, lo);
+            }
+          }
+        }
+      }
+    }
+  }
+}
+
+// Ascending sort of all 128 elements of two registers.
+__device__ __forceinline__ void bitonic_sort128(uint32_t (&hi)[2], uint32_t (&lo)[2]) {
+  bitonic_steps64<2, 1, 0>(hi[0], lo[0]);
+  bitonic_steps64<2, 1, 64>(hi[1], lo[1]);
+  bitonic_steps64<4, 2, 0>(hi[0], lo[0]);
+  bitonic_steps64<4, 2, 64>(hi[1], lo[1]);
+  bitonic_steps64<8, 4, 0>(hi[0], lo[0]);
+  bitonic_steps64<8, 4, 64>(hi[1], lo[1]);
+  bitonic_steps64<16, 8, 0>(hi[0], lo[0]);
+  bitonic_steps64<16, 8, 64>(hi[1], lo[1]);
+  bitonic_steps64<32, 16, 0>(hi[0], lo[0]);
+  bitonic_steps64<32, 16, 64>(hi[1], lo[1]);
+  bitonic_steps64<64, 32, 0>(hi[0], lo[0]);  // ascending block
+  bitonic_steps64<64, 32, 64>(hi[1], lo[1]); // descending block
+  // Stage 128, j = 64: the partners share a lane; register 0 keeps the
+  // smaller key.
+  {
+    const uint64_t a = (static_cast<uint64_t>(hi[0]) << 32) | lo[0];
+    const uint64_t b = (static_cast<uint64_t>(hi[1]) << 32) | lo[1];
+    const bool swap = a > b;
+    const uint32_t h0 = hi[0], l0 = lo[0];
+    hi[0] = swap ? hi[1] : hi[0];
+    lo[0] = swap ? lo[1] : lo[0];
+    hi[1] = swap ? h0 : hi[1];
+    lo[1] = swap ? l0 : lo[1];
+  }
+  bitonic_steps64<128, 32, 0>(hi[0], lo[0]);
+  bitonic_steps64<128, 32, 64>(hi[1], lo[1]);
 }
 
 // Space-saving sketch of capacity 32*CELLS spread over one wave64.
@@ -311,6 +371,10 @@ template <int CELLS> struct WaveSketch {
         }
       }
     }
+    if constexpr (CELLS >= 3 && CELLS <= 4) {
+      emit_sorted_lists(k, out, fk, fw);
+      return;
+    }
     // k-way merge; lane (i & 63) keeps output entry i in register i >> 6.
     // The row has k <= M = 32 * CELLS <= 64 * LC entries (m = (int)(k * ovs)
     // >= k for ovs >= 1, and M rounds m up), so LC registers per lane hold the
@@ -354,6 +418,67 @@ template <int CELLS> struct WaveSketch {
     }
   }
 
+  // The merge of select_top_k for 3 <= CELLS <= 4, from the selection-sorted
+  // lists fk/fw of logical lane L (held by physical lane L < 32).  The merge
+  // emits every entry of weight above w before any of weight w (each list
+  // descends), and among equal weights drains the smallest logical lane's
+  // run first, in list order: output order is (weight descending, L, list
+  // position pos).  Entry e = L*CELLS + pos is placed at element x = e of two
+  // registers (x = 64*q + lane) with the key (~weight bits, e); live entries
+  // are a prefix of e (slots fill logical lane by logical lane, and the sort
+  // keeps a lane's live cells first), so rows of at most 64 live entries sort
+  // register 0 alone, up to the block that covers them.  Element i of the
+  // sorted keys is output entry i.
+  __device__ __forceinline__ void emit_sorted_lists(int32_t k, uint64_t *out,
+                                                    const int32_t (&fk)[CELLS],
+                                                    const float (&fw)[CELLS]) {
+    static_assert(CELLS >= 3 && CELLS <= 4, "two registers of 64 elements");
+    const int lane = lane_id();
+    int32_t sk[2];
+    uint32_t hi[2], lo[2];
+    uint64_t lm[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      // Element x = 64q + lane holds e = x: list entry pos of logical lane L.
+      const int e = 64 * q + lane;
+      const int L = e / CELLS, pos = e - L * CELLS;
+      const int src = L & 31;
+      int32_t kx = -1;
+      float wx = 0.0f;
+#pragma unroll
+      for (int p = 0; p < CELLS; ++p) {
+        const int32_t kp = __shfl(fk[p], src, kWave);
+        const float wp = __shfl(fw[p], src, kWave);
+        if (pos == p) {
+          kx = kp;
+          wx = wp;
+        }
+      }
+      if (L >= 32) kx = -1; // past M = 32*CELLS (CELLS == 3)
+      const bool live = kx != -1;
+      sk[q] = kx;
+      lm[q] = ballot(live);
+      hi[q] = live ? ~__float_as_uint(wx) : 0xFFFFFFFFu;
+      lo[q] = live ? static_cast<uint32_t>(e) : 0xFFFFFFFFu;
+    }
+    const int n_live = __popcll(lm[0]) + __popcll(lm[1]);
+    if (lm[1] != 0) {
+      bitonic_sort128(hi, lo);
+    } else {
+      bitonic_sort_prefix64<64>(hi[0], lo[0], lm[0] ? 64 - __builtin_clzll(lm[0]) : 0);
+    }
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int i = 64 * q + lane;
+      const int e = static_cast<int>(lo[q] & 127u);
+      const int32_t k0 = __shfl(sk[0], e & 63, kWave);
+      const int32_t k1 = __shfl(sk[1], e & 63, kWave);
+      const int32_t idx = e < 64 ? k0 : k1;
+      const uint64_t v = i < n_live ? pack_wi(idx, __uint_as_float(~hi[q])) : 0ull;
+      if (i < k) out[i] = v;
+    }
+  }
+
   // select_top_k for CELLS <= 2 (one cell per physical lane).  The merge
   // emits the live slots in (weight descending, slot ascending) order: a
   // logical lane's cells leave the selection sort in (weight descending, cell
@@ -387,24 +512,7 @@ template <int CELLS> struct WaveSketch {
     uint32_t hi = live ? ~__float_as_uint(sw) : 0xFFFFFFFFu;
     uint32_t lo = live ? static_cast<uint32_t>(lane) : 0xFFFFFFFFu;
     const int span = lm ? 64 - __builtin_clzll(lm) : 0;
-    if (span > 1) {
-      bitonic_stage64<2>(hi, lo);
-      if (span > 2) {
-        bitonic_stage64<4>(hi, lo);
-        if (span > 4) {
-          bitonic_stage64<8>(hi, lo);
-          if (span > 8) {
-            bitonic_stage64<16>(hi, lo);
-            if (span > 16) {
-              bitonic_stage64<32>(hi, lo);
-              if constexpr (CELLS == 2) {
-                if (span > 32) bitonic_stage64<64>(hi, lo);
-              }
-            }
-          }
-        }
-      }
-    }
+    bitonic_sort_prefix64<(CELLS == 2 ? 64 : 32)>(hi, lo, span);
     const int32_t idx = __shfl(sk, static_cast<int>(lo & 63u), kWave);
     const uint64_t v = lane < n_live ? pack_wi(idx, __uint_as_float(~hi)) : 0ull;
     if (lane < k) out[lane] = v;
