@@ -269,6 +269,21 @@ __device__ __forceinline__ int64_t xcd_block() {
 
 __device__ __forceinline__ uint64_t ballot(bool p) { return __ballot(p); }
 
+// A wave-uniform mask with bit i (wave-uniform) cleared: one s_bitset0,
+// where mask &= mask - 1 takes a 64-bit subtract and an and.  readfirstlane
+// states the uniformity to the compiler, which drops it where it already
+// holds both in scalar registers.
+__device__ __forceinline__ uint64_t clear_bit(uint64_t mask, int i) {
+  uint64_t m =
+      static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int32_t>(mask))) |
+      (static_cast<uint64_t>(static_cast<uint32_t>(
+           __builtin_amdgcn_readfirstlane(static_cast<int32_t>(mask >> 32))))
+       << 32);
+  const int32_t b = __builtin_amdgcn_readfirstlane(i);
+  asm("s_bitset0_b64 %0, %1" : "+s"(m) : "s"(b));
+  return m;
+}
+
 __device__ __forceinline__ int32_t readlane(int32_t v, int lane) {
   return __builtin_amdgcn_readlane(v, lane);
 }

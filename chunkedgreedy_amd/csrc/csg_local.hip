@@ -386,7 +386,7 @@ __global__ void __launch_bounds__(kLocalThreads, (local_min_waves<CELLS, KEYCAP>
           while (mask) {
             const int i = __builtin_ctzll(mask);
             store.add(readlane(other, i), readlane_f(alpha, i));
-            mask &= mask - 1;
+            mask = clear_bit(mask, i);
           }
         }
       }
