@@ -45,6 +45,8 @@ constexpr int kLocalThreads = 1024;
 constexpr int kLocalWaves = kLocalThreads / kWave;
 // Buckets up to this size are sorted by one thread.
 constexpr int kSmallBucket = 48;
+// Column loads in flight per thread in the bucket count.
+constexpr int kCountLoads = 8;
 // Row classes of step 3b: clz(row size) in [0, 31] for rows with candidates,
 // kClasses for the others.
 constexpr int kClasses = 32;
@@ -194,8 +196,19 @@ __global__ void __launch_bounds__(kLocalThreads, (local_min_waves<CELLS, KEYCAP>
       if (row_valid != nullptr) row_valid[cs + r] = 0;
     }
     __syncthreads();
-    for (int32_t i = tid; i < E; i += kLocalThreads) {
-      atomicAdd(&s_bend[bucket_of(static_cast<uint32_t>(col_ind[e0 + i]), nbl)], 1);
+    // kCountLoads coalesced column loads in flight per thread before their
+    // atomics (one load at a time waited out the memory latency per key).
+    for (int32_t i0 = tid; i0 < E; i0 += kCountLoads * kLocalThreads) {
+      uint32_t c[kCountLoads];
+#pragma unroll
+      for (int u = 0; u < kCountLoads; ++u) {
+        const int32_t i = i0 + u * kLocalThreads;
+        c[u] = i < E ? static_cast<uint32_t>(col_ind[e0 + i]) : 0u;
+      }
+#pragma unroll
+      for (int u = 0; u < kCountLoads; ++u) {
+        if (i0 + u * kLocalThreads < E) atomicAdd(&s_bend[bucket_of(c[u], nbl)], 1);
+      }
     }
     __syncthreads();
     // Exclusive scan of the counts: s_bend[b] = start of bucket b.  Up to 16
@@ -225,17 +238,40 @@ __global__ void __launch_bounds__(kLocalThreads, (local_min_waves<CELLS, KEYCAP>
     }
     __syncthreads();
     // 2a. Scatter: one thread per row writes its keys; the bucket cursor
-    //     moves s_bend[b] from the start to the end of bucket b.
+    //     moves s_bend[b] from the start to the end of bucket b.  A thread
+    //     reads its row in 16-byte groups (the aligned groups that cover the
+    //     row, read whole only inside the chunk's nonzeros; a group at the
+    //     chunk's edge is read element by element): the lanes of a wave read
+    //     different rows, so each load instruction touches a line per lane,
+    //     and a group's four columns cost one such access.
     unsigned long long msum = 0; // this thread's rows' mirror-check terms, when asked
+    const bool vec_ok = (reinterpret_cast<uintptr_t>(col_ind) & 15u) == 0;
     for (int32_t r = tid; r < rows; r += kLocalThreads) {
       const int32_t rb = row_ptr[cs + r];
-      const int32_t len = s_size[r];
-#pragma unroll 4
-      for (int32_t q = 0; q < len; ++q) {
-        const uint32_t c = static_cast<uint32_t>(col_ind[rb + q]);
-        const int32_t slot = atomicAdd(&s_bend[bucket_of(c, nbl)], 1);
-        s_keys[slot] = (c << lb) | static_cast<uint32_t>(r);
-        if (mirror != nullptr) msum += mirror_term(cs + r, static_cast<int32_t>(c));
+      const int32_t re = rb + s_size[r];
+      for (int32_t q = vec_ok ? (rb & ~3) : rb; q < re; q += vec_ok ? 4 : 1) {
+        int32_t v[4];
+        if (vec_ok && q >= e0 && q + 4 <= e0 + E) {
+          const int4 g = *reinterpret_cast<const int4 *>(col_ind + q);
+          v[0] = g.x;
+          v[1] = g.y;
+          v[2] = g.z;
+          v[3] = g.w;
+        } else {
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            v[u] = (q + u >= rb && q + u < re && (vec_ok || u == 0)) ? col_ind[q + u] : 0;
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          if (q + u >= rb && q + u < re && (vec_ok || u == 0)) {
+            const uint32_t c = static_cast<uint32_t>(v[u]);
+            const int32_t slot = atomicAdd(&s_bend[bucket_of(c, nbl)], 1);
+            s_keys[slot] = (c << lb) | static_cast<uint32_t>(r);
+            if (mirror != nullptr) msum += mirror_term(cs + r, static_cast<int32_t>(c));
+          }
+        }
       }
     }
     if (mirror != nullptr) {
