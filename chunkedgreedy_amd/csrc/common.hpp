@@ -221,14 +221,15 @@ void chunk_sketch_top_k(Context &ctx, int32_t n, int32_t nnz, int32_t k, int32_t
 // chunk_local_classify fills d_lists (2*num_chunks int32) and d_counts (2
 // int32): the chunks of LDS tier 2 in d_lists[0 .. d_counts[0]) and the chunks
 // too large for LDS in d_lists[num_chunks .. num_chunks + d_counts[1]), the
-// latter for chunk_sketch_top_k over the global CSC.  chunk_local_sketch_top_k
+// latter for chunk_sketch_top_k over the global CSC (with is_symmetric, the
+// largest chunks that tier 2 could hold go there as well, to run beside it).  chunk_local_sketch_top_k
 // then writes the rows of tier-1 chunks (tiers & 1; chunk_size <= 1024) and of
 // the listed tier-2 chunks (tiers & 2); the two launches are independent and
 // may run on different streams.  d_row_valid as for chunk_sketch_top_k.
 constexpr int kLocalRowCap = 4096;
 bool chunk_local_supported(int32_t n, int32_t chunk_size);
 void chunk_local_classify(Context &ctx, int32_t n, int32_t chunk_size, const int32_t *d_ptr,
-                          int32_t *d_lists, int32_t *d_counts);
+                          int32_t *d_lists, int32_t *d_counts, bool is_symmetric);
 void chunk_local_sketch_top_k(Context &ctx, int32_t n, int32_t k, int32_t chunk_size,
                               int32_t m_capacity, const int32_t *d_ptr, const int32_t *d_ind,
                               uint64_t *d_table, const int32_t *d_lists,

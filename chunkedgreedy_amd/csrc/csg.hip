@@ -950,7 +950,7 @@ void build_table(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
   // transpose of a non-symmetric matrix is built only when the global path
   // has chunks.
   t_sim->begin(ctx.stream);
-  chunk_local_classify(ctx, n, chunk_size, d_ptr, lists, counts);
+  chunk_local_classify(ctx, n, chunk_size, d_ptr, lists, counts, is_symmetric);
   int32_t *h_counts = ctx.host_words;
   SP_HIP(hipMemcpyAsync(h_counts, counts, 2 * sizeof(int32_t), hipMemcpyDeviceToHost,
                         ctx.stream));

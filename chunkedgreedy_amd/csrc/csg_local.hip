@@ -439,6 +439,14 @@ __global__ void __launch_bounds__(kLocalThreads, (local_min_waves<CELLS, KEYCAP>
 // Tier parameters: (key capacity, row capacity, log2 buckets).
 constexpr int kT1Keys = 16384, kT1Rows = 1024, kT1Nb = 11;
 constexpr int kT2Keys = 32768, kT2Rows = 4096, kT2Nb = 10;
+// On a symmetric matrix the global path reads the CSR as its CSC (no
+// transpose), and its waves, with little LDS, run on the CUs beside tier 2's
+// one workgroup per CU: tier 2 then takes chunks of at most this many
+// nonzeros and the larger ones go to the global path, which adds waves to
+// the SIMDs that tier 2 leaves at four.  Measured on C5 (Chung-Lu, most
+// chunks tier 2): csg 37.3-38.2 ms with the split at 32768, 33.1 at 26624,
+// 33.7-34.4 at 28672, 34.4 at 24576, 42.0 at 20480; C3 unchanged.
+constexpr int kT2SharedKeys = 26624;
 
 constexpr int kClassifyThreads = 1024;
 // Up to this many chunks one workgroup classifies and orders the lists,
@@ -447,11 +455,12 @@ constexpr int kClassifyPer = 8;
 constexpr int kClassifyOrderCap = kClassifyThreads * kClassifyPer;
 
 // Tier of a chunk of `rows` rows and E nonzeros: 1 and 2 are the LDS tiers
-// (1 only when t1 is set), 3 the global-CSC path.  The same tests as the
-// tier kernels' own.
-__device__ __forceinline__ int chunk_tier(int32_t E, int32_t rows, bool t1) {
+// (1 only when t1 is set), 3 the global-CSC path.  The tier-1 test and the
+// capacities are the tier kernels' own; t2_keys (at most kT2Keys) is where
+// tier 2 hands chunks to the global path.
+__device__ __forceinline__ int chunk_tier(int32_t E, int32_t rows, bool t1, int32_t t2_keys) {
   if (t1 && E <= kT1Keys && rows <= kT1Rows) return 1;
-  if (E <= kT2Keys && rows <= kT2Rows) return 2;
+  if (E <= t2_keys && rows <= kT2Rows) return 2;
   return 3;
 }
 
@@ -463,7 +472,7 @@ __device__ __forceinline__ int chunk_tier(int32_t E, int32_t rows, bool t1) {
 // (more than kClassifyOrderCap chunks) the lists are unordered and counts
 // must be zero on entry.  The table does not depend on list order.
 __global__ void __launch_bounds__(kClassifyThreads)
-    classify_chunks_kernel(int32_t n, int32_t chunk_size, int t1,
+    classify_chunks_kernel(int32_t n, int32_t chunk_size, int t1, int32_t t2_keys,
                            const int32_t *__restrict__ row_ptr, int32_t *__restrict__ lists,
                            int32_t *__restrict__ counts) {
   __shared__ int32_t s_cls[2][kClasses + 1];
@@ -473,7 +482,7 @@ __global__ void __launch_bounds__(kClassifyThreads)
     const int64_t cs = q * chunk_size;
     const int64_t ce = cs + chunk_size < n ? cs + chunk_size : n;
     *E = row_ptr[ce] - row_ptr[cs];
-    return chunk_tier(*E, static_cast<int32_t>(ce - cs), t1 != 0);
+    return chunk_tier(*E, static_cast<int32_t>(ce - cs), t1 != 0, t2_keys);
   };
   if (gridDim.x > 1) {
     for (int64_t q0 = static_cast<int64_t>(blockIdx.x) * kClassifyThreads; q0 < chunks;
@@ -574,7 +583,7 @@ bool chunk_local_supported(int32_t n, int32_t chunk_size) {
 }
 
 void chunk_local_classify(Context &ctx, int32_t n, int32_t chunk_size, const int32_t *d_ptr,
-                          int32_t *d_lists, int32_t *d_counts) {
+                          int32_t *d_lists, int32_t *d_counts, bool is_symmetric) {
   SP_EXPECT(chunk_local_supported(n, chunk_size), "chunk-local sketch not applicable");
   const int64_t chunks = ceil_div64(n, chunk_size);
   const int t1 = chunk_size <= kT1Rows ? 1 : 0;
@@ -583,8 +592,9 @@ void chunk_local_classify(Context &ctx, int32_t n, int32_t chunk_size, const int
     grid = ctx.grid_for(ceil_div64(chunks, kClassifyThreads), kClassifyThreads, 1);
     fill_u32(ctx, d_counts, 2, 0u);
   }
-  classify_chunks_kernel<<<grid, kClassifyThreads, 0, ctx.stream>>>(n, chunk_size, t1, d_ptr,
-                                                                    d_lists, d_counts);
+  const int32_t t2_keys = is_symmetric ? kT2SharedKeys : kT2Keys;
+  classify_chunks_kernel<<<grid, kClassifyThreads, 0, ctx.stream>>>(n, chunk_size, t1, t2_keys,
+                                                                    d_ptr, d_lists, d_counts);
   SP_LAUNCH_CHECK();
 }
 
