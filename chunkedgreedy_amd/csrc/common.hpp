@@ -164,9 +164,11 @@ constexpr int kSpmmTileRows = 64;
 
 // Row-split SpMM in the stated order over the listed tiles (every row when
 // `tiles` is null), long rows in segments; reserves the context workspace.
+// long_rows false: the caller knows that no row passes SPORDER_SPMM_LONG_ROW
+// nonzeros, and the long-row workspace and launches are left out.
 void spmm_rowsplit_tiles(Context &ctx, int32_t n, int32_t nnz, const int32_t *ptr,
                          const int32_t *ind, const float *val, int32_t N, const float *B,
-                         float *C, const int32_t *tiles, int64_t ntiles);
+                         float *C, const int32_t *tiles, int64_t ntiles, bool long_rows = true);
 
 // In-place exclusive (inclusive=false) or inclusive scan of `count` int32
 // values; `tmp` must hold scan_tmp_elems(count) int32.

@@ -207,7 +207,7 @@ __global__ void __launch_bounds__(kSpmmBlock)
   // A claimed row longer than kLongRow goes to the segment launch and counts
   // as finished at once.
   auto take_long = [&]() {
-    if (row >= 0 && e - p > kLongRow) {
+    if (longs != nullptr && row >= 0 && e - p > kLongRow) {
       if (gl == 0) register_row(ctl, longs, owner, static_cast<int32_t>(r0 + row), e - p);
       is_long = true;
       p = e;
@@ -665,7 +665,10 @@ void launch_rowsplit_g(Context &ctx, int32_t n, int32_t nnz, const int32_t *ptr,
                        float *C, const SpmmLongWs &w, int64_t seg_cap, int64_t long_cap,
                        const int32_t *tiles, int64_t ntiles) {
   constexpr int rpw = kWave / G;
-  fill_u32(ctx, w.ctl, sizeof(LongCtl) / 4, 0u);
+  // Without a long-row workspace (a plan found no row past kLongRow) the row
+  // launch computes every row and the segment launches are not made.
+  const bool long_rows = w.ctl != nullptr;
+  if (long_rows) fill_u32(ctx, w.ctl, sizeof(LongCtl) / 4, 0u);
   // Narrow widths (G <= 8 lanes per row, 8+ rows per wave) lose most to
   // row-length imbalance inside a wave: claim rows dynamically there.  With
   // wider rows the fixed assignment keeps more waves in flight.  With a tile
@@ -682,6 +685,7 @@ void launch_rowsplit_g(Context &ctx, int32_t n, int32_t nnz, const int32_t *ptr,
         n, ptr, ind, val, N, B, C, w.ctl, w.longs, w.owner, tiles, ntiles);
   }
   SP_LAUNCH_CHECK();
+  if (!long_rows) return;
   // Persistent grid over the registered segment units (none: exits at once).
   const int g = ctx.grid_for(ceil_div64(seg_cap, rpw * kSpmmWaves), kSpmmBlock, 2);
   spmm_long_segments<G><<<g, kSpmmBlock, 0, ctx.stream>>>(ptr, ind, val, N, B, w.ctl,
@@ -744,9 +748,12 @@ void spmm_rowsplit(Context &ctx, int32_t n, int32_t nnz, const int32_t *ptr,
 
 void spmm_rowsplit_tiles(Context &ctx, int32_t n, int32_t nnz, const int32_t *ptr,
                          const int32_t *ind, const float *val, int32_t N, const float *B,
-                         float *C, const int32_t *tiles, int64_t ntiles) {
-  ctx.reserve(spmm_ws_bytes(nnz, N));
-  const SpmmLongWs w = take_long_ws(ctx, nnz, N);
+                         float *C, const int32_t *tiles, int64_t ntiles, bool long_rows) {
+  SpmmLongWs w{nullptr, nullptr, nullptr, nullptr};
+  if (long_rows) {
+    ctx.reserve(spmm_ws_bytes(nnz, N));
+    w = take_long_ws(ctx, nnz, N);
+  }
   spmm_rowsplit(ctx, n, nnz, ptr, ind, val, N, B, C, w, -1, -1, tiles, ntiles);
 }
 

@@ -305,6 +305,7 @@ struct sporder_spmm_plan_struct {
   int32_t *blocked = nullptr; // blocked tiles
   int32_t *direct = nullptr;  // the other tiles
   int32_t n_blocked = 0, n_direct = 0;
+  bool long_rows = true; // some row passes SPORDER_SPMM_LONG_ROW nonzeros
   sporder_spmm_plan_info_t info{};
 };
 
@@ -373,6 +374,8 @@ sporder_spmm_plan_t sporder_spmm_plan_create(sporder_context_t h, int32_t n, int
     in.blocked_nnz += hp[r1] - hp[r0];
   }
   in.blocked_tiles = static_cast<int32_t>(blocked.size());
+  pl->long_rows = false;
+  for (int32_t r = 0; r < n && !pl->long_rows; ++r) pl->long_rows = hp[r + 1] - hp[r] > kLongRowPlan;
   in.entries = off[blocks];
   pl->entries = dev_alloc<int2>(static_cast<size_t>(off[blocks]));
   SP_HIP(hipMemcpyAsync(pl->boff, off.data(), off.size() * 4, hipMemcpyHostToDevice, ctx.stream));
@@ -431,7 +434,8 @@ void sporder_spmm_csr_plan(sporder_context_t h, sporder_spmm_plan_t plan, int32_
   const int vec = cols % 256 == 0 ? 4 : (cols % 128 == 0 ? 2 : (cols % 64 == 0 ? 1 : 0));
   t.begin(ctx.stream);
   if (!aligned || vec == 0 || plan->n_blocked == 0) {
-    spmm_rowsplit_tiles(ctx, n, nnz, d_ptr, d_ind, d_val, cols, d_b, d_c, nullptr, 0);
+    spmm_rowsplit_tiles(ctx, n, nnz, d_ptr, d_ind, d_val, cols, d_b, d_c, nullptr, 0,
+                        plan->long_rows);
   } else {
     if (vec == 4) {
       launch_blocks<4>(ctx, *plan, d_ptr, d_val, cols, d_b, d_c);
@@ -442,7 +446,7 @@ void sporder_spmm_csr_plan(sporder_context_t h, sporder_spmm_plan_t plan, int32_
     }
     if (plan->n_direct > 0) {
       spmm_rowsplit_tiles(ctx, n, nnz, d_ptr, d_ind, d_val, cols, d_b, d_c, plan->direct,
-                          plan->n_direct);
+                          plan->n_direct, plan->long_rows);
     }
   }
   t.end(ctx.stream);
