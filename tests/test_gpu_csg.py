@@ -321,6 +321,32 @@ def test_overflow_chunks_take_global_path(sporder, symmetric, chunk):
     assert np.array_equal(g.cpu().numpy(), o)
 
 
+def test_tier2_split_symmetric(sporder):
+    """On a symmetric pattern tier 2 keeps chunks of at most 26,624 nonzeros
+    and the larger ones, up to its 32,768 capacity, go to the global path,
+    which runs beside it; chunks on both sides of the split (no tier-1 chunk
+    here) give the oracle's table and permutation bit for bit."""
+    n, chunk = 6144, 1024
+    degs = [10, 13, 16, 12, 17, 9]
+    rng = np.random.default_rng(43)
+    rows = np.concatenate([np.repeat(np.arange(q * chunk, (q + 1) * chunk), d)
+                           for q, d in enumerate(degs)])
+    cols = rng.integers(0, n, size=rows.size)
+    rows, cols = np.concatenate([rows, cols]), np.concatenate([cols, rows])
+    keys = np.unique(rows.astype(np.int64) * n + cols)
+    r, c = keys // n, keys % n
+    ptr = np.zeros(n + 1, np.int64)
+    np.cumsum(np.bincount(r, minlength=n), out=ptr[1:])
+    ptr, ind = ptr.astype(np.int32), c.astype(np.int32)
+    E = ptr[chunk::chunk] - ptr[:-1:chunk]
+    assert ((E > 16384) & (E <= 26624)).any() and ((E > 26624) & (E <= 32768)).any()
+    check_table(sporder, ptr, ind, 16, 4.0, chunk, True)
+    dptr, dind = dev_csr(ptr, ind)
+    g = sporder.chunk_similarity_greedy(dptr, dind, is_symmetric=True, chunk_size=chunk)
+    o, _ = oracle.chunk_similarity_greedy(ptr, ind, is_symmetric=True, chunk_size=chunk)
+    assert np.array_equal(g.cpu().numpy(), o)
+
+
 def hub_matrix(n, deg, hubs, seed, symmetric):
     """Random rows of `deg` columns plus hub rows {row: nonzeros}."""
     rng = np.random.default_rng(seed)
