@@ -7,7 +7,9 @@ resident in HBM before timing starts.
 
 One step = csg reorder (sporder.chunk_similarity_greedy) + symmetric
 permutation apply with values (sporder.reorder) + CSR SpMM at N=128 on the
-reordered matrix.  W untimed steps, then K timed steps between
+reordered matrix, without a plan (a new reordering has none; a plan is the
+harness's untimed prepare step and is used for the per-launch SpMM figures
+below).  W untimed steps, then K timed steps between
 torch.cuda.synchronize() calls -> ms_per_step.
 
 Reported beside it (same run):
@@ -19,6 +21,9 @@ Reported beside it (same run):
     original and the reordered matrix at N = 32 and 128, as algorithmic GB/s
     with B_spmm(N) = 4(n+1) + 8 nnz + 8 n N bytes;
   - value = reordered SpMM GB/s at N = 128;
+  - hbm_ceiling: this library's own read, write and copy kernels over 1 GiB
+    (sporder_hbm_stream, ordinary and non-temporal), the rate streaming code
+    reaches on the device;
   - roofline of the dominant kernel (largest share of the step) against
     8 TB/s, and cpu_baseline: the oracle (C++/OpenMP restatement of csg and a
     CSR SpMM in the same fmaf order) on the host cores.
@@ -235,17 +240,17 @@ def main():
     ctx = sporder.Context()
     out128 = torch.empty((n, 128), dtype=torch.float32, device=dev)
 
-    def step(plan=None):
+    def step():
         """csg reorder, P A P^T with values, SpMM at N=128 on the reordered
-        matrix (through `plan` when given: the SpMM harness builds it in its
-        untimed prepare step)."""
+        matrix (row-split, no plan: the step makes a new pattern)."""
         order = sporder.chunk_similarity_greedy(ptr, ind, is_symmetric=is_sym, ctx=ctx)
         p2, i2, v2 = sporder.reorder(ptr, ind, order, val=val, symmetric=True, ctx=ctx)
-        sporder.spmm_csr(p2, i2, v2, B128, out=out128, ctx=ctx, plan=plan)
+        sporder.spmm_csr(p2, i2, v2, B128, out=out128, ctx=ctx)
         return order, (p2, i2, v2)
 
     # The reordered pattern (the same each step: csg is deterministic) and its
-    # SpMM plan, built once outside the timed region.
+    # SpMM plan for the per-launch figures, built once outside the timed
+    # region (the harness's prepare step).
     order, (p2, i2, v2) = step()
     t_plan = time.perf_counter()
     plan = sporder.spmm_plan(p2, i2, ctx=ctx)
@@ -260,11 +265,11 @@ def main():
         return
 
     for _ in range(args.warmup):
-        step(plan)
+        step()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        order, reordered = step(plan)
+        order, reordered = step()
     torch.cuda.synchronize()
     ms_per_step = (time.perf_counter() - t0) * 1e3 / max(args.steps, 1)
     log(f"step {ms_per_step:.3f} ms")
@@ -347,6 +352,12 @@ def main():
     log(f"spmm ceiling {ceiling}")
     band = band_demo(sporder, torch, dev, ctx, args.spmm_iters)
     copy_gbs = copy_rate(torch, dev)
+    from chunkedgreedy_amd.hbm import hbm_ceiling
+
+    ceiling_hbm = hbm_ceiling(1 << 30, 10, ctx=ctx)
+    log(f"hbm ceiling (own kernels, 1 GiB) {ceiling_hbm}")
+    best_read = max(ceiling_hbm["read"]["gbs"], ceiling_hbm["read"]["gbs_nt"])
+    band["frac_of_read_ceiling"] = round(band["blocked_gbs"] / best_read, 4)
 
     k_used = stats["k_used"]
     # Dominant kernel of the step: compare the stage spans with the SpMM.
@@ -388,7 +399,7 @@ def main():
         oracle.set_num_threads(threads)
         log(f"cpu baseline on {threads} threads ({model}; {usable} usable of {ncpu})")
         cpu_reorder = []
-        for _ in range(3):
+        for _ in range(5):
             t1 = time.perf_counter()
             o_order, _ = oracle.chunk_similarity_greedy(ptr_h, ind_h, is_symmetric=is_sym)
             cpu_reorder.append((time.perf_counter() - t1) * 1e3)
@@ -399,7 +410,7 @@ def main():
         apply_parity = bool(np.array_equal(op, p2h) and np.array_equal(oi, i2h)
                             and np.array_equal(ov.view(np.uint32), v2h.view(np.uint32)))
         cpu_spmm = []
-        for _ in range(3):
+        for _ in range(5):
             t1 = time.perf_counter()
             c_ref = oracle.spmm_csr(p2h, i2h, v2h, B_h)
             cpu_spmm.append((time.perf_counter() - t1) * 1e3)
@@ -415,8 +426,8 @@ def main():
         log(f"cpu parity: permutation {parity}, apply {apply_parity}, spmm {spmm_parity}")
         cpu = {"value": round(spmm_bytes(n, nnz, 128) / (cs * 1e-3) / 1e9, 2), "unit": "GB/s",
                "cores": threads, "kind": "port",
-               "sample": "full C2: oracle CSR SpMM N=128 on the reordered matrix (median of 3)"
-                         "; csg reorder by the oracle on full C2 (median of 3)",
+               "sample": "full C2: oracle CSR SpMM N=128 on the reordered matrix (median of 5)"
+                         "; csg reorder by the oracle on full C2 (median of 5)",
                "cpu_model": model, "cpu_count": ncpu, "cpus_usable": usable,
                "reorder_ms": round(statistics.median(cpu_reorder), 2),
                "spmm_ms": round(cs, 2), "permutation_bit_exact_vs_gpu": parity,
@@ -452,6 +463,7 @@ def main():
         "spmm_plan_c2": {"info": plan.info, "plan_ms": round(plan_ms, 2)},
         "spmm_block_band": band,
         "hbm_copy_gbs": copy_gbs,
+        "hbm_ceiling": ceiling_hbm,
         "cpu_baseline": cpu,
     }
     band.pop("_check", None)

@@ -103,6 +103,9 @@ SPMM_ROW_SPLIT = 1
 SPMM_MERGE_PATH = 2
 SPMM_NOALLOC_SCRATCH_BYTES = 64 << 20  # SPORDER_SPMM_NOALLOC_SCRATCH_BYTES
 SPMM_NOALLOC_TOO_LARGE = 1             # SPORDER_SPMM_NOALLOC_TOO_LARGE
+STREAM_READ = 0                        # sporder_stream_op_t
+STREAM_WRITE = 1
+STREAM_COPY = 2
 
 # Every symbol include/sporder.h declares, with its ctypes signature.
 SIGNATURES = {
@@ -128,6 +131,7 @@ SIGNATURES = {
     "sporder_spmm_plan_create": ([vp, i32, i32, vp, vp, P(SpmmPlanInfo)], vp),
     "sporder_spmm_plan_destroy": ([vp], None),
     "sporder_spmm_csr_plan": ([vp, vp, i32, i32, vp, vp, vp, i32, vp, vp, P(f32)], None),
+    "sporder_hbm_stream": ([vp, i32, i32, vp, vp, ctypes.c_int64, i32, P(f32)], None),
 }
 
 _lib = None

@@ -844,6 +844,10 @@ static __device__ __align__(256) unsigned char scratch[kNoAllocBytes];
 constexpr int kMaxDevices = 64;
 std::mutex noalloc_mu;
 void *noalloc_ptr[kMaxDevices] = {};
+// Held by a no-allocation call from its first use of the device's array to
+// its final synchronize, so that calls of this process on one device run one
+// after another (other processes hold arrays of their own).
+std::mutex noalloc_call_mu[kMaxDevices];
 
 // Rows past kLongRow nonzeros and their segments: ctl->rows, ctl->segments
 // (zeroed by the caller).  Grid-stride, one lane per row.
@@ -908,6 +912,7 @@ int32_t sporder_spmm_csr_noalloc(sporder_context_t h, int32_t n, int32_t nnz,
   SP_EXPECT(cols >= 1, "cols must be >= 1");
   Context &ctx = h->impl;
   char *base = static_cast<char *>(noalloc_scratch(ctx.device));
+  std::lock_guard<std::mutex> call_lock(noalloc_call_mu[ctx.device]);
   const bool aligned = (cols % 4 == 0) && (reinterpret_cast<uintptr_t>(d_b) % 16 == 0) &&
                        (reinterpret_cast<uintptr_t>(d_c) % 16 == 0);
   if (!aligned) {

@@ -19,9 +19,9 @@
 // Inspector (spmm_plan_tiles, one workgroup per tile of kSpmmTileRows rows,
 // run twice: count, then write): each block's (column, row) keys are sorted
 // in LDS; runs of equal columns are entries.  A tile is blocked when its
-// entries are at most half its nonzeros and no row has more than
-// SPORDER_SPMM_LONG_ROW nonzeros (those keep their segment launches); other
-// tiles run the row-split over a tile list.
+// entries are at most half its nonzeros, no row has more than
+// SPORDER_SPMM_LONG_ROW nonzeros (those keep their segment launches) and no
+// row holds a column twice; other tiles run the row-split over a tile list.
 //
 // Kernel (spmm_block_kernel, one wave per block): the lanes hold 64 entries
 // at a time; each lane gathers the CSR values of its own entry (for row j,
@@ -71,7 +71,8 @@ __device__ void block_bitonic(uint64_t *keys, int m2) {
 // the entries (column, row mask) of each blocked tile's blocks at boff[block].
 // Each block's (column << 3 | row) keys are sorted in LDS (a block holds at
 // most 8 rows of at most SPORDER_SPMM_LONG_ROW nonzeros); a run of equal
-// columns is one entry.
+// columns is one entry.  A tile in which a row holds a column twice is not
+// blocked (one mask bit cannot stand for two values).
 __global__ void __launch_bounds__(kPlanBlock)
     spmm_plan_tiles(int32_t n, const int32_t *__restrict__ ptr, const int32_t *__restrict__ ind,
                     bool write, int32_t *__restrict__ kind, int32_t *__restrict__ ecount,
@@ -81,6 +82,7 @@ __global__ void __launch_bounds__(kPlanBlock)
   __shared__ int32_t s_cnt[kTileBlocks];
   __shared__ int32_t s_scan[kPlanBlock / kWave];
   __shared__ int32_t s_long;
+  __shared__ int32_t s_dup; // some row repeats a column inside the tile
   static_assert(kBlockRows * kLongRowPlan <= kPlanKeys, "a block's keys fit the sort");
   const int64_t tile = blockIdx.x;
   if (write && kind[tile] == 0) return;
@@ -89,7 +91,10 @@ __global__ void __launch_bounds__(kPlanBlock)
   const int tid = threadIdx.x, lane = lane_id(), wave = tid / kWave;
   if (tid <= r1 - r0) s_ptr[tid] = ptr[r0 + tid];
   if (tid < kTileBlocks) s_cnt[tid] = 0;
-  if (tid == 0) s_long = 0;
+  if (tid == 0) {
+    s_long = 0;
+    s_dup = 0;
+  }
   __syncthreads();
   if (tid < r1 - r0 && s_ptr[tid + 1] - s_ptr[tid] > kLongRowPlan) atomicOr(&s_long, 1);
   __syncthreads();
@@ -121,7 +126,15 @@ __global__ void __launch_bounds__(kPlanBlock)
     const int per = (m2 + kPlanBlock - 1) / kPlanBlock;
     const int a = tid * per, b = min(a + per, mb);
     int32_t cnt = 0;
-    for (int i = a; i < b; ++i) cnt += i == 0 || (keys[i] >> 3) != (keys[i - 1] >> 3);
+    bool dup = false;
+    for (int i = a; i < b; ++i) {
+      cnt += i == 0 || (keys[i] >> 3) != (keys[i - 1] >> 3);
+      // Equal (column, row) keys: a row that holds one column twice.  Its
+      // entry would carry one mask bit for two values, so the tile stays on
+      // the row-split, which adds both.
+      dup = dup || (i > 0 && keys[i] == keys[i - 1]);
+    }
+    if (!write && dup) atomicOr(&s_dup, 1);
     const int32_t incl = wave_incl_scan(cnt);
     if (lane == kWave - 1) s_scan[wave] = incl;
     __syncthreads();
@@ -150,7 +163,8 @@ __global__ void __launch_bounds__(kPlanBlock)
   if (!write) {
     const int32_t total = (s_cnt[0] + s_cnt[1] + s_cnt[2] + s_cnt[3]) +
                           (s_cnt[4] + s_cnt[5] + s_cnt[6] + s_cnt[7]);
-    const bool blocked = 2 * static_cast<int64_t>(total) <= static_cast<int64_t>(m);
+    const bool blocked =
+        s_dup == 0 && 2 * static_cast<int64_t>(total) <= static_cast<int64_t>(m);
     if (tid < kTileBlocks) ecount[tile * kTileBlocks + tid] = blocked ? s_cnt[tid] : 0;
     if (tid == 0) kind[tile] = blocked ? 1 : 0;
   }

@@ -57,7 +57,7 @@ def _normalize(value):
 def canonicalize_params(params: dict) -> str:
     """Canonical JSON of a params dict: sorted keys, no spaces."""
     if not isinstance(params, dict):
-        raise TypeError("params must be a dict")
+        raise TypeError(f"reorder parameters: expected a dict, got {type(params).__name__}")
     return json.dumps({k: _normalize(params[k]) for k in sorted(params)}, sort_keys=True,
                       separators=(",", ":"))
 
@@ -66,7 +66,7 @@ def compute_reorder_hash(reorder_method: str, params: dict, env: dict | None = N
     """12-hex-digit identity of a reorder configuration."""
     env = env or {}
     if not isinstance(env, dict):
-        raise TypeError("env must be a dict")
+        raise TypeError(f"reorder environment: expected a dict, got {type(env).__name__}")
     payload = {"method": reorder_method, "params": json.loads(canonicalize_params(params))}
     if env:
         payload["env"] = json.loads(canonicalize_params(env))
@@ -81,9 +81,9 @@ def get_perm_path(root, matrix: str, reorder_method: str, reorder_hash: str) -> 
 def validate_row_perm(row_perm, nrows: int) -> np.ndarray:
     perm = np.asarray(row_perm, dtype=np.int64)
     if perm.ndim != 1:
-        raise ValueError("row_perm must be a 1-D array")
+        raise ValueError(f"row permutation has {perm.ndim} dimensions; one is required")
     if perm.shape[0] != nrows:
-        raise ValueError(f"row_perm length {perm.shape[0]} != matrix rows {nrows}")
+        raise ValueError(f"row permutation holds {perm.shape[0]} entries for a matrix of {nrows} rows")
     seen = np.zeros(nrows, dtype=bool)
     if perm.size and (perm.min() < 0 or perm.max() >= nrows):
         raise ValueError("row_perm must hold each row index 0..nrows-1 exactly once")

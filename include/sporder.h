@@ -309,8 +309,9 @@ SPORDER_API void sporder_spmm_csr(sporder_context_t ctx, int32_t n,
  * bands, meshes in natural order, rows grouped by a reordering) is
  * "blocked": sporder_spmm_csr_plan computes each of its blocks with one load
  * of each entry's B row, applied to every row of the block that holds the
- * column.  Other tiles, and tiles with a row past SPORDER_SPMM_LONG_ROW
- * nonzeros, run the row-split.  Entries are visited in ascending column
+ * column.  Other tiles, tiles with a row past SPORDER_SPMM_LONG_ROW
+ * nonzeros and tiles in which a row repeats a column (a CSR with duplicate
+ * entries) run the row-split.  Entries are visited in ascending column
  * order, so the result is bit-identical to sporder_spmm_csr ROW_SPLIT (each C
  * element is the same fmaf chain in CSR order).  Blocks apply when cols is a
  * multiple of 64 and B and C are 16-byte aligned; otherwise the call is the
@@ -340,17 +341,44 @@ SPORDER_API void sporder_spmm_csr_plan(sporder_context_t ctx, sporder_spmm_plan_
                                        float *kernel_ms);
 
 /*
+ * (new) HBM ceiling.  No counterpart in the reference, whose SpMM hook times
+ * its kernel with events on the library stream
+ * (sporder/src/bench_cusparse_spmm.cu:51-100); this times a pure read, a pure
+ * write or a copy of `bytes` (a multiple of 16) with this library's own
+ * streaming kernels (16 bytes per lane per access, each workgroup a contiguous
+ * 16 KiB span, spans in contiguous runs per XCD), with ordinary or
+ * non-temporal accesses, so that the HBM-bound kernels' roofline fractions
+ * can be read against the rate streaming code reaches on the device.  One
+ * untimed launch, then `iters` timed ones; *ms_per_launch (optional) gets
+ * their mean.  READ leaves d_dst (16-byte aligned, at least 16 bytes) as it
+ * was; WRITE fills d_dst with the float 1.0f; COPY copies d_src to d_dst
+ * (non-overlapping).  Synchronous.
+ */
+typedef enum {
+  SPORDER_STREAM_READ = 0,
+  SPORDER_STREAM_WRITE = 1,
+  SPORDER_STREAM_COPY = 2
+} sporder_stream_op_t;
+SPORDER_API void sporder_hbm_stream(sporder_context_t ctx, int32_t op, int32_t nontemporal,
+                                    void *d_dst, const void *d_src, int64_t bytes,
+                                    int32_t iters, float *ms_per_launch);
+
+/*
  * (new) sporder_spmm_csr (ROW_SPLIT) that allocates nothing.  It has no
  * counterpart in the reference: it is for callers that cannot allocate device
- * memory (code under HIP graph capture, tight serving loops, harnesses that
- * forbid hipMalloc).  The result equals sporder_spmm_csr's bit for bit (same
+ * memory (tight serving loops, harnesses that forbid hipMalloc).  It runs
+ * eagerly on the library's private stream, reads a count back to the host
+ * partway and ends with a synchronize, so it cannot be recorded into a HIP
+ * graph.  The result equals sporder_spmm_csr's bit for bit (same
  * kernels, same stated order).  The caller passes every input and output; the
  * scratch the row-split needs for rows past SPORDER_SPMM_LONG_ROW nonzeros
  * (a 16-byte descriptor per such row, 4 bytes per segment and a partial row of
  * `cols` floats per segment, each part rounded up to 256 bytes) comes from a
  * static device array of SPORDER_SPMM_NOALLOC_SCRATCH_BYTES that each GPU
  * holds from the first context created on it until the process ends.  Every
- * call on one GPU shares that array: calls that overlap on one GPU race.
+ * call on one GPU shares that array: calls from one process on one GPU are
+ * serialised by a lock held for the whole call; calls that overlap from two
+ * processes on one GPU each use their own process's array.
  * Returns 0 when C is written, or SPORDER_SPMM_NOALLOC_TOO_LARGE (nothing
  * computed) when the input's long rows need more scratch than the array
  * holds.  Invalid arguments abort, as elsewhere.  Synchronous.

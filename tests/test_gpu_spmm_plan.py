@@ -54,6 +54,23 @@ def random_rows(n, deg, seed, hubs=None):
     return ptr.astype(np.int32), c.astype(np.int32)
 
 
+def with_repeats(csr, rows):
+    """Repeat the first column of each listed row (sorted, not distinct: a
+    CSR with duplicate entries, which the SpMM adds one after the other)."""
+    ptr, ind = csr[0], csr[1]
+    lens = np.diff(ptr)
+    parts = []
+    for r in range(ptr.shape[0] - 1):
+        seg = ind[ptr[r]:ptr[r + 1]]
+        if r in rows and seg.size:
+            seg = np.concatenate([seg[:1], seg])
+            lens[r] += 1
+        parts.append(seg)
+    p = np.zeros_like(ptr)
+    np.cumsum(lens, out=p[1:])
+    return p, np.concatenate(parts).astype(np.int32)
+
+
 def with_empty_rows(csr, every):
     """Drop the nonzeros of every `every`-th row."""
     ptr, ind = csr[0], csr[1]
@@ -76,6 +93,9 @@ MATS = {
     "band_hubs": with_values(synth.band(6000, 4), 6),           # replaced below
     "band_empty_rows": with_values(with_empty_rows(synth.band(3000, 6), 7), 7),
     "C1": synth.config1(11),
+    # Rows 5, 70 and 1000 repeat a column: their tiles (0, 1, 15) stay on the
+    # row-split, the other band tiles are blocked.
+    "band_repeats": with_values(with_repeats(synth.band(2000, 8), {5, 70, 1000}), 9),
 }
 # A band with long rows spliced in: their tiles go to the row-split segments.
 _p, _i = random_rows(6000, 0, 8, hubs={100: 900, 3000: 2000, 5999: 600})
@@ -122,7 +142,7 @@ def test_planned_spmm_equals_row_split(sporder, plans, name, N):
 def plan_model(ptr, ind):
     """The plan rule restated: 8-row blocks' entries are their distinct
     columns; a 64-row tile is blocked when no row has more than 512
-    nonzeros and 2 * entries <= nonzeros."""
+    nonzeros, no row holds a column twice and 2 * entries <= nonzeros."""
     n = ptr.shape[0] - 1
     out = {"tiles": (n + 63) // 64, "blocked_tiles": 0, "blocked_rows": 0, "blocked_nnz": 0,
            "entries": 0}
@@ -130,6 +150,9 @@ def plan_model(ptr, ind):
         r0, r1 = 64 * t, min(64 * t + 64, n)
         m = int(ptr[r1] - ptr[r0])
         if m == 0 or (np.diff(ptr[r0:r1 + 1]) > 512).any():
+            continue
+        if any(np.unique(ind[ptr[r]:ptr[r + 1]]).size < ptr[r + 1] - ptr[r]
+               for r in range(r0, r1)):
             continue
         e = sum(np.unique(ind[ptr[b]:ptr[min(b + 8, r1)]]).size for b in range(r0, r1, 8))
         if 2 * e <= m:
@@ -159,6 +182,8 @@ def test_plan_blocks_where_rows_share_columns(plans):
         assert info[name]["blocked_tiles"] == 0, name
     h = info["band_hubs"]
     assert h["blocked_tiles"] == h["tiles"] - len({100 // 64, 3000 // 64, 5999 // 64})
+    d = info["band_repeats"]
+    assert d["blocked_tiles"] == d["tiles"] - 3
 
 
 def test_plan_rejects_other_matrix(sporder, plans):

@@ -102,3 +102,41 @@ def test_noalloc_rejects_oversized_scratch(sporder, ctx):
     assert int(torch.count_nonzero(out)) == 0
     del B, out
     check_case(sporder, ctx, ptr_h, ind_h, val_h, N=128, seed=5)
+
+
+def test_noalloc_leaves_device_memory_unchanged(sporder):
+    """On a fresh context (empty workspace), a call with long rows leaves the
+    device's free memory as it was; sporder_spmm_csr on the same input and
+    context then grows the workspace (n = 60000, 1.2 M nonzeros, N = 512:
+    about 9 MiB of segment rows), which the same measurement sees, so the
+    check can tell an allocation apart."""
+    print("[noalloc] device memory unchanged on a fresh context", flush=True)
+    ptr_h, ind_h, val_h = hub_csr(60000, 20, {7: 4000, 30000: 9000, 59999: 700}, 65)
+    ptr, ind, val = to_dev(ptr_h, ind_h, val_h)
+    n, N = ptr_h.shape[0] - 1, 512
+    gen = torch.Generator(device="cuda:0").manual_seed(6)
+    B = torch.randn((n, N), generator=gen, dtype=torch.float32, device="cuda:0")
+    out = torch.zeros((n, N), dtype=torch.float32, device="cuda:0")
+    ref = torch.zeros((n, N), dtype=torch.float32, device="cuda:0")
+    fresh = sporder.Context()
+    # One small call first, so that the context's stream and the kernels are
+    # set up (the runtime may allocate for those on first use) before the
+    # measured call.
+    small = hub_csr(3000, 5, {10: 900}, 66)
+    sptr, sind, sval = to_dev(*small)
+    sB = torch.ones((3000, 64), dtype=torch.float32, device="cuda:0")
+    sC = torch.empty((3000, 64), dtype=torch.float32, device="cuda:0")
+    assert call_noalloc(sporder, fresh, sptr, sind, sval, sB, sC) == 0
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info()[0]
+    assert call_noalloc(sporder, fresh, ptr, ind, val, B, out) == 0
+    torch.cuda.synchronize()
+    free1 = torch.cuda.mem_get_info()[0]
+    assert free1 == free0, (free0, free1)
+    _lib.load().sporder_spmm_csr(fresh.handle, n, ind.numel(), ptr.data_ptr(), ind.data_ptr(),
+                                 val.data_ptr(), N, B.data_ptr(), ref.data_ptr(),
+                                 _lib.SPMM_ROW_SPLIT, None)
+    torch.cuda.synchronize()
+    free2 = torch.cuda.mem_get_info()[0]
+    assert free2 < free1, (free1, free2)
+    assert torch.equal(out.view(torch.int32), ref.view(torch.int32))
