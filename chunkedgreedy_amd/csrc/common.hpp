@@ -272,6 +272,13 @@ __device__ __forceinline__ int64_t xcd_block() {
 
 __device__ __forceinline__ uint64_t ballot(bool p) { return __ballot(p); }
 
+// Orders a wave's LDS accesses: what one lane wrote before is visible to
+// every lane of the wave after.
+__device__ __forceinline__ void wave_lds_order() {
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+}
+
 // A wave-uniform mask with bit i (wave-uniform) cleared: one s_bitset0,
 // where mask &= mask - 1 takes a 64-bit subtract and an and.  readfirstlane
 // states the uniformity to the compiler, which drops it where it already

@@ -174,11 +174,6 @@ struct RunLookup {
   int32_t base[kWave]; // a_j - excl_j: CSC index of item f is base[j] + f
 };
 
-__device__ __forceinline__ void wave_lds_order() {
-  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-}
-
 // CSC indices of items f0 .. f0+63 of a block whose run j (lane j) starts at
 // item excl_j and holds len_j items.  Each run starting inside the batch marks
 // its first slot with j + 1; a running maximum carries the run over its items

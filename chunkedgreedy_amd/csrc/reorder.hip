@@ -31,6 +31,14 @@ constexpr int kBlockSortThreads = 256;
 constexpr int kBigRow = 1024;
 constexpr int kPrepBlock = 1024;
 constexpr int kCopyUnit = 4096;
+// sort_runs: blocks of up to 2^kRunMaxBits columns (a bitmap of that many
+// bits per wave in LDS); runs of at most kRunRankCap entries are placed by
+// counting, in registers.
+constexpr int kRunMaxBits = 13;
+constexpr int kRunWords = (1 << kRunMaxBits) / 32;
+constexpr int kRunBlock = 256;
+constexpr int kRunWaves = kRunBlock / kWave;
+constexpr int kRunRankCap = 8;
 
 struct BigRow {
   int32_t src;  // first old entry
@@ -42,14 +50,20 @@ struct BigCtl {
   int32_t rows;
   int32_t units;
 };
-// One call's control words, zeroed by prepare_rows and read back once after
-// permute_rows: the three sort-list counts, the wide-remap flag, the big-row
-// registry's counts.
+// One call's control words, zeroed by prepare_rows and read back after
+// permute_rows (and after sort_runs): the three sort-list counts, the big-row
+// registry's counts, the wide-remap flag, the bit count `sh` of the largest
+// c ^ old2new[c] (every column stays inside its aligned block of 2^sh), and
+// the flag sort_runs sets when an input row is not strictly increasing.
 struct Ctl {
   int32_t counts[3];
-  int32_t wide;
   BigCtl big;
+  int32_t wide;
+  int32_t sh;
+  int32_t unsorted;
 };
+// Words of Ctl that a second permute_rows pass appends to from zero.
+constexpr int kCtlListWords = 5;
 
 int64_t max_big_rows(int32_t nnz) { return nnz / (kBigRow + 1) + 1; }
 int64_t max_copy_units(int32_t nnz) { return nnz / kCopyUnit + max_big_rows(nnz) + 1; }
@@ -104,26 +118,40 @@ __global__ void __launch_bounds__(kPrepBlock)
 // that moves every index by less than 2^15 (csg's, whose chains stay inside
 // chunks of at most 32768 rows, among them) gets a table half the size of
 // old2new, which stays in L2 where the 4-byte table at n = 2^20 fills it.  Any
-// larger move sets ctl->wide, and permute_rows then reads old2new.
+// larger move sets ctl->wide, and permute_rows then reads old2new.  Also
+// ctl->sh = the bit length of the largest c ^ old2new[c]: every column then
+// stays inside its aligned block of 2^sh indices (c >> sh is unchanged), which
+// is what lets sort_runs sort only within blocks (csg's chunk-local orders
+// give sh <= log2(chunk_size) for a power-of-two chunk size).
 __global__ void __launch_bounds__(256)
     narrow_map(int32_t n, const int32_t *__restrict__ old2new, int16_t *__restrict__ delta,
                Ctl *__restrict__ ctl) {
-  __shared__ int32_t s_far;
-  if (threadIdx.x == 0) s_far = 0;
+  __shared__ int32_t s_far, s_sh;
+  if (threadIdx.x == 0) {
+    s_far = 0;
+    s_sh = 0;
+  }
   __syncthreads();
   bool far = false;
+  uint32_t moved = 0; // OR of c ^ old2new[c]: its bit length is the largest one's
   for (int64_t c = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; c < n;
        c += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    const int32_t d = old2new[c] - static_cast<int32_t>(c);
+    const int32_t o = old2new[c];
+    const int32_t d = o - static_cast<int32_t>(c);
     far |= d < -32768 || d > 32767;
+    moved |= static_cast<uint32_t>(o) ^ static_cast<uint32_t>(c);
     delta[c] = static_cast<int16_t>(d);
   }
   if (far) s_far = 1;
+  const int32_t sh = moved ? 32 - __clz(static_cast<int32_t>(moved)) : 0;
+  const int32_t wsh = static_cast<int32_t>(wave_max_u32(static_cast<uint32_t>(sh)));
+  if (lane_id() == 0 && wsh != 0) atomicMax(&s_sh, wsh);
   __syncthreads();
   // One atomic per workgroup (the grid is a few per CU): a random permutation
   // sets the flag from every workgroup, and per-wave atomics on one word
   // would serialise.
   if (threadIdx.x == 0 && s_far != 0) atomicOr(&ctl->wide, 1);
+  if (threadIdx.x == 0 && s_sh != 0) atomicMax(&ctl->sh, s_sh);
 }
 
 // Appends `value` for every lane with `take` to list[*count ...]: one atomic
@@ -224,10 +252,13 @@ __global__ void __launch_bounds__(256)
                  int32_t *__restrict__ ind_new, float *__restrict__ val_new,
                  int32_t *__restrict__ key_tmp, float *__restrict__ val_tmp,
                  int32_t *__restrict__ lists, int32_t list_stride, Ctl *__restrict__ ctl,
-                 BigRow *big_rows, int32_t *big_owner) {
+                 BigRow *big_rows, int32_t *big_owner, int allow_runs) {
   constexpr int kRowsPerWave = kWave / G;
   // The 16-bit remap when narrow_map found every move within its range.
   const bool narrow = delta != nullptr && ctl->wide == 0;
+  // Run mode: the listed rows are gathered and sorted by sort_runs itself,
+  // so they are not copied here.
+  const bool runs = narrow && allow_runs != 0 && ctl->sh <= kRunMaxBits;
   constexpr int kRowsPerIter = kRowsPerWave * U;
   const int lane = lane_id();
   const int gl = lane % G;
@@ -301,7 +332,7 @@ __global__ void __launch_bounds__(256)
       // Rows sorted above need no bookkeeping; most waves have only those.
       if (ballot(row_ok && !sort_here) == 0) continue;
       const int32_t copy_cap = col_map ? kWaveSortCap : kBigRow;
-      if (row_ok && !sort_here && len[u] <= copy_cap) {
+      if (row_ok && !sort_here && len[u] <= copy_cap && !runs) {
         int32_t *ki = col_map ? key_tmp : ind_new;
         float *vo = col_map ? val_tmp : val_new;
         // Four entries per lane in flight: the column gather depends on the
@@ -527,6 +558,221 @@ __global__ void __launch_bounds__(kBlockSortThreads)
   }
 }
 
+// ---- run mode: rows already ordered by block ---------------------------------
+//
+// When every column c stays inside its aligned block of 2^sh indices
+// (old2new[c] >> sh == c >> sh) and an input row is strictly increasing, the
+// remapped row is already ordered by block: it is a sequence of runs of
+// entries with equal c >> sh, and sorting it means sorting each run on its
+// own.  A run holds at most 2^sh entries (distinct columns of one block), and
+// its remapped columns have distinct low sh bits.
+//
+// sort_runs gives each wave one task: a whole listed row of at most
+// kBlockSortCap entries, or one kCopyUnit-entry unit of a longer row (the
+// units permute_rows registered), widened at both ends to the next run
+// boundary so that every run belongs to exactly one task.  The wave walks its
+// range 64 entries at a time:
+//   - the longest prefix of whole runs inside the window is placed at once:
+//     singleton runs are copied, runs of at most kRunRankCap entries are
+//     placed by counting the smaller keys of their run (shuffles), otherwise
+//     the prefix is sorted by a bitonic network over the wave (it consists of
+//     whole runs, so sorting it by remapped column sorts each run);
+//   - a run longer than the window is placed with a bitmap of its low bits
+//     in LDS: one pass sets a bit per entry, a scan of the words' population
+//     counts gives each word's rank, a second pass writes each entry at its
+//     rank.
+// Every pair of neighbouring input entries of the task is checked; a row
+// that is not strictly increasing sets ctl->unsorted, and the host then
+// redoes the call's long rows with the full sorts (positions stay inside the
+// task's output range either way).
+
+struct RunBits {
+  uint32_t bits[kRunWords];
+  uint32_t rank[kRunWords];
+};
+
+// First index i >= q with i == len or c[i] >> sh != c[i - 1] >> sh (q >= 1):
+// a run boundary.  For a strictly increasing row it lies within 2^sh entries
+// of q; a longer search means the row is not, and sets *bad (the result is
+// then any deterministic index in [q, len], the same for both tasks that ask).
+__device__ __forceinline__ int32_t next_run_start(const int32_t *__restrict__ row, int32_t q,
+                                                  int32_t len, int sh, bool *bad) {
+  const int lane = lane_id();
+  for (int32_t w0 = q; w0 < len; w0 += kWave) {
+    const int32_t i = w0 + lane;
+    bool edge = i >= len;
+    if (!edge) edge = (row[i] >> sh) != (row[i - 1] >> sh);
+    const uint64_t m = ballot(edge);
+    if (m != 0) return w0 + __builtin_ctzll(m);
+    if (w0 + kWave - q > (1 << sh)) {
+      *bad = true;
+      return w0 + kWave < len ? w0 + kWave : len;
+    }
+  }
+  return len;
+}
+
+// Places the run starting at s (longer than one window) through the wave's
+// bitmap; returns its end.  Entries past the run (another block) are left to
+// the caller.
+__device__ __forceinline__ int32_t place_long_run(RunBits *rb, const int32_t *__restrict__ ind,
+                                                  const float *__restrict__ val,
+                                                  const int16_t *__restrict__ delta, int32_t s,
+                                                  int32_t b, int32_t len, int sh,
+                                                  int32_t *__restrict__ key_out,
+                                                  float *__restrict__ val_out, bool *bad) {
+  const int lane = lane_id();
+  const int32_t h0 = ind[s] >> sh;
+  const uint32_t lowmask = (1u << sh) - 1u;
+  const int words = sh >= 5 ? (1 << (sh - 5)) : 1;
+  int32_t re = b;
+  for (int32_t w0 = s;; w0 += kWave) {
+    const int32_t i = w0 + lane;
+    const bool in = i < b;
+    const int32_t c = in ? ind[i] : 0;
+    const bool inrun = in && (c >> sh) == h0;
+    if (inrun) {
+      const int32_t cn = i + 1 < len ? ind[i + 1] : 0x7fffffff;
+      if (cn <= c) *bad = true;
+      const uint32_t low = static_cast<uint32_t>(c + delta[c]) & lowmask;
+      atomicOr(&rb->bits[low >> 5], 1u << (low & 31u));
+    }
+    const int cnt = __popcll(ballot(inrun));
+    if (cnt < kWave) {
+      re = w0 + cnt;
+      break;
+    }
+    if (w0 + kWave - s > (1 << sh)) {
+      // More than 2^sh entries of one block: not strictly increasing.
+      *bad = true;
+      re = w0 + kWave;
+      break;
+    }
+  }
+  wave_lds_order();
+  // Rank of each word: the set bits of the words before it.
+  int32_t carry = 0;
+  for (int w = lane; w - lane < words; w += kWave) {
+    const int32_t x = w < words ? __popc(rb->bits[w]) : 0;
+    const int32_t incl = wave_incl_scan(x);
+    if (w < words) rb->rank[w] = carry + incl - x;
+    carry += readlane(incl, kWave - 1);
+  }
+  wave_lds_order();
+  for (int32_t w0 = s; w0 < re; w0 += kWave) {
+    const int32_t i = w0 + lane;
+    if (i < re) {
+      const int32_t c = ind[i];
+      // Entries of another block (only in a row that is not strictly
+      // increasing) are not written: their bit may be missing.
+      if ((c >> sh) == h0) {
+        const int32_t key = c + delta[c];
+        const uint32_t low = static_cast<uint32_t>(key) & lowmask;
+        const uint32_t word = rb->bits[low >> 5];
+        const int32_t pos = rb->rank[low >> 5] + __popc(word & ((1u << (low & 31u)) - 1u));
+        key_out[s + pos] = key;
+        if (val_out) val_out[s + pos] = val ? val[i] : 0.0f;
+      }
+    }
+  }
+  wave_lds_order();
+  for (int w = lane; w < words; w += kWave) rb->bits[w] = 0;
+  wave_lds_order();
+  return re;
+}
+
+__global__ void __launch_bounds__(kRunBlock)
+    sort_runs(const int32_t *__restrict__ lists, int32_t list_stride, int32_t rows0,
+              int32_t rows1, int32_t units, const int32_t *__restrict__ ptr_new,
+              const int32_t *__restrict__ src_new, const BigRow *__restrict__ big_rows,
+              const int32_t *__restrict__ big_owner, const int32_t *__restrict__ ind_old,
+              const float *__restrict__ val_old, const int16_t *__restrict__ delta, int sh,
+              int32_t *__restrict__ ind_new, float *__restrict__ val_new,
+              Ctl *__restrict__ ctl) {
+  __shared__ RunBits s_bits[kRunWaves];
+  RunBits *rb = &s_bits[threadIdx.x / kWave];
+  const int lane = lane_id();
+  for (int w = lane; w < kRunWords; w += kWave) rb->bits[w] = 0;
+  wave_lds_order();
+  bool bad = false;
+  const int64_t wave0 = (blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x) / kWave;
+  const int64_t nwaves = static_cast<int64_t>(gridDim.x) * blockDim.x / kWave;
+  const int64_t tasks = static_cast<int64_t>(units) + rows1 + rows0;
+  // Units (the longest rows) first, then the rows of the two lists.
+  for (int64_t t = wave0; t < tasks; t += nwaves) {
+    int32_t src, len, dst, a, b;
+    if (t < units) {
+      const BigRow br = big_rows[big_owner[t]];
+      src = br.src;
+      len = br.len;
+      dst = br.dst;
+      const int32_t q0 = (static_cast<int32_t>(t) - br.base) * kCopyUnit;
+      const int32_t q1 = q0 + kCopyUnit < len ? q0 + kCopyUnit : len;
+      a = q0 == 0 ? 0 : next_run_start(ind_old + src, q0, len, sh, &bad);
+      b = q1 == len ? len : next_run_start(ind_old + src, q1, len, sh, &bad);
+    } else {
+      const int64_t l = t - units;
+      const int32_t r = l < rows1 ? lists[list_stride + l] : lists[l - rows1];
+      src = src_new[r];
+      dst = ptr_new[r];
+      len = ptr_new[r + 1] - dst;
+      a = 0;
+      b = len;
+    }
+    const int32_t *ind = ind_old + src;
+    const float *val = val_old ? val_old + src : nullptr;
+    int32_t *kout = ind_new + dst;
+    float *vout = val_new ? val_new + dst : nullptr;
+    int32_t s = a;
+    while (s < b) {
+      const int32_t i = s + lane;
+      const bool in = i < b;
+      const int32_t c = in ? ind[i] : 0;
+      const int32_t cn = in && i + 1 < len ? ind[i + 1] : 0x7fffffff;
+      if (in && cn <= c) bad = true;
+      // Lane i ends a run when the next entry is past the task or in another
+      // block.
+      const uint64_t me = ballot(in && (i + 1 == b || (cn >> sh) != (c >> sh)));
+      if (me == 0) {
+        // The run at s is longer than the window.
+        s = place_long_run(rb, ind, val, delta, s, b, len, sh, kout, vout, &bad);
+        continue;
+      }
+      // Whole runs in lanes [0, last].
+      const int last = 63 - __builtin_clzll(me);
+      const bool mine = lane <= last;
+      int32_t key = mine ? c + delta[c] : 0x7fffffff;
+      float v = (mine && val) ? val[i] : 0.0f;
+      // Run of this lane: [rs, re] in lanes.
+      const uint64_t starts = (me << 1) | 1ull;
+      const int rs = 63 - __builtin_clzll(starts & (~0ull >> (63 - lane)));
+      const int re = __builtin_ctzll(me & (~0ull << lane) | (1ull << 63));
+      const uint32_t span = mine ? static_cast<uint32_t>(re - rs + 1) : 1u;
+      const uint32_t longest = wave_max_u32(span);
+      int pos = lane;
+      if (longest > static_cast<uint32_t>(kRunRankCap)) {
+        // Sort the whole-run prefix (lanes past `last` hold the padding key).
+        group_sort<kWave>(key, v, lane);
+      } else if (longest > 1) {
+        int rank = 0;
+        for (int d = 1; d < static_cast<int>(longest); ++d) {
+          const int32_t up = __shfl(key, lane - d >= 0 ? lane - d : 0, kWave);
+          const int32_t dn = __shfl(key, lane + d < kWave ? lane + d : kWave - 1, kWave);
+          rank += (lane - d >= rs && up < key) ? 1 : 0;
+          rank += (lane + d <= re && dn < key) ? 1 : 0;
+        }
+        pos = rs + rank;
+      }
+      if (mine) {
+        kout[s + pos] = key;
+        if (vout) vout[s + pos] = v;
+      }
+      s += last + 1;
+    }
+  }
+  if (ballot(bad) != 0 && lane == 0) atomicOr(&ctl->unsorted, 1);
+}
+
 // ---- rows longer than kBlockSortCap: one device-wide sort ------------------
 //
 // Their entries are gathered into one array and sorted by (row rank, column):
@@ -640,13 +886,14 @@ void launch_permute_g(Context &ctx, int32_t n, const int32_t *src_new, const int
                       const float *val_old, const int32_t *col_map, const int16_t *delta,
                       const int32_t *ptr_new, int32_t *ind_new, float *val_new,
                       int32_t *key_tmp, float *val_tmp, int32_t *lists, int32_t list_stride,
-                      Ctl *ctl, BigRow *big_rows, int32_t *big_owner) {
+                      Ctl *ctl, BigRow *big_rows, int32_t *big_owner, bool allow_runs) {
   constexpr int U = G <= 16 ? 4 : 2;
   constexpr int rows_per_block = 4 * (kWave / G) * U;
   const int g = ctx.grid_for(ceil_div64(n, rows_per_block), 256, 4);
   permute_rows<G, U><<<g, 256, 0, ctx.stream>>>(n, src_new, ind_old, val_old, col_map, delta,
                                                 ptr_new, ind_new, val_new, key_tmp, val_tmp,
-                                                lists, list_stride, ctl, big_rows, big_owner);
+                                                lists, list_stride, ctl, big_rows, big_owner,
+                                                allow_runs ? 1 : 0);
   SP_LAUNCH_CHECK();
 }
 
@@ -654,13 +901,14 @@ void launch_permute(Context &ctx, int G, int32_t n, const int32_t *src_new,
                     const int32_t *ind_old, const float *val_old, const int32_t *col_map,
                     const int16_t *delta, const int32_t *ptr_new, int32_t *ind_new,
                     float *val_new, int32_t *key_tmp, float *val_tmp, int32_t *lists,
-                    int32_t list_stride, Ctl *ctl, BigRow *big_rows, int32_t *big_owner) {
+                    int32_t list_stride, Ctl *ctl, BigRow *big_rows, int32_t *big_owner,
+                    bool allow_runs) {
   switch (G) {
 #define SP_CASE(V)                                                                       \
   case V:                                                                                \
     launch_permute_g<V>(ctx, n, src_new, ind_old, val_old, col_map, delta, ptr_new,      \
                         ind_new, val_new, key_tmp, val_tmp, lists, list_stride, ctl,     \
-                        big_rows, big_owner);                                            \
+                        big_rows, big_owner, allow_runs);                                \
     break;
     SP_CASE(4) SP_CASE(8) SP_CASE(16) SP_CASE(32) SP_CASE(64)
 #undef SP_CASE
@@ -740,7 +988,7 @@ extern "C" void sporder_reorder(sporder_context_t h, int32_t n, int32_t nnz,
   if (!symmetric) {
     launch_permute(ctx, G, n, src_new, d_ind_old, d_val_old, nullptr, nullptr, d_ptr_new,
                    d_ind_new, d_val_new, nullptr, nullptr, nullptr, 0, ctl, big_rows,
-                   big_owner);
+                   big_owner, false);
     read_ctl();
     if (hc.big.units > 0) {
       launch_copy_big(ctx, hc.big.units, d_ind_old, d_val_old, nullptr, big_rows, big_owner,
@@ -768,8 +1016,29 @@ extern "C" void sporder_reorder(sporder_context_t h, int32_t n, int32_t nnz,
   // longer rows are listed by length for the stage that sorts them, and the
   // stages launch only when their lists have rows.
   launch_permute(ctx, G, n, src_new, d_ind_old, vo, old2new, delta, d_ptr_new, d_ind_new, vn,
-                 unsorted, vt, lists, stride, ctl, big_rows, big_owner);
+                 unsorted, vt, lists, stride, ctl, big_rows, big_owner, true);
   read_ctl();
+  // Run mode, as permute_rows decided it from the same control words: every
+  // listed row is gathered and sorted run by run in one launch.  A row that
+  // is not strictly increasing sends the call's long rows back through the
+  // full sorts below, after a second permute_rows pass without run mode.
+  if (hc.wide == 0 && hc.sh <= kRunMaxBits) {
+    const int64_t tasks = static_cast<int64_t>(hc.big.units) + hc.counts[0] + hc.counts[1];
+    if (tasks == 0) return;
+    const int g = std::min<int>(ctx.grid_for(ceil_div64(tasks, kRunWaves), kRunBlock, 8),
+                                8 * ctx.num_cus);
+    sort_runs<<<g, kRunBlock, 0, ctx.stream>>>(lists, stride, hc.counts[0], hc.counts[1],
+                                               hc.big.units, d_ptr_new, src_new, big_rows,
+                                               big_owner, d_ind_old, vo, delta, hc.sh,
+                                               d_ind_new, vn, ctl);
+    SP_LAUNCH_CHECK();
+    read_ctl();
+    if (hc.unsorted == 0) return;
+    fill_u32(ctx, ctl, kCtlListWords, 0u);
+    launch_permute(ctx, G, n, src_new, d_ind_old, vo, old2new, delta, d_ptr_new, d_ind_new,
+                   vn, unsorted, vt, lists, stride, ctl, big_rows, big_owner, false);
+    read_ctl();
+  }
   const bool narrow = hc.wide == 0;
   bool queued = false;
   if (hc.counts[0] > 0) {

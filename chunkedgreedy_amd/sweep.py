@@ -15,11 +15,14 @@ chunk-restricted candidate streams hold at most M distinct items (the
 space-saving sketch never evicts there) and how much of the stream work those
 rows hold, plus the longest streams' distinct counts (``candidate_stats``).
 
+With ``--runs`` (host only): the rows the permutation apply sends to its
+long-row stage and their runs of equal column block (``run_stats``).
+
 Configurations: C1..C5 (synth.CONFIGS) and the inputs with in-chunk locality
 C2r, C4n, RGG20 (synth.LOCALITY).
 
 Usage:  python -m chunkedgreedy_amd.sweep [--cfg C1,C2,C3,C4,C5] [--no-spmm]
-        [--algos row_split,merge_path,plan] [--cg] [--candidates]
+        [--algos row_split,merge_path,plan] [--cg] [--candidates] [--runs]
 """
 
 from __future__ import annotations
@@ -107,11 +110,16 @@ def measure(name: str, *, spmm=True, algos=("row_split",), repeats=3, cg=False) 
     del flush
 
     sporder.reorder(ptr, ind, order, val=val, symmetric=True, ctx=ctx)  # warmup
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    p2, i2, v2 = sporder.reorder(ptr, ind, order, val=val, symmetric=True, ctx=ctx)
-    torch.cuda.synchronize()
-    rec["permute_ms"] = (time.perf_counter() - t1) * 1e3
+    perm_ms = []
+    for _ in range(5):
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        p2, i2, v2 = sporder.reorder(ptr, ind, order, val=val, symmetric=True, ctx=ctx)
+        torch.cuda.synchronize()
+        perm_ms.append((time.perf_counter() - t1) * 1e3)
+    rec["permute_ms"] = statistics.median(perm_ms)
+    print(f"[{name}] permutation apply {rec['permute_ms']:.3f} ms (median of 5)",
+          file=sys.stderr, flush=True)
 
     if spmm:
         if "plan" in algos:
@@ -175,6 +183,35 @@ def candidate_stats(ptr, ind, chunk: int, M: int) -> dict:
     }
 
 
+def run_stats(ptr, ind, block_bits: int = 10) -> dict:
+    """The rows the permutation apply lists for its long-row stage (more than
+    2G entries, G = the mean row length rounded up to a power of two in
+    [4, 64]) and their runs of equal column block c >> block_bits: under an
+    order that keeps every column inside its block (csg and cg with chunks of
+    2^block_bits) the apply sorts runs, not rows.  Host only."""
+    ptr = np.asarray(ptr, np.int64)
+    ind = np.asarray(ind, np.int64)
+    n, nnz = ptr.shape[0] - 1, ind.shape[0]
+    G = 4
+    while G < 64 and G * n < nnz:
+        G <<= 1
+    lens = np.diff(ptr)
+    long_rows = lens > 2 * G
+    rows = np.repeat(np.arange(n), lens)
+    sel = long_rows[rows]
+    key = rows[sel] * ((n >> block_bits) + 1) + (ind[sel] >> block_bits)
+    cut = np.flatnonzero(np.diff(key) != 0) + 1
+    runs = np.diff(np.concatenate([[0], cut, [key.shape[0]]])) if key.size else np.zeros(0)
+    out = {"G": G, "long_rows": int(long_rows.sum()), "long_entries": int(lens[long_rows].sum()),
+           "runs": int(runs.shape[0]), "mean_run": float(runs.mean()) if runs.size else 0.0,
+           "max_run": int(runs.max()) if runs.size else 0}
+    for t in (1, 2, 8, 64):
+        out[f"runs_le_{t}"] = float((runs <= t).mean()) if runs.size else 1.0
+        out[f"entries_in_runs_le_{t}"] = (float(runs[runs <= t].sum() / runs.sum())
+                                          if runs.size else 1.0)
+    return out
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--cfg", default="C1,C2,C3,C4,C5")
@@ -184,7 +221,16 @@ def main(argv=None) -> int:
     ap.add_argument("--cg", action="store_true", help="also time sporder-cg once")
     ap.add_argument("--candidates", action="store_true",
                     help="host only: rows whose candidate streams fit the sketch")
+    ap.add_argument("--runs", action="store_true",
+                    help="host only: long rows of the permutation apply and their block runs")
     args = ap.parse_args(argv)
+
+    if args.runs:
+        gens = generators()
+        for name in args.cfg.split(","):
+            ptr, ind = gens[name]()[:2]
+            print(json.dumps({"config": name, **run_stats(ptr, ind)}), flush=True)
+        return 0
 
     if args.candidates:
         gens = generators()

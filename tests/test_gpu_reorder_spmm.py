@@ -93,16 +93,36 @@ MATS = mats()
 
 
 def permutation(n, kind, seed=5):
-    """A uniform permutation, or one that shuffles rows only inside aligned
-    windows of 1024 (as csg's chains do inside their chunks), which moves
-    every index by less than 2^15 and so takes the 16-bit column remap."""
+    """A uniform permutation, or one that shuffles rows only inside windows:
+    aligned windows of 1024 (as csg's chains do inside their chunks) or 8192
+    keep every column inside an aligned block of 2^10 or 2^13 indices (the
+    apply's run mode); aligned windows of 16384 move indices by less than
+    2^15 (16-bit column remap) but past run mode's largest block; windows of
+    1000 are not aligned to a power of two (the blocks they stay inside
+    depend on where a window crosses one); "identity" moves nothing."""
     rng = np.random.default_rng(seed)
     if kind == "uniform":
         return rng.permutation(n).astype(np.int32)
+    if kind == "identity":
+        return np.arange(n, dtype=np.int32)
+    width = {"windowed": 1024, "windowed8192": 8192, "windowed16384": 16384,
+             "unaligned1000": 1000}[kind]
     perm = np.arange(n)
-    for w in range(0, n, 1024):
-        rng.shuffle(perm[w:w + 1024])
+    for w in range(0, n, width):
+        rng.shuffle(perm[w:w + width])
     return perm.astype(np.int32)
+
+
+def _reorder_check(sporder, ptr, ind, val, perm, symmetric, with_val):
+    if with_val:
+        gp, gi, gv = sporder.reorder(t(ptr), t(ind), t(perm), val=t(val), symmetric=symmetric)
+        op, oi, ov = oracle.reorder(ptr, ind, perm, val=val, symmetric=symmetric)
+        assert np.array_equal(gv.cpu().numpy().view(np.uint32), ov.view(np.uint32))
+    else:
+        gp, gi = sporder.reorder(t(ptr), t(ind), t(perm), symmetric=symmetric)
+        op, oi = oracle.reorder(ptr, ind, perm, symmetric=symmetric)
+    assert np.array_equal(gp.cpu().numpy(), op)
+    assert np.array_equal(gi.cpu().numpy(), oi)
 
 
 @pytest.mark.parametrize("name", sorted(MATS))
@@ -126,6 +146,54 @@ def test_reorder_bit_exact(sporder, name, symmetric, with_val, kind):
         op, oi = oracle.reorder(ptr, ind, perm, symmetric=symmetric)
     assert np.array_equal(gp.cpu().numpy(), op)
     assert np.array_equal(gi.cpu().numpy(), oi)
+
+
+@pytest.mark.parametrize("name", ["longrows", "hub", "manyhuge", "rmat12", "skewed"])
+@pytest.mark.parametrize("kind", ["identity", "windowed8192", "windowed16384", "unaligned1000",
+                                  "csg", "cg"])
+def test_reorder_block_runs(sporder, name, kind):
+    """SYMMETRIC with values under permutations that keep columns inside
+    aligned blocks (run mode: rows of 2G+1..512, 513..4096 and past 4096
+    entries, singleton runs, runs placed by counting, by the wave sort and
+    by the LDS bitmap) and ones that do not (full sorts): csg's and cg's own
+    orders of the matrix, the identity, and windowed shuffles."""
+    ptr, ind, val = MATS[name]
+    n = ptr.shape[0] - 1
+    if kind in ("csg", "cg"):
+        fn = sporder.chunk_similarity_greedy if kind == "csg" else sporder.chunk_greedy
+        perm = fn(t(ptr), t(ind)).cpu().numpy().astype(np.int32)
+    else:
+        perm = permutation(n, kind)
+    print(f"[reorder runs] {name} perm={kind}", flush=True)
+    _reorder_check(sporder, ptr, ind, val, perm, True, True)
+
+
+def unsorted_rows_matrix(n=30000, seed=11):
+    """Distinct columns, but rows 5 (300 entries), 40 (5000 entries, the
+    device-wide class) and 90 (2000 entries) not in increasing order: one
+    pair swapped, the whole row reversed, a run's order rotated."""
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(0, 12, size=n)
+    lens[5], lens[40], lens[90] = 300, 5000, 2000
+    rows = [np.sort(rng.choice(n, size=L, replace=False)) for L in lens]
+    rows[5][[100, 101]] = rows[5][[101, 100]]
+    rows[40] = rows[40][::-1].copy()
+    rows[90] = np.concatenate([rows[90][1:], rows[90][:1]])
+    ptr = np.zeros(n + 1, np.int64)
+    np.cumsum(lens, out=ptr[1:])
+    ind = np.concatenate(rows)
+    val = rng.standard_normal(ind.shape[0]).astype(np.float32)
+    return ptr.astype(np.int32), ind.astype(np.int32), val
+
+
+@pytest.mark.parametrize("kind", ["windowed", "identity", "uniform"])
+def test_reorder_unsorted_input_rows(sporder, kind):
+    """Input rows that are not strictly increasing: run mode detects them and
+    the call takes the full sorts; the output is sorted like the oracle's."""
+    ptr, ind, val = unsorted_rows_matrix()
+    perm = permutation(ptr.shape[0] - 1, kind)
+    print(f"[reorder unsorted] perm={kind}", flush=True)
+    _reorder_check(sporder, ptr, ind, val, perm, True, True)
 
 
 def test_reorder_csg_roundtrip(sporder):
