@@ -418,12 +418,7 @@ __global__ void __launch_bounds__(kLocalThreads, (local_min_waves<CELLS, KEYCAP>
               item = true;
             }
           }
-          uint64_t mask = ballot(item);
-          while (mask) {
-            const int i = __builtin_ctzll(mask);
-            store.add(readlane(other, i), readlane_f(alpha, i));
-            mask = clear_bit(mask, i);
-          }
+          store.consume(ballot(item), other, alpha);
         }
       }
       store.select_top_k(k, out);

@@ -248,6 +248,15 @@ template <int CELLS> struct WaveSketch {
   // are a dependent chain, and every taken branch lengthens it: the global
   // path's hub rows).
   __device__ __forceinline__ void feed(uint64_t mask, int32_t other, float alpha) {
+    if constexpr (CELLS == 4) {
+      feed4(mask, other, alpha);
+    } else {
+      feed_generic(mask, other, alpha);
+    }
+  }
+
+  // feed() in compiled code, for every capacity.
+  __device__ __forceinline__ void feed_generic(uint64_t mask, int32_t other, float alpha) {
     const int lane = lane_id();
     while (mask != 0 && filled < M) {
       const int i = __builtin_ctzll(mask);
@@ -293,6 +302,180 @@ template <int CELLS> struct WaveSketch {
         }
       }
     }
+  }
+
+  // The chunk tiers' item loop: add() item by item in lane order (the form
+  // that measured fastest there for capacities other than 128), or feed4.
+  __device__ __forceinline__ void consume(uint64_t mask, int32_t other, float alpha) {
+    if constexpr (CELLS == 4) {
+      feed4(mask, other, alpha);
+    } else {
+      while (mask) {
+        const int i = __builtin_ctzll(mask);
+        add(readlane(other, i), readlane_f(alpha, i));
+        mask = clear_bit(mask, i);
+      }
+    }
+  }
+
+  // feed() for CELLS == 4 (M = 128, two cells in every lane: the capacity of
+  // csg's default k of 17..32), written as one block of GCN assembly.  The
+  // same updates as add() item by item; written out because the compiler's
+  // version of the same steps issues more instructions per miss (register
+  // copies where the hit and miss paths join, both cells written where one
+  // changes, a three-instruction lowest-bit isolation per cell), and the
+  // chunk tiers are issue-bound: on a C5-like stream (half the items from
+  // 100 hot keys, half from 1000 cold ones) the whole GPU moves 23.0 G
+  // items/s through the compiled loop and 27.9 G items/s through this one
+  // at four waves per SIMD, with the same slots afterwards.
+  //
+  // Per item (lane i of the mask, lowest first): k, w by v_readlane; the hit
+  // masks h0, h1 of the two cells.  A hit adds w in both cells, each select
+  // on its hit mask (one of them is empty): no branch on the cell, which
+  // costs a single wave more than the two vector instructions it saves.
+  // Each path ends with its own test for a next item and jump back, so a hit
+  // takes one taken branch.  A miss while slots are free fills
+  // slot s = filled: logical lane s >> 2, cell s & 3, i.e. physical lane
+  // (s >> 2) + 32 (s & 1), local cell (s >> 1) & 1, written by v_writelane.
+  // A miss on a full sketch takes the DPP minimum of the weight bits (as
+  // wave_min_u32), then the first tied lane of cell 0, else of cell 1 (tie
+  // order c*32 + L = 64j + p), and writes k there with v_writelane and
+  // wmin + w as the lane's own weight plus w (the lane holds exactly wmin).
+  //
+  // Wait states: the s_nop counts are those the compiler puts between the
+  // same instructions (a VALU write of an SGPR before a VALU read of it: 2; a
+  // VALU write of a VGPR before a DPP read of it: 2; a DPP write before
+  // v_readlane of it: 1).  Lane selects of v_readlane and v_writelane are
+  // written by scalar instructions (s_ff1, s_add); the one of v_writelane is
+  // M0 (with an SGPR data operand, another SGPR as lane select breaks the
+  // one-scalar-operand limit of a VALU instruction), with one wait state
+  // after its write; the block saves M0 and restores it at the end.
+  // Every lane of the wave must be active.
+  __device__ __forceinline__ void feed4(uint64_t mask, int32_t other, float alpha) {
+    static_assert(CELLS == 4, "two cells per lane");
+    uint32_t i, p, q, kk, ww, wmin;
+    uint64_t h0, h1, any, mm, sel;
+    float t;
+    // Both are wave-uniform; readfirstlane states it, so that the compiler
+    // hands them over in scalar registers.
+    mask = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int32_t>(mask))) |
+           (static_cast<uint64_t>(static_cast<uint32_t>(
+                __builtin_amdgcn_readfirstlane(static_cast<int32_t>(mask >> 32))))
+            << 32);
+    filled = __builtin_amdgcn_readfirstlane(filled);
+    uint32_t m0_saved;
+    asm volatile(
+        "s_mov_b32 %[m0s], m0\n\t"
+        "s_cmp_eq_u64 %[mask], 0\n\t"
+        "s_cbranch_scc1 9f\n"
+        // ---- while slots are free (mask != 0 here)
+        "0:\n\t"
+        "s_cmp_ge_u32 %[f], 0x80\n\t"
+        "s_cbranch_scc1 5f\n\t"
+        "s_ff1_i32_b64 %[i], %[mask]\n\t"
+        "s_bitset0_b64 %[mask], %[i]\n\t"
+        "v_readlane_b32 %[kk], %[other], %[i]\n\t"
+        "v_readlane_b32 %[ww], %[alpha], %[i]\n\t"
+        "s_nop 0\n\t"
+        "v_cmp_eq_u32_e64 %[h0], %[kk], %[k0]\n\t"
+        "v_cmp_eq_u32_e64 %[h1], %[kk], %[k1]\n\t"
+        "s_or_b64 %[any], %[h0], %[h1]\n\t"
+        "s_cbranch_scc0 2f\n\t"
+        // hit: the add in both cells, selected by the hit masks (one is empty)
+        "v_add_f32_e64 %[t], %[ww], %[w0]\n\t"
+        "v_cndmask_b32_e64 %[w0], %[w0], %[t], %[h0]\n\t"
+        "v_add_f32_e64 %[t], %[ww], %[w1]\n\t"
+        "v_cndmask_b32_e64 %[w1], %[w1], %[t], %[h1]\n\t"
+        "s_cmp_lg_u64 %[mask], 0\n\t"
+        "s_cbranch_scc1 0b\n\t"
+        "s_branch 9f\n"
+        // fill slot f: physical lane (f >> 2) + 32 (f & 1), cell (f >> 1) & 1
+        "2:\n\t"
+        "s_lshr_b32 %[p], %[f], 2\n\t"
+        "s_and_b32 %[q], %[f], 1\n\t"
+        "s_lshl_b32 %[q], %[q], 5\n\t"
+        "s_add_u32 m0, %[p], %[q]\n\t"
+        "s_bitcmp1_b32 %[f], 1\n\t"
+        "s_cbranch_scc1 3f\n\t"
+        "v_writelane_b32 %[k0], %[kk], m0\n\t"
+        "v_writelane_b32 %[w0], %[ww], m0\n\t"
+        "s_add_u32 %[f], %[f], 1\n\t"
+        "s_cmp_lg_u64 %[mask], 0\n\t"
+        "s_cbranch_scc1 0b\n\t"
+        "s_branch 9f\n"
+        "3:\n\t"
+        "v_writelane_b32 %[k1], %[kk], m0\n\t"
+        "v_writelane_b32 %[w1], %[ww], m0\n\t"
+        "s_add_u32 %[f], %[f], 1\n\t"
+        "s_cmp_lg_u64 %[mask], 0\n\t"
+        "s_cbranch_scc1 0b\n\t"
+        "s_branch 9f\n"
+        // ---- full: every miss evicts (mask != 0 here)
+        "5:\n\t"
+        "s_ff1_i32_b64 %[i], %[mask]\n\t"
+        "s_bitset0_b64 %[mask], %[i]\n\t"
+        "v_readlane_b32 %[kk], %[other], %[i]\n\t"
+        "v_readlane_b32 %[ww], %[alpha], %[i]\n\t"
+        "s_nop 0\n\t"
+        "v_cmp_eq_u32_e64 %[h0], %[kk], %[k0]\n\t"
+        "v_cmp_eq_u32_e64 %[h1], %[kk], %[k1]\n\t"
+        "s_or_b64 %[any], %[h0], %[h1]\n\t"
+        "s_cbranch_scc0 6f\n\t"
+        "v_add_f32_e64 %[t], %[ww], %[w0]\n\t"
+        "v_cndmask_b32_e64 %[w0], %[w0], %[t], %[h0]\n\t"
+        "v_add_f32_e64 %[t], %[ww], %[w1]\n\t"
+        "v_cndmask_b32_e64 %[w1], %[w1], %[t], %[h1]\n\t"
+        "s_cmp_lg_u64 %[mask], 0\n\t"
+        "s_cbranch_scc1 5b\n\t"
+        "s_branch 9f\n"
+        "6:\n\t"
+        "v_min_u32_e32 %[t], %[w0], %[w1]\n\t"
+        "s_nop 1\n\t"
+        "v_min_u32_dpp %[t], %[t], %[t] quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"
+        "s_nop 1\n\t"
+        "v_min_u32_dpp %[t], %[t], %[t] quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf\n\t"
+        "s_nop 1\n\t"
+        "v_min_u32_dpp %[t], %[t], %[t] row_half_mirror row_mask:0xf bank_mask:0xf\n\t"
+        "s_nop 1\n\t"
+        "v_min_u32_dpp %[t], %[t], %[t] row_mirror row_mask:0xf bank_mask:0xf\n\t"
+        "s_nop 1\n\t"
+        "v_min_u32_dpp %[t], %[t], %[t] row_bcast:15 row_mask:0xa bank_mask:0xf\n\t"
+        "s_nop 1\n\t"
+        "v_min_u32_dpp %[t], %[t], %[t] row_bcast:31 row_mask:0xc bank_mask:0xf\n\t"
+        "s_nop 0\n\t"
+        "v_readlane_b32 %[wmin], %[t], 63\n\t"
+        "s_nop 1\n\t"
+        "v_cmp_eq_u32_e64 %[mm], %[wmin], %[w0]\n\t"
+        "s_cmp_eq_u64 %[mm], 0\n\t"
+        "s_cbranch_scc1 7f\n\t"
+        "s_ff1_i32_b64 m0, %[mm]\n\t"
+        "s_nop 0\n\t"
+        "v_writelane_b32 %[k0], %[kk], m0\n\t"
+        "s_lshl_b64 %[sel], 1, m0\n\t"
+        "v_add_f32_e64 %[t], %[ww], %[w0]\n\t"
+        "v_cndmask_b32_e64 %[w0], %[w0], %[t], %[sel]\n\t"
+        "s_cmp_lg_u64 %[mask], 0\n\t"
+        "s_cbranch_scc1 5b\n\t"
+        "s_branch 9f\n"
+        "7:\n\t"
+        "v_cmp_eq_u32_e64 %[mm], %[wmin], %[w1]\n\t"
+        "s_ff1_i32_b64 m0, %[mm]\n\t"
+        "s_nop 0\n\t"
+        "v_writelane_b32 %[k1], %[kk], m0\n\t"
+        "s_lshl_b64 %[sel], 1, m0\n\t"
+        "v_add_f32_e64 %[t], %[ww], %[w1]\n\t"
+        "v_cndmask_b32_e64 %[w1], %[w1], %[t], %[sel]\n\t"
+        "s_cmp_lg_u64 %[mask], 0\n\t"
+        "s_cbranch_scc1 5b\n"
+        "9:\n\t"
+        "s_mov_b32 m0, %[m0s]"
+        : [k0] "+v"(key[0]), [k1] "+v"(key[1]), [w0] "+v"(wt[0]), [w1] "+v"(wt[1]),
+          [mask] "+s"(mask), [f] "+s"(filled), [t] "=&v"(t), [i] "=&s"(i), [p] "=&s"(p),
+          [q] "=&s"(q), [kk] "=&s"(kk), [ww] "=&s"(ww), [wmin] "=&s"(wmin), [h0] "=&s"(h0),
+          [h1] "=&s"(h1), [any] "=&s"(any), [mm] "=&s"(mm), [sel] "=&s"(sel),
+          [m0s] "=&s"(m0_saved)
+        : [other] "v"(other), [alpha] "v"(alpha)
+        : "scc");
   }
 
   // The hit test: true (and the weight added) when k is held.  HIT_FIRST adds

@@ -201,6 +201,9 @@ def main(argv=None) -> int:
     # sporder-cg's global sketch streams sum(deg(c)^2) items per row set; on a
     # Chung-Lu graph with 600K-degree hubs that is minutes, so it is opt-in.
     ap.add_argument("--orders", default="ORIGIN,sporder-csg")
+    ap.add_argument("--degree-order", action="store_true",
+                    help="vertices in expected-degree order (synth LOCALITY C5d) "
+                    "instead of the scrambled ids of configuration C5")
     args = ap.parse_args(argv)
 
     import torch
@@ -211,9 +214,11 @@ def main(argv=None) -> int:
     from chunkedgreedy_amd import synth
 
     t0 = time.time()
-    ptr_h, ind_h, _ = synth.chung_lu(args.nodes, args.exponent, args.degree, args.seed)
+    ptr_h, ind_h, _ = synth.chung_lu(args.nodes, args.exponent, args.degree, args.seed,
+                                     scramble=not args.degree_order)
     print(f"[e2e] Chung-Lu n={ptr_h.shape[0] - 1} nnz={ind_h.shape[0]} "
-          f"({time.time() - t0:.1f}s)", file=sys.stderr, flush=True)
+          f"({'degree order' if args.degree_order else 'scrambled ids'}, "
+          f"{time.time() - t0:.1f}s)", file=sys.stderr, flush=True)
     for row in run(ptr_h, ind_h, features=args.features, hidden=args.hidden,
                    classes=args.classes, epochs=args.epochs,
                    orders=tuple(args.orders.split(",")), seed=args.seed):

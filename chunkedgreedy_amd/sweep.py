@@ -19,10 +19,11 @@ With ``--runs`` (host only): the rows the permutation apply sends to its
 long-row stage and their runs of equal column block (``run_stats``).
 
 Configurations: C1..C5 (synth.CONFIGS) and the inputs with in-chunk locality
-C2r, C4n, RGG20 (synth.LOCALITY).
+C2r, C4n, RGG20, C5d (synth.LOCALITY).
 
 Usage:  python -m chunkedgreedy_amd.sweep [--cfg C1,C2,C3,C4,C5] [--no-spmm]
         [--algos row_split,merge_path,plan] [--cg] [--candidates] [--runs]
+        [--widths 32,256] [--spmm-iters K] [--spmm-warmup W] [--calibrate BYTES]
 """
 
 from __future__ import annotations
@@ -38,7 +39,7 @@ import numpy as np
 WIDTHS = {"C1": [32], "C2": [32, 128], "C3": [32, 64, 256], "C4": [16, 32, 64, 128, 256],
           "C5": [128],
           # inputs with in-chunk locality (synth.LOCALITY)
-          "C2r": [128], "C4n": [32], "RGG20": [32, 128]}
+          "C2r": [128], "C4n": [32], "RGG20": [32, 128], "C5d": [128]}
 
 
 def generators() -> dict:
@@ -51,7 +52,7 @@ def spmm_bytes(n: int, nnz: int, N: int) -> int:
     return 4 * (n + 1) + 8 * nnz + 8 * n * N
 
 
-def _spmm_ms(sporder, ctx, ptr, ind, val, B, algo, iters=20):
+def _spmm_ms(sporder, ctx, ptr, ind, val, B, algo, iters=20, warmup=5):
     """Median launch time; algo "plan" times the planned SpMM, the plan made
     beforehand and untimed (the harness's prepare step)."""
     import torch
@@ -59,7 +60,7 @@ def _spmm_ms(sporder, ctx, ptr, ind, val, B, algo, iters=20):
     plan = sporder.spmm_plan(ptr, ind, ctx=ctx) if algo == "plan" else None
     kw = {"plan": plan} if plan is not None else {"algo": algo}
     out = torch.empty(B.shape, dtype=torch.float32, device=B.device)
-    for _ in range(5):
+    for _ in range(warmup):
         sporder.spmm_csr(ptr, ind, val, B, out=out, ctx=ctx, **kw)
     ms = statistics.median(
         sporder.spmm_csr(ptr, ind, val, B, out=out, ctx=ctx, **kw)[1] for _ in range(iters))
@@ -68,7 +69,29 @@ def _spmm_ms(sporder, ctx, ptr, ind, val, B, algo, iters=20):
     return ms
 
 
-def measure(name: str, *, spmm=True, algos=("row_split",), repeats=3, cg=False) -> dict:
+def calibration_copy(nbytes: int, ctx) -> None:
+    """One launch of the library's copy kernel over nbytes (reads nbytes,
+    writes nbytes): the reference dispatch by which a `rocprofv3 --pmc` run
+    scales FETCH_SIZE and WRITE_SIZE to bytes."""
+    import ctypes
+
+    import torch
+
+    from chunkedgreedy_amd import _lib
+
+    src = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    ms = ctypes.c_float()
+    _lib.load().sporder_hbm_stream(ctx.handle, _lib.STREAM_COPY, 0, dst.data_ptr(),
+                                   src.data_ptr(), nbytes, 1, ctypes.byref(ms))
+    del src, dst
+    print(f"[calibration] sporder_hbm_stream copy of {nbytes} bytes: {ms.value:.4f} ms",
+          file=sys.stderr, flush=True)
+
+
+def measure(name: str, *, spmm=True, algos=("row_split",), repeats=3, cg=False,
+            widths=None, spmm_iters=20, spmm_warmup=5, calibrate=0) -> dict:
     import torch
 
     from chunkedgreedy_amd import sporder, synth
@@ -76,6 +99,8 @@ def measure(name: str, *, spmm=True, algos=("row_split",), repeats=3, cg=False) 
     gens = generators()
     dev = torch.device("cuda:0")
     ctx = sporder.Context()
+    if calibrate > 0:
+        calibration_copy(calibrate, ctx)
     t0 = time.time()
     ptr_h, ind_h, val_h = gens[name]()
     n, nnz = ptr_h.shape[0] - 1, ind_h.shape[0]
@@ -130,13 +155,13 @@ def measure(name: str, *, spmm=True, algos=("row_split",), repeats=3, cg=False) 
                 rec["plan"][tag] = dict(plan.info)
                 plan.close()
         rec["spmm"] = {}
-        for N in WIDTHS[name]:
+        for N in (widths or WIDTHS[name]):
             gen = torch.Generator(device=dev).manual_seed(42)
             B = torch.randn((n, N), generator=gen, dtype=torch.float32, device=dev)
             by = spmm_bytes(n, nnz, N)
             for algo in algos:
-                to = _spmm_ms(sporder, ctx, ptr, ind, val, B, algo)
-                tr = _spmm_ms(sporder, ctx, p2, i2, v2, B, algo)
+                to = _spmm_ms(sporder, ctx, ptr, ind, val, B, algo, spmm_iters, spmm_warmup)
+                tr = _spmm_ms(sporder, ctx, p2, i2, v2, B, algo, spmm_iters, spmm_warmup)
                 rec["spmm"][f"{N}/{algo}"] = {
                     "orig_ms": round(to, 4), "reordered_ms": round(tr, 4),
                     "orig_gbs": round(by / to / 1e6, 1), "reordered_gbs": round(by / tr / 1e6, 1)}
@@ -221,6 +246,13 @@ def main(argv=None) -> int:
     ap.add_argument("--cg", action="store_true", help="also time sporder-cg once")
     ap.add_argument("--candidates", action="store_true",
                     help="host only: rows whose candidate streams fit the sketch")
+    ap.add_argument("--widths", default=None, help="SpMM widths, e.g. 32,256 (default: "
+                    "the configuration's own)")
+    ap.add_argument("--spmm-iters", type=int, default=20)
+    ap.add_argument("--spmm-warmup", type=int, default=5)
+    ap.add_argument("--calibrate", type=int, default=0, metavar="BYTES",
+                    help="one library copy-kernel launch over BYTES before each "
+                    "configuration (the reference dispatch of a --pmc run)")
     ap.add_argument("--runs", action="store_true",
                     help="host only: long rows of the permutation apply and their block runs")
     args = ap.parse_args(argv)
@@ -250,8 +282,11 @@ def main(argv=None) -> int:
         print("sweep needs a ROCm GPU", file=sys.stderr)
         return 1
     for name in args.cfg.split(","):
+        widths = [int(w) for w in args.widths.split(",")] if args.widths else None
         rec = measure(name, spmm=not args.no_spmm, algos=tuple(args.algos.split(",")),
-                      repeats=args.repeats, cg=args.cg)
+                      repeats=args.repeats, cg=args.cg, widths=widths,
+                      spmm_iters=args.spmm_iters, spmm_warmup=args.spmm_warmup,
+                      calibrate=args.calibrate)
         print(json.dumps(rec), flush=True)
         torch.cuda.empty_cache()
     return 0

@@ -210,13 +210,17 @@ def _alias_table(w: np.ndarray):
     return np.array(prob), np.array(alias, np.int64)
 
 
-def chung_lu(n: int, exponent: float, avg_degree: float, seed: int) -> Csr:
+def chung_lu(n: int, exponent: float, avg_degree: float, seed: int,
+             scramble: bool = True) -> Csr:
     """Chung-Lu graph with expected degrees w_i proportional to
     (i + 1)^(-1/(exponent-1)): edges with both endpoints drawn proportional to
     w, symmetrized and deduplicated, drawn in rounds until the mean number of
     distinct neighbours (self loops excluded) reaches `avg_degree` (the hubs
     draw many duplicates, so n*avg_degree/2 draws alone fall short); then the
-    identity added and values D^-1/2 (A + I) D^-1/2."""
+    identity added and values D^-1/2 (A + I) D^-1/2.  With `scramble` (the
+    default) vertex ids are a random permutation of the expected-degree order;
+    without it vertex i is the i-th largest expected degree (the same graph,
+    relabelled: the edges are drawn first, the relabelling last)."""
     rng = _rng(seed)
     w = (np.arange(n, dtype=np.float64) + 1.0) ** (-1.0 / (exponent - 1.0))
     prob, alias = _alias_table(w)
@@ -248,7 +252,7 @@ def chung_lu(n: int, exponent: float, avg_degree: float, seed: int) -> Csr:
         m = max(1024, int((target - k.shape[0]) / per_draw * 1.05))
     k = np.union1d(k, np.arange(n, dtype=np.int64) * (n + 1))  # self loops
     # Scramble vertex ids so that degree does not follow the index.
-    p = rng.permutation(n)
+    p = rng.permutation(n) if scramble else np.arange(n, dtype=np.int64)
     rows, cols = p[k // n], p[k % n]
     deg = np.bincount(rows, minlength=n).astype(np.float64)
     dinv = 1.0 / np.sqrt(deg)
@@ -256,8 +260,8 @@ def chung_lu(n: int, exponent: float, avg_degree: float, seed: int) -> Csr:
     return _coo_to_csr(n, rows, cols, vals)
 
 
-def config5(seed: int = 5, n: int = 2_449_029) -> Csr:
-    return chung_lu(n, 2.1, 25.0, seed)
+def config5(seed: int = 5, n: int = 2_449_029, scramble: bool = True) -> Csr:
+    return chung_lu(n, 2.1, 25.0, seed, scramble=scramble)
 
 
 def rgg(n: int, avg_degree: float, seed: int) -> Csr:
@@ -329,10 +333,12 @@ CONFIGS = {
 # Inputs whose rows carry locality inside each chunk (the reorder benchmark's
 # SuiteSparse and DIMACS matrices do; C2 and C4 as configured are scrambled, so
 # their chunk-restricted candidate streams are nearly empty): C2 with its rows
-# in planted block order, C4 in natural grid order, and a random geometric
-# graph of 2^20 points with mean degree 13.
+# in planted block order, C4 in natural grid order, a random geometric graph of
+# 2^20 points with mean degree 13, and C5 with vertices in expected-degree
+# order (hubs first, the order a degree-sorted graph file has).
 LOCALITY = {
     "C2r": lambda: config2(planted_rows=True),
     "C4n": lambda: stencil7(160, 4, scramble=False),
     "RGG20": lambda: rgg(1 << 20, 13.0, 20),
+    "C5d": lambda: config5(scramble=False),
 }

@@ -40,3 +40,22 @@ def test_chung_lu_reaches_its_mean_degree():
     d = np.diff(ptr).astype(np.float64)
     np.testing.assert_allclose(val, (1.0 / np.sqrt(d[rows] * d[ind])).astype(np.float32),
                                rtol=1e-6)
+
+
+def test_chung_lu_degree_order_is_the_same_graph_relabelled():
+    """Without the scramble the graph is the scrambled one relabelled (the
+    edges are drawn first, the relabelling last): the same multiset of edges
+    seen as (degree of row, degree of column) pairs, and the largest expected
+    degrees at the lowest ids."""
+    n, deg = 20000, 8.0
+    ptr_s, ind_s, _ = synth.chung_lu(n, 2.1, deg, 7)
+    ptr_d, ind_d, _ = synth.chung_lu(n, 2.1, deg, 7, scramble=False)
+    ds, dd = np.diff(ptr_s), np.diff(ptr_d)
+
+    def degree_pairs(ptr, ind, d):
+        rows = np.repeat(np.arange(n), np.diff(ptr))
+        return np.sort(d[rows].astype(np.int64) * (n + 1) + d[ind])
+
+    assert np.array_equal(degree_pairs(ptr_s, ind_s, ds), degree_pairs(ptr_d, ind_d, dd))
+    assert dd[:100].mean() > 10 * dd.mean()
+    assert ds[:100].mean() < 3 * ds.mean()
