@@ -439,9 +439,12 @@ constexpr int kT2Keys = 32768, kT2Rows = 4096, kT2Nb = 10;
 // one workgroup per CU: tier 2 then takes chunks of at most this many
 // nonzeros and the larger ones go to the global path, which adds waves to
 // the SIMDs that tier 2 leaves at four.  Measured on C5 (Chung-Lu, most
-// chunks tier 2): csg 37.3-38.2 ms with the split at 32768, 33.1 at 26624,
-// 33.7-34.4 at 28672, 34.4 at 24576, 42.0 at 20480; C3 unchanged.
-constexpr int kT2SharedKeys = 26624;
+// chunks tier 2), csg median of 5, with the capacity-128 sketch update in
+// GCN assembly: 36.7 ms with the split at 22528, 33.8 at 24576, 30.8 at
+// 26624, 28.5 at 28672, 29.0 at 30720, 31.0 at 32768 (with the compiled
+// update, whose tier-2 items cost more, 33.1 at 26624 was the best); C3
+// unchanged.
+constexpr int kT2SharedKeys = 28672;
 
 constexpr int kClassifyThreads = 1024;
 // Up to this many chunks one workgroup classifies and orders the lists,

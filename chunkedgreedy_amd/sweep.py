@@ -24,6 +24,7 @@ C2r, C4n, RGG20, C5d (synth.LOCALITY).
 Usage:  python -m chunkedgreedy_amd.sweep [--cfg C1,C2,C3,C4,C5] [--no-spmm]
         [--algos row_split,merge_path,plan] [--cg] [--candidates] [--runs]
         [--widths 32,256] [--spmm-iters K] [--spmm-warmup W] [--calibrate BYTES]
+        [--cache DIR]
 """
 
 from __future__ import annotations
@@ -46,6 +47,23 @@ def generators() -> dict:
     from chunkedgreedy_amd import synth
 
     return {**synth.CONFIGS, **synth.LOCALITY}
+
+
+def generate(name: str, cache: str | None = None):
+    """The configuration's CSR (ptr, ind, val), from `cache`/<name>.npz when
+    present, else generated (and written there when `cache` is given), so
+    that several runs of one session generate each input once."""
+    import os
+
+    path = os.path.join(cache, f"{name}.npz") if cache else None
+    if path and os.path.exists(path):
+        with np.load(path) as z:
+            return z["ptr"], z["ind"], z["val"]
+    ptr, ind, val = generators()[name]()
+    if path:
+        os.makedirs(cache, exist_ok=True)
+        np.savez(path, ptr=ptr, ind=ind, val=val)
+    return ptr, ind, val
 
 
 def spmm_bytes(n: int, nnz: int, N: int) -> int:
@@ -91,7 +109,7 @@ def calibration_copy(nbytes: int, ctx) -> None:
 
 
 def measure(name: str, *, spmm=True, algos=("row_split",), repeats=3, cg=False,
-            widths=None, spmm_iters=20, spmm_warmup=5, calibrate=0) -> dict:
+            widths=None, spmm_iters=20, spmm_warmup=5, calibrate=0, cache=None) -> dict:
     import torch
 
     from chunkedgreedy_amd import sporder, synth
@@ -102,7 +120,7 @@ def measure(name: str, *, spmm=True, algos=("row_split",), repeats=3, cg=False,
     if calibrate > 0:
         calibration_copy(calibrate, ctx)
     t0 = time.time()
-    ptr_h, ind_h, val_h = gens[name]()
+    ptr_h, ind_h, val_h = generate(name, cache)
     n, nnz = ptr_h.shape[0] - 1, ind_h.shape[0]
     sym = synth.is_pattern_symmetric(ptr_h, ind_h)
     print(f"[{name}] generated n={n} nnz={nnz} symmetric={sym} in {time.time() - t0:.1f}s",
@@ -253,6 +271,8 @@ def main(argv=None) -> int:
     ap.add_argument("--calibrate", type=int, default=0, metavar="BYTES",
                     help="one library copy-kernel launch over BYTES before each "
                     "configuration (the reference dispatch of a --pmc run)")
+    ap.add_argument("--cache", default=None, metavar="DIR",
+                    help="keep generated inputs as DIR/<config>.npz and reuse them")
     ap.add_argument("--runs", action="store_true",
                     help="host only: long rows of the permutation apply and their block runs")
     args = ap.parse_args(argv)
@@ -286,7 +306,7 @@ def main(argv=None) -> int:
         rec = measure(name, spmm=not args.no_spmm, algos=tuple(args.algos.split(",")),
                       repeats=args.repeats, cg=args.cg, widths=widths,
                       spmm_iters=args.spmm_iters, spmm_warmup=args.spmm_warmup,
-                      calibrate=args.calibrate)
+                      calibrate=args.calibrate, cache=args.cache)
         print(json.dumps(rec), flush=True)
         torch.cuda.empty_cache()
     return 0

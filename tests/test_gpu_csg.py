@@ -322,7 +322,7 @@ def test_overflow_chunks_take_global_path(sporder, symmetric, chunk):
 
 
 def test_tier2_split_symmetric(sporder):
-    """On a symmetric pattern tier 2 keeps chunks of at most 26,624 nonzeros
+    """On a symmetric pattern tier 2 keeps chunks of at most 28,672 nonzeros
     and the larger ones, up to its 32,768 capacity, go to the global path,
     which runs beside it; chunks on both sides of the split (no tier-1 chunk
     here) give the oracle's table and permutation bit for bit."""
@@ -339,7 +339,7 @@ def test_tier2_split_symmetric(sporder):
     np.cumsum(np.bincount(r, minlength=n), out=ptr[1:])
     ptr, ind = ptr.astype(np.int32), c.astype(np.int32)
     E = ptr[chunk::chunk] - ptr[:-1:chunk]
-    assert ((E > 16384) & (E <= 26624)).any() and ((E > 26624) & (E <= 32768)).any()
+    assert ((E > 16384) & (E <= 28672)).any() and ((E > 28672) & (E <= 32768)).any()
     check_table(sporder, ptr, ind, 16, 4.0, chunk, True)
     dptr, dind = dev_csr(ptr, ind)
     g = sporder.chunk_similarity_greedy(dptr, dind, is_symmetric=True, chunk_size=chunk)

@@ -1,5 +1,7 @@
 """Host logic of the configuration sweep (no GPU calls)."""
 
+import numpy as np
+
 from chunkedgreedy_amd import sweep
 
 
@@ -12,7 +14,7 @@ def test_spmm_bytes_matches_c2_figures():
 def test_widths_cover_every_config():
     assert sweep.WIDTHS == {"C1": [32], "C2": [32, 128], "C3": [32, 64, 256],
                             "C4": [16, 32, 64, 128, 256], "C5": [128],
-                            "C2r": [128], "C4n": [32], "RGG20": [32, 128]}
+                            "C2r": [128], "C4n": [32], "RGG20": [32, 128], "C5d": [128]}
     assert set(sweep.generators()) == set(sweep.WIDTHS)
 
 
@@ -59,3 +61,20 @@ def test_candidate_stats_against_brute_force():
     assert st["items_within_M"] == length[busy & (distinct <= M)].sum()
     assert st["rows_at_M"] == (distinct == M).sum()
     assert st["longest"][0]["items"] == length.max()
+
+
+def test_generate_cache_round_trip(tmp_path, monkeypatch):
+    """generate() writes the input once and reads it back unchanged."""
+    calls = []
+
+    def fake():
+        calls.append(1)
+        return (np.array([0, 1, 2], np.int32), np.array([1, 0], np.int32),
+                np.array([0.5, -0.25], np.float32))
+
+    monkeypatch.setattr(sweep, "generators", lambda: {"X": fake})
+    a = sweep.generate("X", str(tmp_path))
+    b = sweep.generate("X", str(tmp_path))
+    assert len(calls) == 1
+    for u, v in zip(a, b):
+        assert u.dtype == v.dtype and np.array_equal(u, v)
