@@ -176,8 +176,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--spmm-iters", type=int, default=100)
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
-                    help="first run one device-to-device copy of BYTES (a kernel of known "
-                         "traffic for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
+                    help="first run one launch of this library's copy kernel over BYTES (a "
+                         "kernel of known traffic for scaling rocprofv3 FETCH_SIZE / "
+                         "WRITE_SIZE)")
     ap.add_argument("--only-spmm", action="store_true",
                     help="profiler pass: one reorder, then --spmm-iters SpMMs at N=128 on the "
                          "reordered matrix; prints no JSON line")
@@ -205,12 +206,12 @@ def main():
     torch.cuda.set_device(dev)
 
     if args.copy_calibration > 0:
-        src = torch.ones(args.copy_calibration // 4, dtype=torch.float32, device=dev)
-        dst = torch.empty_like(src)
-        dst.copy_(src)
-        torch.cuda.synchronize()
+        # One launch of this library's copy kernel (stream_copy_kernel<false>)
+        # over the given bytes: the reference dispatch of a --pmc run.
+        from chunkedgreedy_amd.sweep import calibration_copy
+
+        calibration_copy(args.copy_calibration, sporder.Context())
         log(f"copy calibration: {args.copy_calibration} bytes read + written")
-        del src, dst
     if args.read_calibration > 0:
         src = torch.ones(args.read_calibration // 4, dtype=torch.float32, device=dev)
         total = float(src.sum())

@@ -270,6 +270,21 @@ __device__ __forceinline__ int64_t xcd_block() {
   return x * q + (x < rem ? x : rem) + blockIdx.x / kXcds;
 }
 
+// Workgroup index remapped so that each run of W consecutive logical
+// workgroups (a tile of rows) stays on one XCD and the tiles are dealt to the
+// XCDs in turn: XCD x takes tiles x, x + kXcds, x + 2 kXcds, ...  Rows of one
+// tile share that XCD's L2, and work that grows or shrinks along the index
+// (hubs first in a degree-sorted graph) is spread over every XCD.  The grid
+// past the last whole round of kXcds tiles keeps its own index.  A bijection
+// of [0, gridDim.x).
+__device__ __forceinline__ int64_t xcd_tile_block(int64_t W) {
+  const int64_t G = gridDim.x, g = blockIdx.x;
+  const int64_t full = (G / (kXcds * W)) * (kXcds * W);
+  if (g >= full) return g;
+  const int64_t x = g % kXcds, i = g / kXcds;
+  return ((i / W) * kXcds + x) * W + i % W;
+}
+
 __device__ __forceinline__ uint64_t ballot(bool p) { return __ballot(p); }
 
 // Orders a wave's LDS accesses: what one lane wrote before is visible to
