@@ -189,6 +189,13 @@ def measure(name: str, *, spmm=True, algos=("row_split",), repeats=3, cg=False,
     return rec
 
 
+# Chunk tiers of the csg sketch (csrc/csg_local.hip chunk_tier: kT1Keys,
+# kT1Rows, kT2SharedKeys for symmetric input, kT2Rows): a chunk of E nonzeros
+# and R rows runs in tier 1 if E <= 16384 and R <= 1024, in tier 2 if
+# E <= 28672 and R <= 4096, else on the global path.
+TIER1_KEYS, TIER1_ROWS, TIER2_KEYS, TIER2_ROWS = 16384, 1024, 28672, 4096
+
+
 def candidate_stats(ptr, ind, chunk: int, M: int) -> dict:
     """Stream length and distinct candidates of every row's chunk-restricted
     stream (reference sporder/src/common/chunk_similarity_top_k.cu:53-83:
@@ -196,7 +203,9 @@ def candidate_stats(ptr, ind, chunk: int, M: int) -> dict:
 
     Distinct candidates of row r = nonzeros of row r of A_q A_q^T without the
     diagonal, A_q the rows of r's chunk; stream length = the sum over r's
-    columns of (rows of the chunk in that column) - 1."""
+    columns of (rows of the chunk in that column) - 1.  ``items_by_tier``
+    splits the stream lengths by the tier that runs the row's chunk for a
+    symmetric input (the table above)."""
     import scipy.sparse as sp
 
     ptr = np.asarray(ptr, np.int64)
@@ -217,10 +226,18 @@ def candidate_stats(ptr, ind, chunk: int, M: int) -> dict:
     busy = length > 0
     fits = busy & (distinct <= M)
     top = np.argsort(length, kind="stable")[::-1][:5]
+    starts = np.arange(0, n, chunk)
+    E = ptr[np.minimum(starts + chunk, n)] - ptr[starts]
+    R = np.minimum(starts + chunk, n) - starts
+    tier = np.where((E <= TIER1_KEYS) & (R <= TIER1_ROWS), 1,
+                    np.where((E <= TIER2_KEYS) & (R <= TIER2_ROWS), 2, 3))
+    by_tier = np.bincount(tier[np.arange(n) // chunk], weights=length, minlength=4)
     return {
         "M": M, "rows_with_items": int(busy.sum()), "rows_within_M": int(fits.sum()),
         "items": int(length.sum()), "items_within_M": int(length[fits].sum()),
         "rows_at_M": int((distinct == M).sum()), "rows_at_M_plus_1": int((distinct == M + 1).sum()),
+        "items_by_tier": {"tier1": int(by_tier[1]), "tier2": int(by_tier[2]),
+                          "global": int(by_tier[3])},
         "longest": [{"row": int(r), "items": int(length[r]), "distinct": int(distinct[r])}
                     for r in top],
     }

@@ -58,6 +58,9 @@ def test_candidate_stats_against_brute_force():
     assert st["rows_with_items"] == busy.sum()
     assert st["rows_within_M"] == (busy & (distinct <= M)).sum()
     assert st["items"] == length.sum()
+    assert sum(st["items_by_tier"].values()) == length.sum()
+    # 600 rows of at most 64 nonzeros in chunks of 64 rows: every chunk fits tier 1
+    assert st["items_by_tier"]["tier1"] == length.sum()
     assert st["items_within_M"] == length[busy & (distinct <= M)].sum()
     assert st["rows_at_M"] == (distinct == M).sum()
     assert st["longest"][0]["items"] == length.max()
@@ -78,3 +81,27 @@ def test_generate_cache_round_trip(tmp_path, monkeypatch):
     assert len(calls) == 1
     for u, v in zip(a, b):
         assert u.dtype == v.dtype and np.array_equal(u, v)
+
+
+def test_candidate_items_by_tier():
+    """Chunks of 10, 20 and 30 nonzeros per row (1024 rows each: 10,240,
+    20,480 and 30,720 nonzeros) fall in tier 1, tier 2 and the global path;
+    each chunk's stream length is sum_c cnt(c) (cnt(c) - 1) over its columns'
+    counts cnt(c)."""
+    import numpy as np
+
+    rng = np.random.default_rng(7)
+    n, chunk = 3072, 1024
+    rows = []
+    for r in range(n):
+        deg = 10 * (r // chunk + 1)
+        rows.append(np.sort(rng.choice(n, deg, replace=False)))
+    ptr = np.concatenate([[0], np.cumsum([len(x) for x in rows])]).astype(np.int32)
+    ind = np.concatenate(rows).astype(np.int32)
+    st = sweep.candidate_stats(ptr, ind, chunk, 128)
+    want = []
+    for q in range(3):
+        cnt = np.bincount(ind[ptr[q * chunk]:ptr[(q + 1) * chunk]], minlength=n).astype(np.int64)
+        want.append(int((cnt * (cnt - 1)).sum()))
+    assert st["items_by_tier"] == {"tier1": want[0], "tier2": want[1], "global": want[2]}
+    assert st["items"] == sum(want)
