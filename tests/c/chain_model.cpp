@@ -14,11 +14,22 @@
 // chunk are counted and not performed; a row written at a second position is
 // counted.
 //
+// Staging modelled: 64-bit entries (weight bits, local index) sorted into
+// preference order when a chunk's in-chunk entries fit entry_cap; else, when
+// packed_cap > 0 and they fit the launch's packed capacity, 16-bit local
+// indices in table order with each run of equal weight sorted by index (the
+// kernel's packed rows, which need the table rows in weight order to give the
+// same preference order); else table reads.  With packed_cap > 0 the chain
+// is split over two launches as the host does it: the narrow launch packs up
+// to min(packed_cap, 4 * entry_cap) entries, the second takes the chunks whose
+// valid-entry sum S lies in (max(entry_cap, that), packed_cap] and packs up to
+// packed_cap.
+//
 // Walks modelled:
 //   variant 0: the kernel's walk, its mode chosen as the kernel chooses it
-//              (table reads when the slice exceeds entry_cap, else the
-//              one-entry mode when at least half the rows with entries have
-//              exactly one, else the sorted scan with read-ahead);
+//              (table reads when the slice is neither staged nor packed, else
+//              the one-entry mode when at least half the rows with entries
+//              have exactly one, else the sorted scan with read-ahead);
 //   variants 1, 2, 3: the kernel's table, one-entry and sorted modes forced
 //              (1 only applies to a slice past entry_cap, 2 and 3 to a
 //              compacted one);
@@ -97,8 +108,10 @@ struct Wave {
 struct Chunk {
   int32_t start, end, size, words;
   std::vector<std::vector<uint64_t>> rows; // in-chunk entries per row, preference order
+  std::vector<std::vector<uint16_t>> packed; // the kernel's packed rows (16-bit local indices)
   std::vector<int32_t> in_count;
   int64_t total;
+  int64_t valid; // S: valid entries of the slice (the sketch's per-row counts, summed)
 };
 
 // Staged entries as the kernel builds them: a row's in-chunk entries among its
@@ -111,16 +124,51 @@ Chunk stage(int32_t n, int32_t k, int32_t chunk_size, int64_t chunk, const uint6
   c.size = c.end - c.start;
   c.words = (c.size + 31) >> 5;
   c.rows.assign(c.size, {});
+  c.packed.assign(c.size, {});
   c.in_count.assign(c.size, 0);
   c.total = 0;
+  c.valid = 0;
   for (int32_t r = 0; r < c.size; ++r) {
     const uint64_t *row = table + static_cast<size_t>(c.start + r) * k;
+    // Valid entries form a prefix of the row (the sketch's count).
+    int32_t rv = 0;
+    while (rv < k && wi_index(row[rv]) >= 0) ++rv;
+    c.valid += rv;
     for (int32_t j = 0; j < k; ++j) {
       const int32_t x = wi_index(row[j]);
       if (x < 0) continue;
       if (x >= c.start && x < c.end) {
         c.rows[r].push_back((row[j] & 0xFFFFFFFF00000000ull) | static_cast<uint32_t>(x - c.start));
       }
+    }
+    // Packed row as the kernel builds it: the valid prefix in table order,
+    // in-chunk entries only; a run of equal weight bits starts wherever an
+    // in-chunk entry's weight differs from the previous in-chunk entry's; each
+    // run sorted by local index (insertion sort).
+    std::vector<uint16_t> &pk = c.packed[r];
+    std::vector<uint8_t> run_start;
+    uint32_t prev_w = 0u;
+    for (int32_t j = 0; j < rv; ++j) {
+      const int32_t x = wi_index(row[j]);
+      if (x < c.start || x >= c.end) continue;
+      const uint32_t wb = static_cast<uint32_t>(row[j] >> 32);
+      run_start.push_back(wb != prev_w);
+      prev_w = wb;
+      pk.push_back(static_cast<uint16_t>(x - c.start));
+    }
+    size_t rs = 0;
+    for (size_t i = 1; i < pk.size(); ++i) {
+      if (run_start[i]) {
+        rs = i;
+        continue;
+      }
+      const uint16_t v = pk[i];
+      size_t j = i;
+      while (j > rs && pk[j - 1] > v) {
+        pk[j] = pk[j - 1];
+        --j;
+      }
+      pk[j] = v;
     }
     std::sort(c.rows[r].begin(), c.rows[r].end(), [](uint64_t a, uint64_t b) {
       return (a ^ 0xFFFFFFFFull) > (b ^ 0xFFFFFFFFull);
@@ -149,17 +197,35 @@ struct Out {
 };
 
 // The kernel's walk (csg.hip, `walk`), modes 0 table, 1 single, 2 ahead.
-void walk_kernel(const Chunk &c, int mode, int32_t k, int32_t rows_cap, int32_t entry_cap,
-                 const uint64_t *table, Wave &wv, Out &out, Diag &d) {
+// 64-bit words of the kernel's entries region (greedy_entry_words).
+int32_t entry_words(int32_t entry_cap, int32_t packed_cap) {
+  return entry_cap > (packed_cap + 3) / 4 ? entry_cap : (packed_cap + 3) / 4;
+}
+
+void walk_kernel(const Chunk &c, int mode, bool packed, int32_t k, int32_t rows_cap,
+                 int32_t entry_cap, int32_t packed_cap, const uint64_t *table, Wave &wv,
+                 Out &out, Diag &d) {
   const bool sorted = mode != 0, single = mode == 1, ahead = mode == 2;
-  // LDS: entries u64[entry_cap] | offsets (row headers when sorted) i32[rows_cap + 1].
-  Checked<uint64_t> ent{std::vector<uint64_t>(entry_cap, 0), &d};
+  // LDS: entries u64[entry_words] (or 16-bit ones in the same bytes) |
+  // offsets (row headers when sorted) i32[rows_cap + 1].
+  const int32_t words64 = entry_words(entry_cap, packed_cap);
+  Checked<uint64_t> ent{std::vector<uint64_t>(packed ? 0 : words64, 0), &d};
+  Checked<uint16_t> ent16{std::vector<uint16_t>(packed ? 4 * static_cast<size_t>(words64) : 0, 0),
+                          &d};
   Checked<int32_t> off{std::vector<int32_t>(rows_cap + 1, 0), &d};
   {
     int64_t a = 0;
     for (int32_t r = 0; r < c.size; ++r) {
       off.a[r] = static_cast<int32_t>(a);
-      if (sorted) {
+      if (sorted && packed) {
+        for (size_t j = 0; j < c.packed[r].size(); ++j) {
+          if (a + static_cast<int64_t>(j) < static_cast<int64_t>(ent16.a.size())) {
+            ent16.a[a + j] = c.packed[r][j];
+          } else {
+            d.oob += 1;
+          }
+        }
+      } else if (sorted) {
         for (size_t j = 0; j < c.rows[r].size(); ++j) ent.a[a + j] = c.rows[r][j];
       }
       a += c.in_count[r];
@@ -168,7 +234,9 @@ void walk_kernel(const Chunk &c, int mode, int32_t k, int32_t rows_cap, int32_t 
     if (sorted) {
       for (int32_t r = 0; r < c.size; ++r) {
         const int32_t a0 = off.a[r], b0 = off.a[r + 1] & kOffMask;
-        if (b0 > a0) off.a[r] = a0 | (static_cast<int32_t>(ent.a[a0] & 0xFFFu) << kOffBits);
+        const int32_t first = packed ? static_cast<int32_t>(ent16.get(a0))
+                                     : static_cast<int32_t>(ent.get(a0) & 0xFFFu);
+        if (b0 > a0) off.a[r] = a0 | (first << kOffBits);
       }
     }
   }
@@ -228,8 +296,12 @@ void walk_kernel(const Chunk &c, int mode, int32_t k, int32_t rows_cap, int32_t 
             cl[l] = -1;
             o0[l] = o1[l] = 0;
             if (j < len) {
-              const uint64_t e = ent.get(d0 + j);
-              cl[l] = static_cast<int32_t>(static_cast<uint32_t>(e));
+              if (packed) {
+                cl[l] = static_cast<int32_t>(ent16.get(d0 + j));
+              } else {
+                const uint64_t e = ent.get(d0 + j);
+                cl[l] = static_cast<int32_t>(static_cast<uint32_t>(e));
+              }
               if (ahead) {
                 o0[l] = off.get(cl[l]);
                 o1[l] = off.get(cl[l] + 1);
@@ -571,32 +643,45 @@ extern "C" {
 // Runs the modelled walk over every chunk of `table` (n rows of k packed
 // entries).  `order` receives the permutation (positions a walk did not
 // write keep their previous value); diag[0..5] = overrun, revisit, oob,
-// misread, runaway, steps; mode_counts[0..2] = chunks walked in table,
-// one-entry and sorted mode (variant 0).  Returns 0, or -1 for a variant
-// that does not apply to some chunk.
+// misread, runaway, steps; mode_counts[0..5] = chunks walked in table,
+// one-entry and sorted mode (variant 0), of those in a 16-bit packed form
+// (one-entry, sorted), and chunks taken by the second launch.  packed_cap 0:
+// no packed form and one launch (the wide launch, or statistics asked for).
+// Returns 0, or -1 for a variant that does not apply to some chunk.
 int32_t chain_model(int32_t n, int32_t k, int32_t chunk_size, const uint64_t *table,
-                    int32_t entry_cap, int32_t variant, int32_t inactive_zero, int32_t *order,
-                    int64_t *diag, int64_t *mode_counts) {
+                    int32_t entry_cap, int32_t packed_cap, int32_t variant,
+                    int32_t inactive_zero, int32_t *order, int64_t *diag,
+                    int64_t *mode_counts) {
   Diag d;
   std::vector<uint8_t> seen(static_cast<size_t>(n), 0);
   const int32_t rows_cap = std::min(chunk_size, n);
   Wave wv{inactive_zero != 0, &d};
   const int64_t chunks = (static_cast<int64_t>(n) + chunk_size - 1) / chunk_size;
+  // The host's split (csg.hip, the narrow launch and the packed launch).
+  const int32_t narrow_packed = std::min(packed_cap, 4 * entry_cap);
+  const bool split = packed_cap > narrow_packed;
+  const int64_t band_lo = std::max(entry_cap, narrow_packed);
+  const int64_t band_hi = split ? packed_cap : 0;
   for (int64_t q = 0; q < chunks; ++q) {
     const Chunk c = stage(n, k, chunk_size, q, table);
     Out out{order, &seen, &d, &c};
+    const bool second = split && band_lo < c.valid && c.valid <= band_hi;
+    const int32_t launch_packed = second ? packed_cap : narrow_packed;
+    mode_counts[5] += second;
     const bool compact = c.total <= entry_cap;
+    const bool packed = !compact && c.total <= launch_packed;
     int single_rows = 0, entry_rows = 0;
     for (int32_t r = 0; r < c.size; ++r) {
       single_rows += c.in_count[r] == 1;
       entry_rows += c.in_count[r] > 0;
     }
+    const bool staged = compact || packed;
     int mode;
     if (variant == 0) {
-      mode = !compact ? 0 : (2 * single_rows >= entry_rows ? 1 : 2);
+      mode = !staged ? 0 : (2 * single_rows >= entry_rows ? 1 : 2);
     } else if (variant >= 1 && variant <= 3) {
       mode = variant - 1;
-      if ((mode == 0) == compact) return -1;
+      if ((mode == 0) == staged) return -1;
     } else if (variant == 10) {
       walk_variant(c, k, rows_cap, entry_cap, compact, table, wv, out, d);
       continue;
@@ -604,7 +689,9 @@ int32_t chain_model(int32_t n, int32_t k, int32_t chunk_size, const uint64_t *ta
       return -1;
     }
     mode_counts[mode] += 1;
-    walk_kernel(c, mode, k, rows_cap, entry_cap, table, wv, out, d);
+    if (packed && mode != 0) mode_counts[mode + 2] += 1;
+    walk_kernel(c, mode, packed, k, rows_cap, entry_cap, second ? packed_cap : narrow_packed,
+                table, wv, out, d);
   }
   diag[0] = d.overrun;
   diag[1] = d.revisit;

@@ -7,6 +7,12 @@ inactive source lane returns 0 (measured on MI355X).  With those rules:
 - the kernel's walk, in the mode the kernel picks and in each mode forced,
   gives the oracle's permutation on the test matrices and on full C2, with no
   out-of-chunk write, no row visited twice and no LDS index outside its array;
+- the same holds under the narrow launch's configuration: chunks whose
+  in-chunk entries pass the 2048 staged ones walk 16-bit packed rows (the
+  kernel's packing: table order, runs of equal weight sorted by index), and
+  chunks with 8193..16,384 valid entries go to the second, packed launch;
+  every walk mode (table reads; one-entry and read-ahead on 64-bit and on
+  packed rows) and both launches are reached;
 - a removed variant, whose visited test ran its shuffles only in the lanes
   holding a candidate (`cl >= 0 && !visited(cl)`), reads visited rows as free,
   revisits them and writes past its chunk (its walk loop had no bound): the
@@ -34,19 +40,21 @@ def model(tmp_path_factory):
                     str(HERE / "c" / "chain_model.cpp")], check=True)
     lib = ctypes.CDLL(str(so))
     P = ctypes.c_void_p
-    lib.chain_model.argtypes = [ctypes.c_int32] * 3 + [P] + [ctypes.c_int32] * 3 + [P, P, P]
+    lib.chain_model.argtypes = [ctypes.c_int32] * 3 + [P] + [ctypes.c_int32] * 4 + [P, P, P]
     lib.chain_model.restype = ctypes.c_int32
 
-    def run(table, chunk, entry_cap, variant, inactive_zero=1):
+    def run(table, chunk, entry_cap, variant, inactive_zero=1, packed_cap=0, all_modes=False):
         table = np.ascontiguousarray(table, np.uint64)
         n, k = table.shape
         order = np.full(n, -1, np.int32)
         diag = np.zeros(6, np.int64)
-        modes = np.zeros(3, np.int64)
-        rc = lib.chain_model(n, k, chunk, table.ctypes.data, entry_cap, variant, inactive_zero,
-                             order.ctypes.data, diag.ctypes.data, modes.ctypes.data)
+        modes = np.zeros(6, np.int64)
+        rc = lib.chain_model(n, k, chunk, table.ctypes.data, entry_cap, packed_cap, variant,
+                             inactive_zero, order.ctypes.data, diag.ctypes.data,
+                             modes.ctypes.data)
         keys = ("overrun", "revisit", "oob", "misread", "runaway", "steps")
-        return rc, order, dict(zip(keys, diag.tolist())), modes.tolist()
+        m = modes.tolist()
+        return rc, order, dict(zip(keys, diag.tolist())), (m if all_modes else m[:3])
 
     return run
 
@@ -115,3 +123,65 @@ def test_full_c2(model):
     assert np.array_equal(order, want)
     rc, order, diag, _ = model(table, 1024, 2048, 10, inactive_zero=1)
     assert diag["overrun"] > 1_000_000 and diag["runaway"] > 0
+
+
+# The host's packed capacity for the narrow launch (csg.hip: rows_max * k
+# capped at kPackedCap = 16384, k <= kPackedMaxK = 32, no statistics).
+def host_packed_cap(n, k, chunk):
+    return min(min(chunk, n) * k, 16384) if k <= 32 else 0
+
+
+@pytest.mark.parametrize("name", sorted(MATS))
+@pytest.mark.parametrize("k,chunk", CASES)
+def test_packed_walks_match_oracle(model, name, k, chunk):
+    """The narrow launch's configuration (2048 staged entries, packed rows
+    past that, the packed launch for slices of 8193..16,384 valid entries):
+    every chunk, staged, packed or read from the table, gives the oracle's
+    order in the mode the kernel picks and in each mode forced."""
+    table, want = table_and_order(*MATS[name], k, chunk)
+    pc = host_packed_cap(*table.shape, chunk)
+    rc, order, diag, modes = model(table, chunk, 2048, 0, packed_cap=pc, all_modes=True)
+    assert rc == 0
+    assert {key: diag[key] for key in CLEAN} == CLEAN
+    assert np.array_equal(order, want)
+    forced = [1, 2] if modes[0] == 0 else ([0] if modes[1] == modes[2] == 0 else [])
+    for mode in forced:
+        rc, order, diag, _ = model(table, chunk, 2048, mode + 1, packed_cap=pc)
+        assert rc == 0
+        assert {key: diag[key] for key in CLEAN} == CLEAN
+        assert np.array_equal(order, want), mode
+
+
+def test_packed_modes_and_second_launch_are_exercised(model):
+    """The matrices above reach both packed walk modes and both launches;
+    a grid-ordered stencil (C4n's structure: every slice between 8192 and
+    16,384 valid entries) runs all its chunks in the packed launch."""
+    seen = np.zeros(6, np.int64)
+    for name in sorted(MATS):
+        for k, chunk in CASES:
+            table, _ = table_and_order(*MATS[name], k, chunk)
+            pc = host_packed_cap(*table.shape, chunk)
+            rc, _, _, modes = model(table, chunk, 2048, 0, packed_cap=pc, all_modes=True)
+            assert rc == 0
+            seen += np.array(modes)
+    assert seen[4] > 0 and seen[5] > 0, seen.tolist()  # packed read-ahead walks, second launch
+    # Twin rows (rows 2i and 2i + 1 hold the same two columns): every row has
+    # exactly one in-chunk entry, 4096 per 4096-row chunk, past the 2048
+    # staged entries: the packed one-entry walk.
+    n = 8192
+    ptr = np.arange(0, 2 * n + 1, 2, dtype=np.int32)
+    ind = np.repeat(np.arange(0, n, 2, dtype=np.int32), 2)
+    ind = np.stack([ind, ind + 1], axis=1).reshape(-1).astype(np.int32)
+    table, want = table_and_order(ptr, ind, 8, 4096)
+    rc, order, diag, modes = model(table, 4096, 2048, 0, packed_cap=host_packed_cap(n, 8, 4096),
+                                   all_modes=True)
+    assert rc == 0 and {key: diag[key] for key in CLEAN} == CLEAN
+    assert np.array_equal(order, want)
+    assert modes[3] == 2, modes
+    ptr, ind = synth.stencil7(24, 13, scramble=False)[:2]
+    table, want = table_and_order(ptr, ind, 16, 1024)
+    rc, order, diag, modes = model(table, 1024, 2048, 0, packed_cap=16384, all_modes=True)
+    assert rc == 0 and {key: diag[key] for key in CLEAN} == CLEAN
+    assert np.array_equal(order, want)
+    chunks = -(-table.shape[0] // 1024)
+    assert modes[3] + modes[4] == chunks and modes[5] >= chunks - 1, modes
