@@ -128,6 +128,7 @@ SIGNATURES = {
         [vp, i32, i32, vp, vp, ctypes.c_bool, i32, f32, i32, vp, vp], None),
     "sporder_spmm_csr": ([vp, i32, i32, vp, vp, vp, i32, vp, vp, i32, P(f32)], None),
     "sporder_spmm_csr_noalloc": ([vp, i32, i32, vp, vp, vp, i32, vp, vp], i32),
+    "sporder_spmm_csr_scaled": ([vp, i32, i32, vp, vp, vp, i32, vp, vp, vp, vp, P(f32)], None),
     "sporder_spmm_plan_create": ([vp, i32, i32, vp, vp, P(SpmmPlanInfo)], vp),
     "sporder_spmm_plan_destroy": ([vp], None),
     "sporder_spmm_csr_plan": ([vp, vp, i32, i32, vp, vp, vp, i32, vp, vp, P(f32)], None),

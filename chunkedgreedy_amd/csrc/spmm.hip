@@ -68,25 +68,40 @@ __device__ __forceinline__ void register_row(LongCtl *ctl, LongRow *longs, int32
   for (int32_t q = 0; q < nseg; ++q) owner[base + q] = id;
 }
 
+__device__ __forceinline__ float4 scale4(float d, float4 v) {
+  return make_float4(d * v.x, d * v.y, d * v.z, d * v.w);
+}
+
+// The row scale applied to a finished row (rs null: none), rounded once per
+// element: the value an elementwise product of the result would hold.
+__device__ __forceinline__ float4 row_scaled(const float *__restrict__ rs, int64_t row, float4 v) {
+  return rs != nullptr ? scale4(rs[row], v) : v;
+}
+
 // A[s, e) x B on the group's float4 column slice col0 (col_ok false: lanes
 // past N).  Every lane of the wave calls it together; groups with different
 // ranges iterate until the longest is done.  Accumulates fmaf in CSR order
-// starting from 0.0f.
-template <int G>
+// starting from 0.0f.  With CS the B row gathered for nonzero p is first
+// multiplied by cs[p] (the scale of that nonzero's column, streamed beside
+// the values), cs[p] * B[col][j] rounded once: the value an elementwise
+// product of B by a column-scale vector would hold.
+template <int G, bool CS>
 __device__ __forceinline__ float4 group_dot(int32_t s, int32_t e, const int32_t *__restrict__ ind,
                                             const float *__restrict__ val, int32_t N,
                                             int32_t col0, bool col_ok,
-                                            const float *__restrict__ B, int gl, int gbase) {
+                                            const float *__restrict__ B, int gl, int gbase,
+                                            const float *__restrict__ cs) {
   constexpr int U = kSpmmDepth;
   float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   for (int32_t pb = s;; pb += G) {
     const int32_t rem = e - pb;
     if (ballot(rem > 0) == 0) break;
     int32_t my_c = 0;
-    float my_v = 0.0f;
+    float my_v = 0.0f, my_d = 1.0f;
     if (gl < rem) {
       my_c = __builtin_nontemporal_load(ind + pb + gl);
       my_v = __builtin_nontemporal_load(val + pb + gl);
+      if constexpr (CS) my_d = __builtin_nontemporal_load(cs + pb + gl);
     }
     const int32_t cnt = rem < G ? rem : G;
     // Wave maximum of cnt bounds the broadcast loop.
@@ -94,7 +109,7 @@ __device__ __forceinline__ float4 group_dot(int32_t s, int32_t e, const int32_t 
         wave_max_u32(static_cast<uint32_t>(cnt > 0 ? cnt : 0)));
     for (int32_t t = 0; t < cmax; t += U) {
       int32_t c[U];
-      float v[U];
+      float v[U], d[U];
       float4 b[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
@@ -107,9 +122,16 @@ __device__ __forceinline__ float4 group_dot(int32_t s, int32_t e, const int32_t 
           b[u] = *reinterpret_cast<const float4 *>(B + static_cast<int64_t>(c[u]) * N + col0);
         }
       }
+      // Each lane loaded its own nonzero's column scale; it is shared out only
+      // after the B rows are requested, so the gathers do not wait for it.
+      if constexpr (CS) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) d[u] = __shfl(my_d, gbase + ((t + u) & (G - 1)), kWave);
+      }
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         if (t + u < cnt && col_ok) {
+          if constexpr (CS) b[u] = scale4(d[u], b[u]);
           acc.x = fmaf(v[u], b[u].x, acc.x);
           acc.y = fmaf(v[u], b[u].y, acc.y);
           acc.z = fmaf(v[u], b[u].z, acc.z);
@@ -132,15 +154,17 @@ __device__ __forceinline__ void store_nt(float *dst, float4 v) {
 // stride).  Rows longer than kLongRow are registered in `longs` for the
 // segment launch (when `longs` is null every row is done here, in one chain).
 // C is written with non-temporal stores: it is not read again by this launch
-// and would only evict B from the caches.
-template <int G>
+// and would only evict B from the caches.  rs / cs (CS): the row scales and
+// the per-nonzero column scales of a scaled product (null rs: none).
+template <int G, bool CS>
 __global__ void __launch_bounds__(kSpmmBlock)
     spmm_rowsplit_v4(int32_t n, const int32_t *__restrict__ ptr,
                      const int32_t *__restrict__ ind,
                      const float *__restrict__ val, int32_t N,
                      const float *__restrict__ B, float *__restrict__ C,
                      LongCtl *ctl, LongRow *longs, int32_t *owner,
-                     const int32_t *__restrict__ tiles, int64_t ntiles) {
+                     const int32_t *__restrict__ tiles, int64_t ntiles,
+                     const float *__restrict__ rs, const float *__restrict__ cs) {
   constexpr int kRowsPerWave = kWave / G;
   const int lane = lane_id();
   const int sub = lane / G;  // row slot within the wave
@@ -173,8 +197,8 @@ __global__ void __launch_bounds__(kSpmmBlock)
   }
   for (int32_t col0 = gl * 4; col0 - gl * 4 < N; col0 += G * 4) {
     const bool col_ok = col0 < N;
-    const float4 acc = group_dot<G>(s, e, ind, val, N, col0, col_ok, B, gl, gbase);
-    if (row_ok && col_ok && !is_long) store_nt(C + row * N + col0, acc);
+    const float4 acc = group_dot<G, CS>(s, e, ind, val, N, col0, col_ok, B, gl, gbase, cs);
+    if (row_ok && col_ok && !is_long) store_nt(C + row * N + col0, row_scaled(rs, row, acc));
   }
 }
 
@@ -185,12 +209,13 @@ __global__ void __launch_bounds__(kSpmmBlock)
 // fmaf chain in CSR order.  Row bounds come from one coalesced load of the
 // wave's 65 row pointers; rows longer than kLongRow are registered for the
 // segment launch as in spmm_rowsplit_v4.
-template <int G>
+template <int G, bool CS>
 __global__ void __launch_bounds__(kSpmmBlock)
     spmm_rows_dyn(int32_t n, const int32_t *__restrict__ ptr, const int32_t *__restrict__ ind,
                   const float *__restrict__ val, int32_t N, const float *__restrict__ B,
                   float *__restrict__ C, LongCtl *ctl, LongRow *longs, int32_t *owner,
-                  const int32_t *__restrict__ tiles, int64_t ntiles) {
+                  const int32_t *__restrict__ tiles, int64_t ntiles,
+                  const float *__restrict__ rs, const float *__restrict__ cs) {
   static_assert(kTileRows == kWave, "a wave owns one tile");
   constexpr int U = kSpmmDepth;
   constexpr int RPW = kWave / G;
@@ -238,7 +263,9 @@ __global__ void __launch_bounds__(kSpmmBlock)
     // the wave's rows are used up.
     while (true) {
       const bool fin = row >= 0 && p >= e;
-      if (fin && !is_long && col_ok) store_nt(C + (r0 + row) * N + col0, acc);
+      if (fin && !is_long && col_ok) {
+        store_nt(C + (r0 + row) * N + col0, row_scaled(rs, r0 + row, acc));
+      }
       const uint64_t fmask = ballot(fin && gl == 0);
       if (fmask == 0) break;
       const int32_t rank = __popcll(fmask & ((1ull << gbase) - 1ull));
@@ -262,16 +289,17 @@ __global__ void __launch_bounds__(kSpmmBlock)
     // One step: up to G nonzeros per group, U B rows in flight.
     const int32_t rem = row >= 0 ? e - p : 0;
     int32_t my_c = 0;
-    float my_v = 0.0f;
+    float my_v = 0.0f, my_d = 1.0f;
     if (gl < rem) {
       my_c = __builtin_nontemporal_load(ind + p + gl);
       my_v = __builtin_nontemporal_load(val + p + gl);
+      if constexpr (CS) my_d = __builtin_nontemporal_load(cs + p + gl);
     }
     const int32_t cnt = rem < G ? rem : G;
     const int32_t cmax = static_cast<int32_t>(wave_max_u32(static_cast<uint32_t>(cnt)));
     for (int32_t t = 0; t < cmax; t += U) {
       int32_t c[U];
-      float v[U];
+      float v[U], d[U];
       float4 bv[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
@@ -284,9 +312,14 @@ __global__ void __launch_bounds__(kSpmmBlock)
           bv[u] = *reinterpret_cast<const float4 *>(B + static_cast<int64_t>(c[u]) * N + col0);
         }
       }
+      if constexpr (CS) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) d[u] = __shfl(my_d, gbase + ((t + u) & (G - 1)), kWave);
+      }
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         if (t + u < cnt && col_ok) {
+          if constexpr (CS) bv[u] = scale4(d[u], bv[u]);
           acc.x = fmaf(v[u], bv[u].x, acc.x);
           acc.y = fmaf(v[u], bv[u].y, acc.y);
           acc.z = fmaf(v[u], bv[u].z, acc.z);
@@ -304,13 +337,13 @@ __global__ void __launch_bounds__(kSpmmBlock)
 // next launch: handing them over inside this one would need a device-scope
 // release/acquire per unit, which on MI355X writes back and invalidates the
 // XCD's L2 and so evicts every other wave's B rows.
-template <int G>
+template <int G, bool CS>
 __global__ void __launch_bounds__(kSpmmBlock)
     spmm_long_segments(const int32_t *__restrict__ ptr, const int32_t *__restrict__ ind,
                        const float *__restrict__ val, int32_t N,
                        const float *__restrict__ B, const LongCtl *__restrict__ ctl,
                        const LongRow *__restrict__ longs, const int32_t *__restrict__ owner,
-                       float *__restrict__ part) {
+                       float *__restrict__ part, const float *__restrict__ cs) {
   constexpr int kRowsPerWave = kWave / G;
   const int lane = lane_id();
   const int sub = lane / G, gl = lane % G, gbase = sub * G;
@@ -329,18 +362,19 @@ __global__ void __launch_bounds__(kSpmmBlock)
     }
     for (int32_t col0 = gl * 4; col0 - gl * 4 < N; col0 += G * 4) {
       const bool col_ok = col0 < N;
-      const float4 acc = group_dot<G>(s, e, ind, val, N, col0, col_ok, B, gl, gbase);
+      const float4 acc = group_dot<G, CS>(s, e, ind, val, N, col0, col_ok, B, gl, gbase, cs);
       if (ok && col_ok) *reinterpret_cast<float4 *>(part + u * N + col0) = acc;
     }
   }
 }
 
 // C[row] = ((P_0 + P_1) + P_2) + ... for each long row, one row group per row,
-// eight partial rows in flight.
+// eight partial rows in flight; then the row scale (rs null: none).
 template <int G>
 __global__ void __launch_bounds__(kSpmmBlock)
     spmm_long_fixup(int32_t N, float *__restrict__ C, const LongCtl *__restrict__ ctl,
-                    const LongRow *__restrict__ longs, const float *__restrict__ part) {
+                    const LongRow *__restrict__ longs, const float *__restrict__ part,
+                    const float *__restrict__ rs) {
   constexpr int kRowsPerWave = kWave / G;
   const int lane = lane_id();
   const int sub = lane / G, gl = lane % G;
@@ -373,7 +407,7 @@ __global__ void __launch_bounds__(kSpmmBlock)
         sum.z = sum.z + v.z;
         sum.w = sum.w + v.w;
       }
-      store_nt(C + static_cast<int64_t>(lr.row) * N + col0, sum);
+      store_nt(C + static_cast<int64_t>(lr.row) * N + col0, row_scaled(rs, lr.row, sum));
     }
   }
 }
@@ -385,7 +419,9 @@ __global__ void __launch_bounds__(kSpmmBlock)
     spmm_rowsplit_scalar(int32_t n, const int32_t *__restrict__ ptr,
                          const int32_t *__restrict__ ind,
                          const float *__restrict__ val, int32_t N,
-                         const float *__restrict__ B, float *__restrict__ C) {
+                         const float *__restrict__ B, float *__restrict__ C,
+                         const float *__restrict__ rs = nullptr,
+                         const float *__restrict__ cs = nullptr) {
   const int lane = lane_id();
   const int64_t wave0 =
       (blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x) / kWave;
@@ -399,11 +435,12 @@ __global__ void __launch_bounds__(kSpmmBlock)
         const int32_t q1 = q0 + seg < e ? q0 + seg : e;
         float acc = 0.0f;
         for (int32_t p = q0; p < q1; ++p) {
-          acc = fmaf(val[p], B[static_cast<int64_t>(ind[p]) * N + j], acc);
+          const float b = B[static_cast<int64_t>(ind[p]) * N + j];
+          acc = fmaf(val[p], cs != nullptr ? cs[p] * b : b, acc);
         }
         sum = (q0 == s) ? acc : sum + acc;
       }
-      C[row * N + j] = sum;
+      C[row * N + j] = rs != nullptr ? rs[row] * sum : sum;
     }
   }
 }
@@ -650,6 +687,14 @@ __global__ void fill_uniform(int64_t count, float *__restrict__ vals, uint64_t s
 // Workspace of the long-row segments for an n x n CSR with nnz nonzeros and
 // N columns: descriptors, unit owners and unit partials, sized for the most
 // long rows and segments nnz nonzeros allow.
+// Scales of a scaled product diag(row) A diag(col) B: `row` holds n row
+// scales, `col` nnz per-nonzero column scales (col[p] = the scale of column
+// ind[p]); null: no scale on that side.
+struct SpmmScale {
+  const float *row = nullptr;
+  const float *col = nullptr;
+};
+
 struct SpmmLongWs {
   LongCtl *ctl;
   LongRow *longs;
@@ -669,11 +714,12 @@ SpmmLongWs take_long_ws(Context &ctx, int32_t nnz, int32_t N) {
   return w;
 }
 
-template <int G>
-void launch_rowsplit_g(Context &ctx, int32_t n, int32_t nnz, const int32_t *ptr,
-                       const int32_t *ind, const float *val, int32_t N, const float *B,
-                       float *C, const SpmmLongWs &w, int64_t seg_cap, int64_t long_cap,
-                       const int32_t *tiles, int64_t ntiles) {
+template <int G, bool CS>
+void launch_rowsplit_gs(Context &ctx, int32_t n, int32_t nnz, const int32_t *ptr,
+                        const int32_t *ind, const float *val, int32_t N, const float *B,
+                        float *C, const SpmmLongWs &w, int64_t seg_cap, int64_t long_cap,
+                        const int32_t *tiles, int64_t ntiles, const float *rs,
+                        const float *cs) {
   constexpr int rpw = kWave / G;
   // Without a long-row workspace (a plan found no row past kLongRow) the row
   // launch computes every row and the segment launches are not made.
@@ -687,23 +733,38 @@ void launch_rowsplit_g(Context &ctx, int32_t n, int32_t nnz, const int32_t *ptr,
   if (G <= 8 && N <= 4 * G) {
     const int64_t dyn_waves = tiles == nullptr ? ceil_div64(n, kWave) : ntiles;
     const int64_t blocks = ceil_div64(dyn_waves, kSpmmWaves);
-    spmm_rows_dyn<G><<<dim3(static_cast<unsigned>(blocks)), kSpmmBlock, 0, ctx.stream>>>(
-        n, ptr, ind, val, N, B, C, w.ctl, w.longs, w.owner, tiles, ntiles);
+    spmm_rows_dyn<G, CS><<<dim3(static_cast<unsigned>(blocks)), kSpmmBlock, 0, ctx.stream>>>(
+        n, ptr, ind, val, N, B, C, w.ctl, w.longs, w.owner, tiles, ntiles, rs, cs);
   } else {
     const int64_t blocks = ceil_div64(waves, kSpmmWaves);
-    spmm_rowsplit_v4<G><<<dim3(static_cast<unsigned>(blocks)), kSpmmBlock, 0, ctx.stream>>>(
-        n, ptr, ind, val, N, B, C, w.ctl, w.longs, w.owner, tiles, ntiles);
+    spmm_rowsplit_v4<G, CS><<<dim3(static_cast<unsigned>(blocks)), kSpmmBlock, 0,
+                              ctx.stream>>>(n, ptr, ind, val, N, B, C, w.ctl, w.longs,
+                                            w.owner, tiles, ntiles, rs, cs);
   }
   SP_LAUNCH_CHECK();
   if (!long_rows) return;
   // Persistent grid over the registered segment units (none: exits at once).
   const int g = ctx.grid_for(ceil_div64(seg_cap, rpw * kSpmmWaves), kSpmmBlock, 2);
-  spmm_long_segments<G><<<g, kSpmmBlock, 0, ctx.stream>>>(ptr, ind, val, N, B, w.ctl,
-                                                            w.longs, w.owner, w.part);
+  spmm_long_segments<G, CS><<<g, kSpmmBlock, 0, ctx.stream>>>(ptr, ind, val, N, B, w.ctl,
+                                                                w.longs, w.owner, w.part, cs);
   SP_LAUNCH_CHECK();
   const int gf = ctx.grid_for(ceil_div64(long_cap, rpw * kSpmmWaves), kSpmmBlock, 2);
-  spmm_long_fixup<G><<<gf, kSpmmBlock, 0, ctx.stream>>>(N, C, w.ctl, w.longs, w.part);
+  spmm_long_fixup<G><<<gf, kSpmmBlock, 0, ctx.stream>>>(N, C, w.ctl, w.longs, w.part, rs);
   SP_LAUNCH_CHECK();
+}
+
+template <int G>
+void launch_rowsplit_g(Context &ctx, int32_t n, int32_t nnz, const int32_t *ptr,
+                       const int32_t *ind, const float *val, int32_t N, const float *B,
+                       float *C, const SpmmLongWs &w, int64_t seg_cap, int64_t long_cap,
+                       const int32_t *tiles, int64_t ntiles, const SpmmScale &sc) {
+  if (sc.col != nullptr) {
+    launch_rowsplit_gs<G, true>(ctx, n, nnz, ptr, ind, val, N, B, C, w, seg_cap, long_cap,
+                                tiles, ntiles, sc.row, sc.col);
+  } else {
+    launch_rowsplit_gs<G, false>(ctx, n, nnz, ptr, ind, val, N, B, C, w, seg_cap, long_cap,
+                                 tiles, ntiles, sc.row, nullptr);
+  }
 }
 
 } // namespace
@@ -715,11 +776,13 @@ size_t spmm_ws_bytes(int32_t nnz, int32_t N) {
 }
 
 // Row-split SpMM in the stated order.  `w` holds room for `long_cap` long rows
-// and `seg_cap` segments (take_long_ws: the most nnz nonzeros allow).
+// and `seg_cap` segments (take_long_ws: the most nnz nonzeros allow).  `sc`:
+// the scales of a scaled product (SpmmScale; null: none).
 void spmm_rowsplit(Context &ctx, int32_t n, int32_t nnz, const int32_t *ptr,
                    const int32_t *ind, const float *val, int32_t N, const float *B, float *C,
                    const SpmmLongWs &w, int64_t seg_cap = -1, int64_t long_cap = -1,
-                   const int32_t *tiles = nullptr, int64_t ntiles = 0) {
+                   const int32_t *tiles = nullptr, int64_t ntiles = 0,
+                   const SpmmScale &sc = SpmmScale{}) {
   if (seg_cap < 0) seg_cap = max_segments(nnz);
   if (long_cap < 0) long_cap = max_long_rows(nnz);
   bool aligned = (N % 4 == 0) && (reinterpret_cast<uintptr_t>(B) % 16 == 0) &&
@@ -727,32 +790,33 @@ void spmm_rowsplit(Context &ctx, int32_t n, int32_t nnz, const int32_t *ptr,
   if (!aligned) {
     SP_EXPECT(tiles == nullptr, "internal: tile lists need aligned float4 operands");
     int g = ctx.grid_for(ceil_div64(n, kSpmmBlock / kWave), kSpmmBlock, 8);
-    spmm_rowsplit_scalar<<<g, kSpmmBlock, 0, ctx.stream>>>(n, ptr, ind, val, N, B, C);
+    spmm_rowsplit_scalar<<<g, kSpmmBlock, 0, ctx.stream>>>(n, ptr, ind, val, N, B, C, sc.row,
+                                                           sc.col);
     SP_LAUNCH_CHECK();
     return;
   }
   int32_t q = N / 4; // float4 columns
   if (q <= 1) {
     launch_rowsplit_g<1>(ctx, n, nnz, ptr, ind, val, N, B, C, w, seg_cap, long_cap,
-                          tiles, ntiles);
+                          tiles, ntiles, sc);
   } else if (q <= 2) {
     launch_rowsplit_g<2>(ctx, n, nnz, ptr, ind, val, N, B, C, w, seg_cap, long_cap,
-                          tiles, ntiles);
+                          tiles, ntiles, sc);
   } else if (q <= 4) {
     launch_rowsplit_g<4>(ctx, n, nnz, ptr, ind, val, N, B, C, w, seg_cap, long_cap,
-                          tiles, ntiles);
+                          tiles, ntiles, sc);
   } else if (q <= 8) {
     launch_rowsplit_g<8>(ctx, n, nnz, ptr, ind, val, N, B, C, w, seg_cap, long_cap,
-                          tiles, ntiles);
+                          tiles, ntiles, sc);
   } else if (q <= 16) {
     launch_rowsplit_g<16>(ctx, n, nnz, ptr, ind, val, N, B, C, w, seg_cap, long_cap,
-                          tiles, ntiles);
+                          tiles, ntiles, sc);
   } else if (q <= 32) {
     launch_rowsplit_g<32>(ctx, n, nnz, ptr, ind, val, N, B, C, w, seg_cap, long_cap,
-                          tiles, ntiles);
+                          tiles, ntiles, sc);
   } else {
     launch_rowsplit_g<64>(ctx, n, nnz, ptr, ind, val, N, B, C, w, seg_cap, long_cap,
-                          tiles, ntiles);
+                          tiles, ntiles, sc);
   }
 }
 
@@ -982,6 +1046,29 @@ void sporder_spmm_csr(sporder_context_t h, int32_t n, int32_t nnz,
     const SpmmLongWs w = take_long_ws(ctx, nnz, cols);
     spmm_rowsplit(ctx, n, nnz, d_ptr, d_ind, d_val, cols, d_b, d_c, w);
   }
+  t.end(ctx.stream);
+  ctx.sync();
+  if (kernel_ms) *kernel_ms = t.ms();
+  t.destroy();
+}
+
+void sporder_spmm_csr_scaled(sporder_context_t h, int32_t n, int32_t nnz,
+                             const int32_t *d_ptr, const int32_t *d_ind, const float *d_val,
+                             int32_t cols, const float *d_b, const float *d_row_scale,
+                             const float *d_nz_col_scale, float *d_c, float *kernel_ms) {
+  SP_EXPECT(h != nullptr, "null context");
+  SP_EXPECT(n >= 1 && nnz >= 0, "expect n >= 1 and nnz >= 0");
+  SP_EXPECT(cols >= 1, "cols must be >= 1");
+  Context &ctx = h->impl;
+  EventSpan t;
+  t.create(kernel_ms != nullptr);
+  ctx.reserve(spmm_ws_bytes(nnz, cols));
+  t.begin(ctx.stream);
+  const SpmmLongWs w = take_long_ws(ctx, nnz, cols);
+  SpmmScale sc;
+  sc.row = d_row_scale;
+  sc.col = d_nz_col_scale;
+  spmm_rowsplit(ctx, n, nnz, d_ptr, d_ind, d_val, cols, d_b, d_c, w, -1, -1, nullptr, 0, sc);
   t.end(ctx.stream);
   ctx.sync();
   if (kernel_ms) *kernel_ms = t.ms();

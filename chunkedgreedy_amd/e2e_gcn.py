@@ -20,6 +20,11 @@ op(x) = d^-1/2 * (A @ (d^-1/2 * x)); h1 = relu(op(X W1)), z = op(h1) W2,
 cross-entropy against uniform random labels, Adam (lr 0.01).  A is symmetric,
 so the backward of op is op itself: 4 SpMMs of width `hidden` per epoch.
 
+With --fused-scaling the operator is one call of
+``sporder.spmm_csr_scaled`` (the two d^-1/2 products applied inside the
+SpMM: the same values bit for bit, without the two elementwise passes); the
+default keeps the reference driver's three steps.
+
 Usage:  python -m chunkedgreedy_amd.e2e_gcn [--nodes N] [--epochs E] ...
 prints one JSON record per ordering (ORIGIN and sporder-csg by default;
 sporder-cg on request).
@@ -41,9 +46,10 @@ def _sync_ms(torch, t0: float) -> float:
 
 
 class GraphOp:
-    """x -> d^-1/2 * (A @ (d^-1/2 * x)) on one GPU, timing each SpMM."""
+    """x -> d^-1/2 * (A @ (d^-1/2 * x)) on one GPU, timing each SpMM.  With
+    `fused` one scaled SpMM call (bit-identical to the three steps)."""
 
-    def __init__(self, ptr, ind, ctx=None):
+    def __init__(self, ptr, ind, ctx=None, fused=False):
         import torch
 
         from chunkedgreedy_amd import sporder
@@ -54,9 +60,18 @@ class GraphOp:
         self.val = torch.ones(ind.numel(), dtype=torch.float32, device=ind.device)
         deg = (ptr[1:] - ptr[:-1]).to(torch.float32).clamp_min(1.0)
         self.dinv = deg.rsqrt().unsqueeze(1)
+        self.fused = fused
+        # The fused call's column scales per nonzero, d^-1/2[ind], once.
+        self.nz_scale = self.dinv.view(-1)[ind.long()] if fused else None
         self.spmm_ms = 0.0
 
     def __call__(self, x):
+        if self.fused:
+            out, ms = self.sporder.spmm_csr_scaled(self.ptr, self.ind, self.val, x.contiguous(),
+                                                   row_scale=self.dinv.view(-1),
+                                                   nz_col_scale=self.nz_scale, ctx=self.ctx)
+            self.spmm_ms += ms
+            return out
         out, ms = self.sporder.spmm_csr(self.ptr, self.ind, self.val,
                                         (self.dinv * x).contiguous(), ctx=self.ctx)
         self.spmm_ms += ms
@@ -82,14 +97,14 @@ def _spmm_fn():
 
 
 def train(ptr, ind, X, y, *, hidden: int, classes: int, epochs: int, warmup: int = 3,
-          seed: int = 0, ctx=None) -> dict:
+          seed: int = 0, ctx=None, fused: bool = False) -> dict:
     """Train the 2-layer GCN for `epochs` timed epochs after `warmup` untimed
     ones; returns per-epoch times, SpMM time per epoch and the losses."""
     import torch
     import torch.nn.functional as F
 
     t0 = time.perf_counter()
-    op = GraphOp(ptr, ind, ctx=ctx)
+    op = GraphOp(ptr, ind, ctx=ctx, fused=fused)
     prep_ms = _sync_ms(torch, t0)
     SpMMFn = _spmm_fn()
     torch.manual_seed(seed)
@@ -133,7 +148,7 @@ def permute_graph(ptr, ind, X, y, order, ctx=None):
 
 
 def run(ptr_h, ind_h, *, features: int, hidden: int, classes: int, epochs: int,
-        orders=("ORIGIN", "sporder-csg"), seed: int = 0) -> list[dict]:
+        orders=("ORIGIN", "sporder-csg"), seed: int = 0, fused: bool = False) -> list[dict]:
     import torch
 
     from chunkedgreedy_amd import sporder
@@ -167,9 +182,10 @@ def run(ptr_h, ind_h, *, features: int, hidden: int, classes: int, epochs: int,
             ptr_u, ind_u, X, y = permute_graph(ptr, ind, X0, y0, order, ctx=ctx)
             perm_ms = _sync_ms(torch, t0)
         r = train(ptr_u, ind_u, X, y, hidden=hidden, classes=classes, epochs=epochs, seed=seed,
-                  ctx=ctx)
+                  ctx=ctx, fused=fused)
         total = reorder_ms + perm_ms + r["prep_ms"] + epochs * r["epoch_ms"]
-        rows.append({"order": name, "n": n, "nnz": int(ind_h.shape[0]), "features": features,
+        rows.append({"order": name, "fused_scaling": fused, "n": n, "nnz": int(ind_h.shape[0]),
+                     "features": features,
                      "hidden": hidden, "classes": classes, "epochs": epochs,
                      "reorder_ms": round(reorder_ms, 3), "perm_ms": round(perm_ms, 3),
                      "prep_ms": round(r["prep_ms"], 3), "epoch_ms": round(r["epoch_ms"], 3),
@@ -204,6 +220,9 @@ def main(argv=None) -> int:
     ap.add_argument("--degree-order", action="store_true",
                     help="vertices in expected-degree order (synth LOCALITY C5d) "
                     "instead of the scrambled ids of configuration C5")
+    ap.add_argument("--fused-scaling", action="store_true",
+                    help="apply d^-1/2 on both sides inside the SpMM (spmm_csr_scaled) "
+                    "instead of as two elementwise products around it")
     args = ap.parse_args(argv)
 
     import torch
@@ -221,7 +240,8 @@ def main(argv=None) -> int:
           f"{time.time() - t0:.1f}s)", file=sys.stderr, flush=True)
     for row in run(ptr_h, ind_h, features=args.features, hidden=args.hidden,
                    classes=args.classes, epochs=args.epochs,
-                   orders=tuple(args.orders.split(",")), seed=args.seed):
+                   orders=tuple(args.orders.split(",")), seed=args.seed,
+                   fused=args.fused_scaling):
         print(json.dumps(row), flush=True)
     return 0
 

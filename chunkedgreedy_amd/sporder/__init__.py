@@ -27,6 +27,7 @@ from ._sporder import similarity_graph as _similarity_graph
 from ._sporder import similarity_graph_exact as _similarity_graph_exact
 from ._sporder import spmm_csr as _spmm_csr
 from ._sporder import spmm_csr_noalloc as _spmm_csr_noalloc
+from ._sporder import spmm_csr_scaled as _spmm_csr_scaled
 from ._sporder import SpmmPlan
 
 __all__ = [
@@ -42,6 +43,7 @@ __all__ = [
     "similarity_graph_exact",
     "spmm_csr",
     "spmm_csr_noalloc",
+    "spmm_csr_scaled",
     "spmm_plan",
     "SpmmPlan",
 ]
@@ -176,6 +178,21 @@ def spmm_csr(ptr, ind, val, B, *, out=None, algo="row_split", ctx=None, plan=Non
     and the others run the row-split; the result equals "row_split" bit for
     bit.  Returns (C, kernel_ms)."""
     return _spmm_csr(ptr, ind, val, B, out=out, algo=algo, ctx=ctx, plan=plan)
+
+
+def spmm_csr_scaled(ptr, ind, val, B, *, row_scale=None, col_scale=None, nz_col_scale=None,
+                    out=None, ctx=None):
+    """(new) C = diag(row_scale) A diag(col_scale) B in the row-split's stated
+    order, with each gathered B row multiplied by its column's scale and each
+    finished row by its row scale (one fp32 multiply per element each): equal,
+    bit for bit, to ``row_scale[:, None] * spmm_csr(ptr, ind, val,
+    col_scale[:, None] * B)[0]`` without the two elementwise passes (a GCN's
+    D^-1/2 A D^-1/2, applied around the SpMM as experiments/e2e_gcn.py:117-123
+    does).  The kernels read the column scales per nonzero, col_scale[ind]:
+    give them as ``nz_col_scale`` to reuse them across calls on one pattern.
+    Either scale may be None.  Returns (C, kernel_ms)."""
+    return _spmm_csr_scaled(ptr, ind, val, B, row_scale=row_scale, col_scale=col_scale,
+                            nz_col_scale=nz_col_scale, out=out, ctx=ctx)
 
 
 def spmm_csr_noalloc(ptr, ind, val, B, *, out, ctx=None):

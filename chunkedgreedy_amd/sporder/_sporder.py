@@ -377,6 +377,57 @@ def spmm_csr(ptr, ind, val, B, out=None, algo="row_split", ctx=None, plan=None):
     return out, ms.value
 
 
+def spmm_csr_scaled(ptr, ind, val, B, row_scale=None, col_scale=None, nz_col_scale=None,
+                    out=None, ctx=None):
+    """C = diag(row_scale) A diag(col_scale) B with the row-split kernels (new
+    export).  Bit-identical to (row_scale[:, None] * spmm_csr(A,
+    col_scale[:, None] * B)); either scale may be None.  The kernels take the
+    column scales per nonzero (col_scale[ind]): pass them as nz_col_scale to
+    skip that gather when the pattern is reused.  Returns (C, kernel_ms)."""
+    ptr = _gpu_in(ptr, torch.int32, "ptr")
+    ind = _gpu_in(ind, torch.int32, "ind")
+    val = _gpu_in(val, torch.float32, "val")
+    n, nnz = _sizes(ptr, ind)
+    if val.numel() != nnz:
+        raise ValueError("val must have length nnz")
+    B = _as_tensor(B, "B")
+    if not B.is_cuda or B.dtype != torch.float32 or B.dim() != 2 or B.shape[0] != n:
+        raise ValueError("B must be an (n, N) float32 GPU tensor")
+    B = B.contiguous()
+    cols = B.shape[1]
+    if cols < 1:
+        raise ValueError("B must have at least one column")
+
+    def checked(name, sc, length):
+        sc = _as_tensor(sc, name)
+        if not sc.is_cuda or sc.dtype != torch.float32 or sc.numel() != length \
+                or sc.device != B.device:
+            raise ValueError(f"{name} must be {length} float32 values on B's device")
+        return sc.reshape(length).contiguous()
+
+    rs = None if row_scale is None else checked("row_scale", row_scale, n)
+    if nz_col_scale is not None:
+        if col_scale is not None:
+            raise ValueError("give col_scale or nz_col_scale, not both")
+        nz = checked("nz_col_scale", nz_col_scale, nnz)
+    elif col_scale is not None:
+        nz = checked("col_scale", col_scale, n)[ind.long()] if nnz else \
+            torch.empty(0, dtype=torch.float32, device=B.device)
+    else:
+        nz = None
+    if out is None:
+        out = torch.empty((n, cols), dtype=torch.float32, device=B.device)
+    elif out.shape != (n, cols) or out.dtype != torch.float32 or not out.is_contiguous():
+        raise ValueError("out must be a contiguous (n, N) float32 tensor")
+    c = _resolve(ctx, ptr)
+    ms = ctypes.c_float(0.0)
+    c._lib.sporder_spmm_csr_scaled(c.handle, n, nnz, _addr(ptr), _addr(ind), _addr(val), cols,
+                                   _addr(B), _addr(rs) if rs is not None else None,
+                                   _addr(nz) if nz is not None and nz.numel() else None,
+                                   _addr(out), ctypes.byref(ms))
+    return out, ms.value
+
+
 def spmm_csr_noalloc(ptr, ind, val, B, out, ctx=None):
     """C = A @ B into the caller's `out` with no device allocation by the
     library (new export, the row-split in the stated order).  Raises

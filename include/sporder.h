@@ -299,6 +299,30 @@ SPORDER_API void sporder_spmm_csr(sporder_context_t ctx, int32_t n,
                                   sporder_spmm_algo_t algo, float *kernel_ms);
 
 /*
+ * (new) C = diag(row_scale) A diag(col_scale) B with the row-split kernels.
+ * It has no counterpart in the reference: it is for callers that scale the
+ * product on both sides, such as a GCN's symmetric normalisation
+ * D^-1/2 A D^-1/2, which the reference driver applies as two elementwise
+ * products around the SpMM (experiments/e2e_gcn.py:117-123).  The column
+ * scales come per nonzero, d_nz_col_scale[p] = col_scale[d_ind[p]] (nnz
+ * floats, streamed beside d_val; a caller whose pattern does not change
+ * computes it once), and d_row_scale holds n floats.  The B row gathered for
+ * nonzero p is multiplied by d_nz_col_scale[p] (one fp32 multiply per
+ * element) before its fmaf, and each finished row by its row scale, so the
+ * result equals, bit for bit, B' = col_scale (.) B, C' = sporder_spmm_csr
+ * ROW_SPLIT (A, B'), C = row_scale (.) C', without writing B' or C'.  Either
+ * scale may be NULL (no scaling on that side).  Synchronous; *kernel_ms
+ * (optional) as for sporder_spmm_csr.
+ */
+SPORDER_API void sporder_spmm_csr_scaled(sporder_context_t ctx, int32_t n,
+                                         int32_t nnz, const int32_t *d_ptr,
+                                         const int32_t *d_ind, const float *d_val,
+                                         int32_t cols, const float *d_b,
+                                         const float *d_row_scale,
+                                         const float *d_nz_col_scale, float *d_c,
+                                         float *kernel_ms);
+
+/*
  * (new) SpMM plans.  The reference's SpMM harness converts each matrix once,
  * untimed, in SpMMMethod.prepare (bench/spmm/spmm_bench/base.py:41-46) and
  * times SpMMMethod.run; a plan is that conversion for this library's CSR

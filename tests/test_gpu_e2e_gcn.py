@@ -1,7 +1,8 @@
 """GPU checks of the end-to-end GCN driver (chunkedgreedy_amd.e2e_gcn).
 
 - The normalised graph operator d^-1/2 A d^-1/2 x matches fp64 scipy within
-  1e-5 relative.
+  1e-5 relative; its fused form (one spmm_csr_scaled call) equals the
+  three-step form bit for bit, and training with it follows the same losses.
 - A GCN is permutation-equivariant and its loss is a mean over nodes, so
   training on P A P^T with permuted features and labels follows the same loss
   trajectory as training on A: the losses agree to fp32 rounding (1e-4
@@ -45,3 +46,22 @@ def test_training_is_permutation_equivariant(sporder):
         assert r["reorder_ms"] > 0 and r["perm_ms"] > 0
         assert r["final_loss"] == pytest.approx(base, rel=1e-4)
         assert "epoch_speedup" in r and "e2e_speedup" in r
+
+
+def test_fused_scaling_is_bit_identical(sporder):
+    ptr, ind, _ = synth.chung_lu(3000, 2.1, 12, 53)
+    n = ptr.shape[0] - 1
+    p, i = torch.from_numpy(ptr).cuda(), torch.from_numpy(ind).cuda()
+    x = torch.randn(n, 64, device="cuda", generator=torch.Generator(device="cuda").manual_seed(2))
+    a = e2e_gcn.GraphOp(p, i)(x)
+    b = e2e_gcn.GraphOp(p, i, fused=True)(x)
+    assert torch.equal(a.view(torch.int32), b.view(torch.int32))
+    print("[e2e] fused n=3000 epochs=4", flush=True)
+    r0 = e2e_gcn.run(ptr, ind, features=16, hidden=32, classes=5, epochs=4,
+                     orders=("ORIGIN",), seed=4)
+    r1 = e2e_gcn.run(ptr, ind, features=16, hidden=32, classes=5, epochs=4,
+                     orders=("ORIGIN",), seed=4, fused=True)
+    assert r1[0]["fused_scaling"] and not r0[0]["fused_scaling"]
+    # The operator's outputs are bit-identical (above); the rest of training is
+    # torch's, whose reductions are not promised bit-reproducible across runs.
+    assert r1[0]["final_loss"] == pytest.approx(r0[0]["final_loss"], rel=1e-6)
