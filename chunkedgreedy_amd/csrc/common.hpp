@@ -60,12 +60,12 @@ struct Context {
   size_t lds_per_block = 0;
   Workspace ws;
   Workspace aux; // second grow-only buffer, for temporaries sized mid-call
-  // Two more streams (default priority) for independent kernels of one call,
-  // forked from and joined back into `stream` with the events below, so a
-  // synchronize of `stream` also waits for their work.
-  hipStream_t side[2] = {};
+  // Three more streams (default priority) for independent kernels of one
+  // call, forked from and joined back into `stream` with the events below, so
+  // a synchronize of `stream` also waits for their work.
+  hipStream_t side[3] = {};
   hipEvent_t fork_ev = nullptr;
-  hipEvent_t join_ev[2] = {};
+  hipEvent_t join_ev[3] = {};
   hipEvent_t prep_ev = nullptr; // a stage's preparation done (csg's global path)
   // Pinned host words for small device-to-host readbacks.
   int32_t *host_words = nullptr;
@@ -207,7 +207,11 @@ void csr2csc(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
 // entries (the non-empty prefix of its table row, written with the row); rows
 // not computed are left as they are.  `mirror`, when given, receives (atomic
 // adds) the mirror_term of every nonzero of the computed rows; the local
-// variant below does the same for its rows.
+// variant below does the same for its rows.  `host_list_len`, when known
+// (>= 2) and d_chunks is given, lets the first listed chunk (the largest
+// size class) have its run search and sketch first while the other chunks'
+// run search runs beside it on side stream 2 (joined back before return).
+// Must be called with ctx.stream = side[0] or the library stream, not side[2].
 size_t chunk_sketch_ws_bytes(int32_t n, int32_t nnz, int32_t chunk_size);
 void chunk_sketch_top_k(Context &ctx, int32_t n, int32_t nnz, int32_t k, int32_t chunk_size,
                         int32_t m_capacity, const int32_t *d_ptr,
@@ -216,7 +220,7 @@ void chunk_sketch_top_k(Context &ctx, int32_t n, int32_t nnz, int32_t k, int32_t
                         const int32_t *d_chunks = nullptr,
                         const int32_t *d_chunk_count = nullptr,
                         hipEvent_t prepared = nullptr, int32_t *d_row_valid = nullptr,
-                        unsigned long long *mirror = nullptr);
+                        unsigned long long *mirror = nullptr, int64_t host_list_len = -1);
 
 // Chunk-local variant: one workgroup per chunk with the chunk's transpose in
 // LDS.  Applicable when chunk_local_supported(n, chunk_size).

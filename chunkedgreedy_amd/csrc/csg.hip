@@ -942,7 +942,8 @@ void build_table(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
   // sketch paths that have work, which write disjoint table rows, run
   // concurrently: tier 2 (mid-size chunks) on side stream 1, the global-CSC
   // path (large chunks, whose hub rows set the critical path on power-law
-  // inputs) on side stream 0, tier 1 on the library stream.  Tier 1's
+  // inputs) on side stream 0 (its largest chunk first, the other chunks' run
+  // search and sketch on side stream 2), tier 1 on the library stream.  Tier 1's
   // workgroups take two per CU and leave no room for others, so it starts
   // last: tier 2 (whose workgroups need a whole CU's LDS) is launched first,
   // and tier 1 waits until the global path's run search is done and its
@@ -970,7 +971,7 @@ void build_table(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
     global_csc(&cp, &ri);
     t_csc->end(ctx.stream);
     chunk_sketch_top_k(ctx, n, nnz, k, chunk_size, m_cap, d_ptr, d_ind, cp, ri, table,
-                       lists + chunks, counts + 1, ctx.prep_ev, row_valid, msum);
+                       lists + chunks, counts + 1, ctx.prep_ev, row_valid, msum, h_counts[1]);
   } else {
     t_csc->begin(ctx.stream);
     t_csc->end(ctx.stream);

@@ -48,6 +48,13 @@ __device__ __forceinline__ int64_t list_len(const int32_t *list, const int32_t *
   return list ? static_cast<int64_t>(*list_count) : num_chunks;
 }
 
+// List entries [l0, l1) of a launch; l1 < 0: to the end of the list.
+__device__ __forceinline__ int64_t range_end(int64_t l1, const int32_t *list,
+                                             const int32_t *list_count, int64_t num_chunks) {
+  const int64_t L = list_len(list, list_count, num_chunks);
+  return l1 < 0 || l1 > L ? L : l1;
+}
+
 // task_off[i] = tasks of list entries before i; task_off[L] = total.
 __global__ void __launch_bounds__(kPlanBlock)
     ovf_plan_kernel(int32_t n, int32_t chunk_size, const int32_t *__restrict__ row_ptr,
@@ -103,19 +110,21 @@ __device__ __forceinline__ int32_t sampled_lower_bound(const int32_t *__restrict
   return lower_bound_dev(a, from, to, t);
 }
 
+// Runs of the nonzeros of list entries [l0, l1) (l1 < 0: to the end).
 __global__ void __launch_bounds__(kRunsBlock)
     ovf_runs_kernel(int32_t n, int32_t chunk_size, const int32_t *__restrict__ row_ptr,
                     const int32_t *__restrict__ col_ind, const int32_t *__restrict__ col_ptr,
                     const int32_t *__restrict__ row_ind, const int32_t *__restrict__ sample,
                     const int32_t *__restrict__ list, const int32_t *__restrict__ list_count,
-                    const int32_t *__restrict__ task_off, int2 *__restrict__ runs) {
-  const int64_t L = list_len(list, list_count, ceil_div64(n, chunk_size));
-  if (L == 0) return;
+                    const int32_t *__restrict__ task_off, int2 *__restrict__ runs, int64_t l0,
+                    int64_t l1) {
+  const int64_t L = range_end(l1, list, list_count, ceil_div64(n, chunk_size));
+  if (L <= l0) return;
   const int32_t tasks = task_off[L];
-  for (int32_t t = blockIdx.x; t < tasks; t += gridDim.x) {
+  for (int32_t t = task_off[l0] + blockIdx.x; t < tasks; t += gridDim.x) {
     // List entry owning task t: the largest i with task_off[i] <= t (entries
     // without tasks share their successor's offset and are skipped).
-    int64_t lo = 0, hi = L - 1;
+    int64_t lo = l0, hi = L - 1;
     while (lo < hi) {
       const int64_t mid = (lo + hi + 1) >> 1;
       if (task_off[mid] <= t) {
@@ -241,7 +250,7 @@ __global__ void __launch_bounds__(kOvfBlock)
                       const int32_t *__restrict__ list,
                       const int32_t *__restrict__ list_count, uint32_t *__restrict__ claim,
                       int32_t *__restrict__ row_valid, const int32_t *__restrict__ col_ind,
-                      unsigned long long *__restrict__ mirror) {
+                      unsigned long long *__restrict__ mirror, int64_t l0, int64_t l1) {
   __shared__ RunLookup s_lookup[kOvfWaves];
   __shared__ unsigned long long s_mirror;
   if (threadIdx.x == 0) s_mirror = 0;
@@ -249,8 +258,10 @@ __global__ void __launch_bounds__(kOvfBlock)
   unsigned long long msum = 0; // mirror-check terms of this lane's nonzeros
   const int lane = lane_id();
   RunLookup *lk = &s_lookup[threadIdx.x / kWave];
-  // work < 2^32: list_len * chunk_size <= n + chunk_size - 1.
-  const int64_t work = list_len(list, list_count, ceil_div64(n, chunk_size)) * chunk_size;
+  // Rows of list entries [l0, l1); work < 2^32: list_len * chunk_size <=
+  // n + chunk_size - 1.
+  const int64_t L = range_end(l1, list, list_count, ceil_div64(n, chunk_size));
+  const int64_t work = (L > l0 ? L - l0 : 0) * chunk_size;
   WaveSketch<CELLS> store;
 
   // Waves claim rows one at a time from a device-wide counter (zeroed by the
@@ -261,8 +272,10 @@ __global__ void __launch_bounds__(kOvfBlock)
     if (lane == 0) claimed = atomicAdd(claim, 1u);
     const int64_t w = static_cast<uint32_t>(readlane(static_cast<int32_t>(claimed), 0));
     if (w >= work) break;
-    int64_t row64 = w;
-    if (list) row64 = static_cast<int64_t>(list[w / chunk_size]) * chunk_size + (w % chunk_size);
+    int64_t row64 = l0 * chunk_size + w;
+    if (list) {
+      row64 = static_cast<int64_t>(list[l0 + w / chunk_size]) * chunk_size + (w % chunk_size);
+    }
     if (row64 >= n) continue;
     const int32_t row = static_cast<int32_t>(row64);
     uint64_t *out = table + static_cast<size_t>(row) * k;
@@ -316,12 +329,13 @@ void launch_ovf_sketch(Context &ctx, int32_t n, int32_t k, int32_t chunk_size,
                        const int32_t *d_ptr, const int2 *runs, const int2 *pairs,
                        uint64_t *d_table, const int32_t *list, const int32_t *list_count,
                        uint32_t *claim, int32_t *d_row_valid, const int32_t *d_ind,
-                       unsigned long long *mirror) {
+                       unsigned long long *mirror, int64_t l0, int64_t l1) {
   const int g = ctx.grid_for(ceil_div64(n, kOvfWaves), kOvfBlock, 4);
   fill_u32(ctx, claim, 1, 0u);
   ovf_sketch_kernel<CELLS><<<g, kOvfBlock, 0, ctx.stream>>>(n, k, chunk_size, d_ptr, runs,
                                                             pairs, d_table, list, list_count,
-                                                            claim, d_row_valid, d_ind, mirror);
+                                                            claim, d_row_valid, d_ind, mirror,
+                                                            l0, l1);
   SP_LAUNCH_CHECK();
 }
 
@@ -330,7 +344,7 @@ void launch_ovf_sketch(Context &ctx, int32_t n, int32_t k, int32_t chunk_size,
 size_t chunk_sketch_ws_bytes(int32_t n, int32_t nnz, int32_t chunk_size) {
   return 2 * ws_bytes<int2>(static_cast<size_t>(nnz)) +
          ws_bytes<int32_t>(static_cast<size_t>(ceil_div64(n, chunk_size)) + 1) +
-         ws_bytes<uint32_t>(1) + ws_bytes<int32_t>(static_cast<size_t>(nnz) / kSample + 1);
+         ws_bytes<uint32_t>(2) + ws_bytes<int32_t>(static_cast<size_t>(nnz) / kSample + 1);
 }
 
 void chunk_sketch_top_k(Context &ctx, int32_t n, int32_t nnz, int32_t k, int32_t chunk_size,
@@ -338,7 +352,8 @@ void chunk_sketch_top_k(Context &ctx, int32_t n, int32_t nnz, int32_t k, int32_t
                         const int32_t *d_col_ptr, const int32_t *d_row_ind,
                         uint64_t *d_table, const int32_t *d_chunks,
                         const int32_t *d_chunk_count, hipEvent_t prepared,
-                        int32_t *d_row_valid, unsigned long long *mirror) {
+                        int32_t *d_row_valid, unsigned long long *mirror,
+                        int64_t host_list_len) {
   SP_EXPECT(k <= 512, "k must be <= 512");
   SP_EXPECT(m_capacity % 32 == 0 && m_capacity >= 32 && m_capacity <= 512,
             "sketch capacity must be a multiple of 32 in [32, 512]");
@@ -346,7 +361,7 @@ void chunk_sketch_top_k(Context &ctx, int32_t n, int32_t nnz, int32_t k, int32_t
   int2 *runs = ctx.take<int2>(static_cast<size_t>(nnz));
   int2 *pairs = ctx.take<int2>(static_cast<size_t>(nnz));
   int32_t *task_off = ctx.take<int32_t>(static_cast<size_t>(chunks) + 1);
-  uint32_t *claim = ctx.take<uint32_t>(1);
+  uint32_t *claim = ctx.take<uint32_t>(2);
   int32_t *sample = ctx.take<int32_t>(static_cast<size_t>(nnz) / kSample + 1);
 
   ovf_plan_kernel<<<1, kPlanBlock, 0, ctx.stream>>>(n, chunk_size, d_ptr, d_chunks,
@@ -358,24 +373,50 @@ void chunk_sketch_top_k(Context &ctx, int32_t n, int32_t nnz, int32_t k, int32_t
   SP_LAUNCH_CHECK();
   const int64_t max_tasks = ceil_div64(nnz, kRunTask) + chunks;
   const int gr = ctx.grid_for(max_tasks, kRunsBlock, 4);
-  ovf_runs_kernel<<<gr, kRunsBlock, 0, ctx.stream>>>(n, chunk_size, d_ptr, d_ind, d_col_ptr,
-                                                     d_row_ind, sample, d_chunks,
-                                                     d_chunk_count, task_off, runs);
-  SP_LAUNCH_CHECK();
-  if (prepared != nullptr) SP_HIP(hipEventRecord(prepared, ctx.stream));
-  switch (m_capacity / 32) {
-#define SP_CASE(C)                                                                       \
-  case C:                                                                                \
-    launch_ovf_sketch<C>(ctx, n, k, chunk_size, d_ptr, runs, pairs, d_table, d_chunks,   \
-                         d_chunk_count, claim, d_row_valid, d_ind, mirror);              \
+  auto runs_launch = [&](int64_t l0, int64_t l1) {
+    ovf_runs_kernel<<<gr, kRunsBlock, 0, ctx.stream>>>(n, chunk_size, d_ptr, d_ind, d_col_ptr,
+                                                       d_row_ind, sample, d_chunks,
+                                                       d_chunk_count, task_off, runs, l0, l1);
+    SP_LAUNCH_CHECK();
+  };
+  auto sketch_launch = [&](uint32_t *cl, int64_t l0, int64_t l1) {
+    switch (m_capacity / 32) {
+#define SP_CASE(C)                                                                         \
+  case C:                                                                                  \
+    launch_ovf_sketch<C>(ctx, n, k, chunk_size, d_ptr, runs, pairs, d_table, d_chunks,     \
+                         d_chunk_count, cl, d_row_valid, d_ind, mirror, l0, l1);           \
     break;
-    SP_CASE(1) SP_CASE(2) SP_CASE(3) SP_CASE(4) SP_CASE(5) SP_CASE(6)
-    SP_CASE(7) SP_CASE(8) SP_CASE(9) SP_CASE(10) SP_CASE(11) SP_CASE(12)
-    SP_CASE(13) SP_CASE(14) SP_CASE(15) SP_CASE(16)
+      SP_CASE(1) SP_CASE(2) SP_CASE(3) SP_CASE(4) SP_CASE(5) SP_CASE(6)
+      SP_CASE(7) SP_CASE(8) SP_CASE(9) SP_CASE(10) SP_CASE(11) SP_CASE(12)
+      SP_CASE(13) SP_CASE(14) SP_CASE(15) SP_CASE(16)
 #undef SP_CASE
-  default:
-    break;
+    default:
+      break;
+    }
+  };
+  if (d_chunks == nullptr || host_list_len < 2) {
+    runs_launch(0, -1);
+    if (prepared != nullptr) SP_HIP(hipEventRecord(prepared, ctx.stream));
+    sketch_launch(claim, 0, -1);
+    return;
   }
+  // The first listed chunk (the largest size class; on power-law inputs it
+  // holds the hub rows whose serial sketch chains are the critical path) has
+  // its run search alone, then its sketch on this stream while the other
+  // chunks' run search and sketch run beside it on side stream 2.  Measured
+  // on C3: the full run search takes 17 ms, which the hub rows' chain no
+  // longer waits for; run beside the other chunks' search, the first chunk's
+  // took 13 ms.
+  runs_launch(0, 1);
+  fork_side(ctx, 2);
+  sketch_launch(claim, 0, 1);
+  {
+    OnStream on(ctx, ctx.side[2]);
+    runs_launch(1, -1);
+    if (prepared != nullptr) SP_HIP(hipEventRecord(prepared, ctx.stream));
+    sketch_launch(claim + 1, 1, -1);
+  }
+  join_side(ctx, 2);
 }
 
 } // namespace sporder_hip
