@@ -209,6 +209,55 @@ static_assert(32 * kGreedyBlock <= kOffMask && kPackedCap <= kOffMask &&
                   kGreedyCompactRows <= 4096 && kOffBits + 12 <= 31,
               "row header fields");
 
+// Rows of at most kPackedSortK table entries are packed by a sorting network
+// in registers (pack_row_sorted).
+constexpr int32_t kPackedSortK = 16;
+
+// The in-chunk entries of a row's valid prefix (rv <= kPackedSortK) in
+// preference order, written to out[0 ..): table order is weight descending,
+// so each run of equal weight (numbered in table order) is put in local-index
+// order, as keys (run << 16) | local sorted ascending; entries outside the
+// chunk sort last.  Returns how many were written.
+__device__ __forceinline__ int32_t pack_row_sorted(const uint64_t *__restrict__ row, int32_t rv,
+                                                   int32_t start, int32_t end, uint16_t *out) {
+  constexpr int KM = kPackedSortK;
+  uint32_t key[KM];
+  int32_t cnt = 0;
+  uint32_t run = 0u, prev_w = 0u; // weights are positive: 0 matches none
+#pragma unroll
+  for (int j = 0; j < KM; ++j) {
+    const uint64_t e = j < rv ? row[j] : 0ull;
+    const int32_t c = wi_index(e);
+    const bool in = j < rv && c >= start && c < end;
+    const uint32_t wb = static_cast<uint32_t>(e >> 32);
+    run += (in && wb != prev_w) ? 1u : 0u;
+    prev_w = in ? wb : prev_w;
+    key[j] = in ? ((run << 16) | static_cast<uint32_t>(c - start)) : 0xFFFFFFFFu;
+    cnt += in ? 1 : 0;
+  }
+#pragma unroll
+  for (int kk = 2; kk <= KM; kk <<= 1) {
+#pragma unroll
+    for (int jj = kk >> 1; jj > 0; jj >>= 1) {
+#pragma unroll
+      for (int i = 0; i < KM; ++i) {
+        const int l = i ^ jj;
+        if (l > i) {
+          const uint32_t x = key[i], y = key[l];
+          const bool swap = ((i & kk) == 0) ? (x > y) : (x < y);
+          key[i] = swap ? y : x;
+          key[l] = swap ? x : y;
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < KM; ++j) {
+    if (j < cnt) out[j] = static_cast<uint16_t>(key[j] & 0xFFFFu);
+  }
+  return cnt;
+}
+
 // 64-bit words of the entries region: entry_cap staged entries, or packed_cap
 // 16-bit ones in the same bytes.
 __host__ __device__ inline int32_t greedy_entry_words(int32_t entry_cap, int32_t packed_cap) {
@@ -396,6 +445,15 @@ __global__ void __launch_bounds__(kGreedyBlock)
       if (b == a) continue;
       const int32_t rv = row_valid != nullptr ? s_rv[r] : k;
       const uint64_t *row = slice + static_cast<size_t>(r) * k;
+      if (k <= kPackedSortK) {
+        // Rows of at most 16 entries: keys (run number << 16) | local in
+        // registers, sorted by a bitonic network with static indices, then
+        // stored in order (on a stencil most of a row is one run of equal
+        // weight, and the insertion sort below moved nearly every entry).
+        const int32_t cnt = pack_row_sorted(row, rv, start, end, s_e16 + a);
+        (void)cnt;
+        continue;
+      }
       uint32_t starts = 0u; // bit t: entry a + t begins a run of equal weight
       uint32_t prev_w = 0u; // weights are positive: 0 matches none
       int32_t o = a;
