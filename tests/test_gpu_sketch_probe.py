@@ -29,3 +29,21 @@ def test_sketch_forms_agree(args):
     assert out.returncode == 0, out.stdout + out.stderr
     agree = [line for line in out.stdout.splitlines() if "equals_form0" in line]
     assert agree == ["form=1 equals_form0=yes", "form=2 equals_form0=yes"]
+
+
+ISSUE = Path(__file__).resolve().parent / "c" / "issue_probe"
+
+
+def test_issue_probe_runs():
+    """tests/c/issue_probe: one wave's cost per instruction group (the cost
+    model of the single-row sketch chain).  Checks that every group ran and
+    that the costs it prints are positive; the figures are printed."""
+    assert ISSUE.exists(), "tests/c/issue_probe missing: run __graft_entry__.build()"
+    print("[issue_probe] 2000", flush=True)
+    out = subprocess.run([str(ISSUE), "2000"], capture_output=True, text=True, timeout=120)
+    print(out.stdout, flush=True)
+    assert out.returncode == 0, out.stdout + out.stderr
+    rows = [line.split() for line in out.stdout.splitlines() if line.startswith("group=")]
+    assert len(rows) == 12
+    for row in rows:
+        assert float(row[2].split("=")[1]) > 0.0, row
