@@ -206,8 +206,8 @@ void csr2csc(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
 // d_row_valid, when given, receives each computed row's number of valid table
 // entries (the non-empty prefix of its table row, written with the row); rows
 // not computed are left as they are.  `mirror`, when given, receives (atomic
-// adds) the mirror_term of every nonzero of the computed rows; the local
-// variant below does the same for its rows.  `host_list_len`, when known
+// adds) the mirror_term of every nonzero of the computed rows, from a kernel
+// beside the sketch; the local variant below does the same for its rows.  `host_list_len`, when known
 // (>= 2) and d_chunks is given, lets the first listed chunk (the largest
 // size class) have its run search and sketch first while the other chunks'
 // run search runs beside it on side stream 2 (joined back before return).

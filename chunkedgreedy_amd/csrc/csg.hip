@@ -899,9 +899,10 @@ void validate_sketch_args(int32_t k, float oversampling, int32_t chunk_size) {
 // meets the reference's precondition of sorted columns within each row
 // (sporder/include/sporder.h:27) the two agree exactly when the pattern is
 // symmetric as a multiset (as many (r, c) as (c, r) for every pair).  The
-// sketch kernels that read the rows (the chunk-local tiers and the global
-// path) add every nonzero's mirror_term (common.hpp) into one word; the sum is
-// zero for a symmetric pattern.  A call whose sum is not zero is run again
+// chunk-local tiers (as they read their rows) and, for the global path's
+// rows, a kernel of its own beside that path's sketch add every nonzero's
+// mirror_term (common.hpp) into one word; the sum is zero for a symmetric
+// pattern.  A call whose sum is not zero is run again
 // with every chunk on the global path, which reads the CSR as the CSC like the
 // reference.
 

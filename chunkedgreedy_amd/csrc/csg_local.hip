@@ -53,6 +53,8 @@ constexpr int kClasses = 32;
 // Step 3's mark: larger than any bucket id (< 2048) or row index (< 4096).
 constexpr uint16_t kMultiMark = 0xFFFF;
 constexpr int kRowsPerThread = kLocalRowCap / kLocalThreads;
+// Tier 2 scatters rows of more nonzeros than this with a whole wave (step 2a).
+constexpr int kScatterRowCap = 32;
 
 __device__ __forceinline__ uint32_t bucket_of(uint32_t col, int nb_log2) {
   // Fibonacci hashing (Knuth, TAOCP vol. 3, 6.4): high bits of col * 2^32/phi.
@@ -141,6 +143,9 @@ __global__ void __launch_bounds__(kLocalThreads, (local_min_waves<CELLS, KEYCAP>
   constexpr int NB = 1 << NB_LOG2;
   static_assert(KEYCAP / (kSmallBucket + 1) <= ROWCAP, "large-bucket list must fit s_order");
   static_assert(NB <= kMultiMark && ROWCAP <= kMultiMark, "kMultiMark must be unused");
+  // Tier 2 (the key capacity past 16384) scatters wide rows with a wave;
+  // tier 1 runs at its register limit and keeps a thread per row.
+  constexpr bool kWideRows = KEYCAP > 16384;
   __shared__ uint32_t s_keys[KEYCAP];
   __shared__ int32_t s_bend[NB];      // after the scatter: end of bucket b
   __shared__ int32_t s_size[ROWCAP];
@@ -243,13 +248,20 @@ __global__ void __launch_bounds__(kLocalThreads, (local_min_waves<CELLS, KEYCAP>
     //     row, read whole only inside the chunk's nonzeros; a group at the
     //     chunk's edge is read element by element): the lanes of a wave read
     //     different rows, so each load instruction touches a line per lane,
-    //     and a group's four columns cost one such access.
+    //     and a group's four columns cost one such access.  In tier 2, rows
+    //     of more than kScatterRowCap nonzeros are scattered by the whole wave
+    //     that holds them, 64 columns per load, after its other rows: on
+    //     skewed graphs a thread per row left the step as long as the chunk's
+    //     longest row.
     unsigned long long msum = 0; // this thread's rows' mirror-check terms, when asked
     const bool vec_ok = (reinterpret_cast<uintptr_t>(col_ind) & 15u) == 0;
-    for (int32_t r = tid; r < rows; r += kLocalThreads) {
-      const int32_t rb = row_ptr[cs + r];
-      const int32_t re = rb + s_size[r];
-      for (int32_t q = vec_ok ? (rb & ~3) : rb; q < re; q += vec_ok ? 4 : 1) {
+    for (int32_t r0 = kWideRows ? wave * kWave : tid; r0 < rows;
+         r0 += kLocalThreads) {
+      const int32_t r = kWideRows ? r0 + lane : r0;
+      const int32_t rb = (!kWideRows || r < rows) ? row_ptr[cs + r] : 0;
+      const int32_t re = (!kWideRows || r < rows) ? rb + s_size[r] : 0;
+      const bool wide = kWideRows && re - rb > kScatterRowCap;
+      for (int32_t q = vec_ok ? (rb & ~3) : rb; !wide && q < re; q += vec_ok ? 4 : 1) {
         int32_t v[4];
         if (vec_ok && q >= e0 && q + 4 <= e0 + E) {
           const int4 g = *reinterpret_cast<const int4 *>(col_ind + q);
@@ -270,6 +282,18 @@ __global__ void __launch_bounds__(kLocalThreads, (local_min_waves<CELLS, KEYCAP>
             const int32_t slot = atomicAdd(&s_bend[bucket_of(c, nbl)], 1);
             s_keys[slot] = (c << lb) | static_cast<uint32_t>(r);
             if (mirror != nullptr) msum += mirror_term(cs + r, static_cast<int32_t>(c));
+          }
+        }
+      }
+      if constexpr (kWideRows) {
+        for (uint64_t wm = ballot(wide); wm != 0; wm = clear_bit(wm, __builtin_ctzll(wm))) {
+          const int32_t i = __builtin_ctzll(wm);
+          const int32_t wr = readlane(r, i), wb = readlane(rb, i), we = readlane(re, i);
+          for (int32_t q = wb + lane; q < we; q += kWave) {
+            const uint32_t c = static_cast<uint32_t>(col_ind[q]);
+            const int32_t slot = atomicAdd(&s_bend[bucket_of(c, nbl)], 1);
+            s_keys[slot] = (c << lb) | static_cast<uint32_t>(wr);
+            if (mirror != nullptr) msum += mirror_term(cs + wr, static_cast<int32_t>(c));
           }
         }
       }

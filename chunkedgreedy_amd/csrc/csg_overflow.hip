@@ -41,6 +41,7 @@ constexpr int kPlanBlock = 256;
 constexpr int kRunsBlock = 256;
 constexpr int kOvfBlock = 256;
 constexpr int kOvfWaves = kOvfBlock / kWave;
+constexpr int kMirrorBlock = 256;
 constexpr int kSample = 16;      // run-search sample stride (one 64-byte line)
 
 __device__ __forceinline__ int64_t list_len(const int32_t *list, const int32_t *list_count,
@@ -249,13 +250,8 @@ __global__ void __launch_bounds__(kOvfBlock)
                       const int2 *__restrict__ pairs, uint64_t *__restrict__ table,
                       const int32_t *__restrict__ list,
                       const int32_t *__restrict__ list_count, uint32_t *__restrict__ claim,
-                      int32_t *__restrict__ row_valid, const int32_t *__restrict__ col_ind,
-                      unsigned long long *__restrict__ mirror, int64_t l0, int64_t l1) {
+                      int32_t *__restrict__ row_valid, int64_t l0, int64_t l1) {
   __shared__ RunLookup s_lookup[kOvfWaves];
-  __shared__ unsigned long long s_mirror;
-  if (threadIdx.x == 0) s_mirror = 0;
-  __syncthreads();
-  unsigned long long msum = 0; // mirror-check terms of this lane's nonzeros
   const int lane = lane_id();
   RunLookup *lk = &s_lookup[threadIdx.x / kWave];
   // Rows of list entries [l0, l1); work < 2^32: list_len * chunk_size <=
@@ -281,9 +277,6 @@ __global__ void __launch_bounds__(kOvfBlock)
     uint64_t *out = table + static_cast<size_t>(row) * k;
     const int32_t rs = row_ptr[row], re = row_ptr[row + 1];
     const int32_t deg = re - rs;
-    if (mirror != nullptr) {
-      for (int32_t q = rs + lane; q < re; q += kWave) msum += mirror_term(row, col_ind[q]);
-    }
     if (deg == 0) {
       for (int32_t j = lane; j < k; j += kWave) out[j] = 0;
       if (row_valid != nullptr && lane == 0) row_valid[row] = 0;
@@ -314,28 +307,63 @@ __global__ void __launch_bounds__(kOvfBlock)
     store.select_top_k(k, out);
     if (row_valid != nullptr && lane == 0) row_valid[row] = min(k, store.filled);
   }
-  if (mirror != nullptr) {
-    // Wave sums into LDS, then one global atomic per workgroup.
+}
+
+// The is_symmetric mirror check of the listed chunks' rows: mirror_term
+// (common.hpp) of every nonzero, summed into *mirror.  A wave per row, its
+// lanes over the row's columns with four loads in flight per lane.  Kept out
+// of the sketch kernel, where each row waited out its column loads before its
+// sketch could start (on C5 about a fifth of the global path's wave time, and
+// on the hub row's serial chain).
+__global__ void __launch_bounds__(kMirrorBlock)
+    ovf_mirror_kernel(int32_t n, int32_t chunk_size, const int32_t *__restrict__ row_ptr,
+                      const int32_t *__restrict__ col_ind, const int32_t *__restrict__ list,
+                      const int32_t *__restrict__ list_count,
+                      unsigned long long *__restrict__ mirror) {
+  __shared__ unsigned long long s_sum;
+  if (threadIdx.x == 0) s_sum = 0;
+  __syncthreads();
+  const int lane = lane_id();
+  constexpr int kWaves = kMirrorBlock / kWave;
+  const int64_t work = list_len(list, list_count, ceil_div64(n, chunk_size)) * chunk_size;
+  unsigned long long msum = 0;
+  for (int64_t w = static_cast<int64_t>(blockIdx.x) * kWaves + threadIdx.x / kWave; w < work;
+       w += static_cast<int64_t>(gridDim.x) * kWaves) {
+    const int64_t row64 =
+        list ? static_cast<int64_t>(list[w / chunk_size]) * chunk_size + w % chunk_size : w;
+    if (row64 >= n) continue;
+    const int32_t row = static_cast<int32_t>(row64);
+    const int32_t rs = row_ptr[row], re = row_ptr[row + 1];
+    for (int32_t q0 = rs; q0 < re; q0 += 4 * kWave) {
+      int32_t c[4];
 #pragma unroll
-    for (int o = kWave / 2; o > 0; o >>= 1) msum += __shfl_xor(msum, o);
-    if (lane == 0 && msum != 0) atomicAdd(&s_mirror, msum);
-    __syncthreads();
-    if (threadIdx.x == 0 && s_mirror != 0) atomicAdd(mirror, s_mirror);
+      for (int u = 0; u < 4; ++u) {
+        const int32_t q = q0 + u * kWave + lane;
+        c[u] = q < re ? col_ind[q] : 0;
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if (q0 + u * kWave + lane < re) msum += mirror_term(row, c[u]);
+      }
+    }
   }
+#pragma unroll
+  for (int o = kWave / 2; o > 0; o >>= 1) msum += __shfl_xor(msum, o);
+  if (lane == 0 && msum != 0) atomicAdd(&s_sum, msum);
+  __syncthreads();
+  if (threadIdx.x == 0 && s_sum != 0) atomicAdd(mirror, s_sum);
 }
 
 template <int CELLS>
 void launch_ovf_sketch(Context &ctx, int32_t n, int32_t k, int32_t chunk_size,
                        const int32_t *d_ptr, const int2 *runs, const int2 *pairs,
                        uint64_t *d_table, const int32_t *list, const int32_t *list_count,
-                       uint32_t *claim, int32_t *d_row_valid, const int32_t *d_ind,
-                       unsigned long long *mirror, int64_t l0, int64_t l1) {
+                       uint32_t *claim, int32_t *d_row_valid, int64_t l0, int64_t l1) {
   const int g = ctx.grid_for(ceil_div64(n, kOvfWaves), kOvfBlock, 4);
   fill_u32(ctx, claim, 1, 0u);
   ovf_sketch_kernel<CELLS><<<g, kOvfBlock, 0, ctx.stream>>>(n, k, chunk_size, d_ptr, runs,
                                                             pairs, d_table, list, list_count,
-                                                            claim, d_row_valid, d_ind, mirror,
-                                                            l0, l1);
+                                                            claim, d_row_valid, l0, l1);
   SP_LAUNCH_CHECK();
 }
 
@@ -384,7 +412,7 @@ void chunk_sketch_top_k(Context &ctx, int32_t n, int32_t nnz, int32_t k, int32_t
 #define SP_CASE(C)                                                                         \
   case C:                                                                                  \
     launch_ovf_sketch<C>(ctx, n, k, chunk_size, d_ptr, runs, pairs, d_table, d_chunks,     \
-                         d_chunk_count, cl, d_row_valid, d_ind, mirror, l0, l1);           \
+                         d_chunk_count, cl, d_row_valid, l0, l1);                          \
     break;
       SP_CASE(1) SP_CASE(2) SP_CASE(3) SP_CASE(4) SP_CASE(5) SP_CASE(6)
       SP_CASE(7) SP_CASE(8) SP_CASE(9) SP_CASE(10) SP_CASE(11) SP_CASE(12)
@@ -394,7 +422,20 @@ void chunk_sketch_top_k(Context &ctx, int32_t n, int32_t nnz, int32_t k, int32_t
       break;
     }
   };
+  // The mirror check of the listed rows, when asked: independent of the
+  // sketch, so it runs beside it (on side stream 2 with the head-first
+  // split below, else ahead of it).
+  auto mirror_launch = [&]() {
+    if (mirror == nullptr) return;
+    const int64_t rows_bound =
+        d_chunks == nullptr ? n : (host_list_len >= 0 ? host_list_len * chunk_size : n);
+    const int gm = ctx.grid_for(ceil_div64(rows_bound, kMirrorBlock / kWave), kMirrorBlock, 2);
+    ovf_mirror_kernel<<<gm, kMirrorBlock, 0, ctx.stream>>>(n, chunk_size, d_ptr, d_ind,
+                                                            d_chunks, d_chunk_count, mirror);
+    SP_LAUNCH_CHECK();
+  };
   if (d_chunks == nullptr || host_list_len < 2) {
+    mirror_launch();
     runs_launch(0, -1);
     if (prepared != nullptr) SP_HIP(hipEventRecord(prepared, ctx.stream));
     sketch_launch(claim, 0, -1);
@@ -412,6 +453,7 @@ void chunk_sketch_top_k(Context &ctx, int32_t n, int32_t nnz, int32_t k, int32_t
   sketch_launch(claim, 0, 1);
   {
     OnStream on(ctx, ctx.side[2]);
+    mirror_launch();
     runs_launch(1, -1);
     if (prepared != nullptr) SP_HIP(hipEventRecord(prepared, ctx.stream));
     sketch_launch(claim + 1, 1, -1);
