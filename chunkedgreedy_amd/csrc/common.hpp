@@ -205,9 +205,7 @@ void csr2csc(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
 // recorded once the run search is done and before the sketch launch.
 // d_row_valid, when given, receives each computed row's number of valid table
 // entries (the non-empty prefix of its table row, written with the row); rows
-// not computed are left as they are.  `mirror`, when given, receives (atomic
-// adds) the mirror_term of every nonzero of the computed rows, from a kernel
-// beside the sketch; the local variant below does the same for its rows.  `host_list_len`, when known
+// not computed are left as they are.  `host_list_len`, when known
 // (>= 2) and d_chunks is given, lets the first listed chunk (the largest
 // size class) have its run search and sketch first while the other chunks'
 // run search runs beside it on side stream 2 (joined back before return).
@@ -220,18 +218,31 @@ void chunk_sketch_top_k(Context &ctx, int32_t n, int32_t nnz, int32_t k, int32_t
                         const int32_t *d_chunks = nullptr,
                         const int32_t *d_chunk_count = nullptr,
                         hipEvent_t prepared = nullptr, int32_t *d_row_valid = nullptr,
-                        unsigned long long *mirror = nullptr, int64_t host_list_len = -1);
+                        int64_t host_list_len = -1);
+// The is_symmetric mirror check of the rows chunk_sketch_top_k computes for
+// the same list: mirror_term (below) of each of their nonzeros, added into
+// *mirror.  Independent of the sketch; the caller runs it where it holds back
+// nothing.
+void chunk_mirror_check(Context &ctx, int32_t n, int32_t chunk_size, const int32_t *d_ptr,
+                        const int32_t *d_ind, const int32_t *d_chunks,
+                        const int32_t *d_chunk_count, int64_t host_list_len,
+                        unsigned long long *mirror);
 
 // Chunk-local variant: one workgroup per chunk with the chunk's transpose in
 // LDS.  Applicable when chunk_local_supported(n, chunk_size).
-// chunk_local_classify fills d_lists (2*num_chunks int32) and d_counts (2
-// int32): the chunks of LDS tier 2 in d_lists[0 .. d_counts[0]) and the chunks
-// too large for LDS in d_lists[num_chunks .. num_chunks + d_counts[1]), the
-// latter for chunk_sketch_top_k over the global CSC (with is_symmetric, the
-// largest chunks that tier 2 could hold go there as well, to run beside it).  chunk_local_sketch_top_k
-// then writes the rows of tier-1 chunks (tiers & 1; chunk_size <= 1024) and of
-// the listed tier-2 chunks (tiers & 2); the two launches are independent and
-// may run on different streams.  d_row_valid as for chunk_sketch_top_k.
+// chunk_local_classify fills d_lists (3*num_chunks int32) and d_counts (4
+// int32): the chunks of LDS tier 2 in d_lists[0 .. d_counts[0]), the chunks
+// too large for LDS in d_lists[num_chunks .. num_chunks + d_counts[1]) (for
+// chunk_sketch_top_k over the global CSC; with is_symmetric, the largest
+// chunks that tier 2 could hold go there as well, to run beside it), the
+// tier-1 chunks in d_lists[2 num_chunks .. 2 num_chunks + d_counts[2]), and
+// d_counts[3] = 0, the counter tier 2 claims its chunks from (so each tier-2
+// launch needs a classification before it).  chunk_local_sketch_top_k then
+// writes the rows of tier-1 chunks (tiers & 1; chunk_size <= 1024) and of the
+// listed tier-2 chunks (tiers & 2); the two launches are independent and may
+// run on different streams.  With t1_list_len >= 0 (d_counts[2], read back)
+// tier 1 runs over its list with at most that many workgroups, else one per
+// chunk.  d_row_valid as for chunk_sketch_top_k.
 constexpr int kLocalRowCap = 4096;
 bool chunk_local_supported(int32_t n, int32_t chunk_size);
 void chunk_local_classify(Context &ctx, int32_t n, int32_t chunk_size, const int32_t *d_ptr,
@@ -239,9 +250,10 @@ void chunk_local_classify(Context &ctx, int32_t n, int32_t chunk_size, const int
 void chunk_local_sketch_top_k(Context &ctx, int32_t n, int32_t k, int32_t chunk_size,
                               int32_t m_capacity, const int32_t *d_ptr, const int32_t *d_ind,
                               uint64_t *d_table, const int32_t *d_lists,
-                              const int32_t *d_counts, int tiers,
+                              int32_t *d_counts, int tiers,
                               int32_t *d_row_valid = nullptr,
-                              unsigned long long *mirror = nullptr);
+                              unsigned long long *mirror = nullptr,
+                              int64_t t1_list_len = -1);
 
 // Degree / weight totals of a top-k table (reference
 // sporder/src/common/similarity_top_k.cu:120-172).

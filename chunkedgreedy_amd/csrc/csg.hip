@@ -935,7 +935,7 @@ size_t table_ws_bytes(int32_t n, int32_t nnz, int32_t k, int32_t chunk_size,
                       bool is_symmetric) {
   size_t b = ws_bytes<uint64_t>(static_cast<size_t>(n) * k);
   int64_t chunks = ceil_div64(n, chunk_size);
-  b += ws_bytes<int32_t>(2 * static_cast<size_t>(chunks)) + ws_bytes<int32_t>(2);
+  b += ws_bytes<int32_t>(3 * static_cast<size_t>(chunks)) + ws_bytes<int32_t>(4);
   b += chunk_sketch_ws_bytes(n, nnz, chunk_size);
   if (!is_symmetric) {
     b += ws_bytes<int32_t>(static_cast<size_t>(n) + 1) +
@@ -959,8 +959,8 @@ void build_table(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
                  EventSpan *t_sim, MirrorCheck *mirror, bool allow_local,
                  int32_t *row_valid = nullptr) {
   const int64_t chunks = ceil_div64(n, chunk_size);
-  int32_t *lists = ctx.take<int32_t>(2 * static_cast<size_t>(chunks));
-  int32_t *counts = ctx.take<int32_t>(2);
+  int32_t *lists = ctx.take<int32_t>(3 * static_cast<size_t>(chunks));
+  int32_t *counts = ctx.take<int32_t>(4);
   const bool local = allow_local && chunk_local_supported(n, chunk_size);
   const bool check_mirror = local && is_symmetric;
   unsigned long long *msum = nullptr;
@@ -997,47 +997,67 @@ void build_table(Context &ctx, int32_t n, int32_t nnz, const int32_t *d_ptr,
     return;
   }
 
-  // Chunks are classified and the two list lengths read back; then the
+  // Chunks are classified and the three list lengths read back; then the
   // sketch paths that have work, which write disjoint table rows, run
   // concurrently: tier 2 (mid-size chunks) on side stream 1, the global-CSC
   // path (large chunks, whose hub rows set the critical path on power-law
   // inputs) on side stream 0 (its largest chunk first, the other chunks' run
-  // search and sketch on side stream 2), tier 1 on the library stream.  Tier 1's
-  // workgroups take two per CU and leave no room for others, so it starts
-  // last: tier 2 (whose workgroups need a whole CU's LDS) is launched first,
-  // and tier 1 waits until the global path's run search is done and its
-  // sketch, whose first rows are the heaviest chunk's, is queued.  The
-  // transpose of a non-symmetric matrix is built only when the global path
-  // has chunks.
+  // search and sketch on side stream 2), tier 1 on the library stream.  Tier
+  // 1's workgroups take two per CU and leave no room for tier 2's, whose
+  // workgroups need a whole CU's LDS.  When tier 1 has at most one chunk per
+  // CU it is launched first, over its list: it then holds at most half of the
+  // CUs for the length of one chunk, and the tier-2 workgroups placed there
+  // late claim fewer chunks (launched after tier 2, it waited for tier 2's
+  // last workgroups and ran alone at the end: 2.2 ms of C5's 25.7 ms).  With
+  // more tier-1 chunks tier 2 is launched first, and tier 1 waits until the
+  // global path's run search is done and its sketch, whose first rows are the
+  // heaviest chunk's, is queued.  The transpose of a non-symmetric matrix is
+  // built only when the global path has chunks.
   t_sim->begin(ctx.stream);
   chunk_local_classify(ctx, n, chunk_size, d_ptr, lists, counts, is_symmetric);
   int32_t *h_counts = ctx.host_words;
-  SP_HIP(hipMemcpyAsync(h_counts, counts, 2 * sizeof(int32_t), hipMemcpyDeviceToHost,
+  SP_HIP(hipMemcpyAsync(h_counts, counts, 3 * sizeof(int32_t), hipMemcpyDeviceToHost,
                         ctx.stream));
   ctx.sync();
   const bool run_t2 = h_counts[0] > 0, run_global = h_counts[1] > 0;
+  const int64_t t1_len = h_counts[2];
+  const bool t1_first = (run_t2 || run_global) && t1_len <= ctx.num_cus;
+  if (run_t2) fork_side(ctx, 1);
+  if (run_global) fork_side(ctx, 0);
+  if (t1_first) {
+    chunk_local_sketch_top_k(ctx, n, k, chunk_size, m_cap, d_ptr, d_ind, table, lists, counts,
+                             1, row_valid, msum, t1_len);
+  }
   if (run_t2) {
-    fork_side(ctx, 1);
     OnStream on(ctx, ctx.side[1]);
     chunk_local_sketch_top_k(ctx, n, k, chunk_size, m_cap, d_ptr, d_ind, table, lists, counts,
                              2, row_valid, msum);
   }
   if (run_global) {
-    fork_side(ctx, 0);
     OnStream on(ctx, ctx.side[0]);
     const int32_t *cp, *ri;
     t_csc->begin(ctx.stream);
     global_csc(&cp, &ri);
     t_csc->end(ctx.stream);
     chunk_sketch_top_k(ctx, n, nnz, k, chunk_size, m_cap, d_ptr, d_ind, cp, ri, table,
-                       lists + chunks, counts + 1, ctx.prep_ev, row_valid, msum, h_counts[1]);
+                       lists + chunks, counts + 1, t1_first ? nullptr : ctx.prep_ev, row_valid,
+                       h_counts[1]);
   } else {
     t_csc->begin(ctx.stream);
     t_csc->end(ctx.stream);
   }
-  if (run_global) SP_HIP(hipStreamWaitEvent(ctx.stream, ctx.prep_ev, 0));
-  chunk_local_sketch_top_k(ctx, n, k, chunk_size, m_cap, d_ptr, d_ind, table, lists, counts, 1,
-                           row_valid, msum);
+  if (!t1_first) {
+    if (run_global) SP_HIP(hipStreamWaitEvent(ctx.stream, ctx.prep_ev, 0));
+    chunk_local_sketch_top_k(ctx, n, k, chunk_size, m_cap, d_ptr, d_ind, table, lists, counts,
+                             1, row_valid, msum);
+  }
+  // The global path's rows' mirror check, behind tier 1 on the library
+  // stream: ahead of the global path's other chunks (on side stream 2) it held
+  // their run search back 3.3 ms on C5.
+  if (run_global && msum != nullptr) {
+    chunk_mirror_check(ctx, n, chunk_size, d_ptr, d_ind, lists + chunks, counts + 1,
+                       h_counts[1], msum);
+  }
   if (run_t2) join_side(ctx, 1);
   if (run_global) join_side(ctx, 0);
   t_sim->end(ctx.stream);

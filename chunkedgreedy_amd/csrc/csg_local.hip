@@ -128,7 +128,7 @@ constexpr int local_min_waves() {
   return (KEYCAP <= 16384 && CELLS <= 7) ? 8 : 1;
 }
 
-template <int CELLS, int KEYCAP, int ROWCAP, int NB_LOG2>
+template <int CELLS, int KEYCAP, int ROWCAP, int NB_LOG2, bool CLAIM>
 __global__ void __launch_bounds__(kLocalThreads, (local_min_waves<CELLS, KEYCAP>()))
     chunk_local_sketch_kernel(int32_t n, int32_t k, int32_t chunk_size, int32_t lb,
                               const int32_t *__restrict__ row_ptr,
@@ -139,7 +139,8 @@ __global__ void __launch_bounds__(kLocalThreads, (local_min_waves<CELLS, KEYCAP>
                               int32_t *__restrict__ overflow,
                               int32_t *__restrict__ overflow_count,
                               int32_t *__restrict__ row_valid,
-                              unsigned long long *__restrict__ mirror) {
+                              unsigned long long *__restrict__ mirror,
+                              uint32_t *__restrict__ claim) {
   constexpr int NB = 1 << NB_LOG2;
   static_assert(KEYCAP / (kSmallBucket + 1) <= ROWCAP, "large-bucket list must fit s_order");
   static_assert(NB <= kMultiMark && ROWCAP <= kMultiMark, "kMultiMark must be unused");
@@ -158,6 +159,7 @@ __global__ void __launch_bounds__(kLocalThreads, (local_min_waves<CELLS, KEYCAP>
   __shared__ int32_t s_class[kClasses + 1]; // counts, then cursors, per class
   __shared__ int32_t s_next_row;            // next entry of s_order to claim
   __shared__ unsigned long long s_mirror;   // this workgroup's mirror-check terms
+  __shared__ uint32_t s_claimed[2];         // claimed list entries, by iteration parity
 
   const int tid = threadIdx.x;
   const int lane = lane_id();
@@ -169,7 +171,22 @@ __global__ void __launch_bounds__(kLocalThreads, (local_min_waves<CELLS, KEYCAP>
   for (int32_t r = threadIdx.x; r < ROWCAP; r += kLocalThreads) s_order[r] = 0;
   if (threadIdx.x == 0) s_mirror = 0;
   __syncthreads();
-  for (int64_t t = blockIdx.x; t < work; t += gridDim.x) {
+  // With CLAIM, workgroups claim list entries one at a time from `claim` (a
+  // zeroed counter), so that workgroups placed late (beside another tier's,
+  // until those leave) take fewer; without it they stride over the work.
+  // The claimed entry sits in one of two words by iteration parity, so it is
+  // not overwritten before every wave has read it (an iteration can end
+  // without a barrier).
+  auto next_entry = [&](int64_t it, int64_t t) -> int64_t {
+    if constexpr (CLAIM) {
+      if (tid == 0) s_claimed[it & 1] = atomicAdd(claim, 1u);
+      __syncthreads();
+      return s_claimed[it & 1];
+    } else {
+      return it == 0 ? static_cast<int64_t>(blockIdx.x) : t + gridDim.x;
+    }
+  };
+  for (int64_t it = 0, t = next_entry(0, 0); t < work; ++it, t = next_entry(it, t)) {
     const int32_t chunk = chunk_list ? chunk_list[t] : static_cast<int32_t>(t);
     const int32_t cs = chunk * chunk_size;
     const int32_t ce = (n - cs > chunk_size) ? cs + chunk_size : n;
@@ -486,18 +503,29 @@ __device__ __forceinline__ int chunk_tier(int32_t E, int32_t rows, bool t1, int3
   return 3;
 }
 
-// Lists the chunks beyond tier 1: tier-2 chunks in lists[0 .. counts[0]),
-// global-path chunks in lists[chunks .. chunks + counts[1]).  With one
-// workgroup each list is ordered by floor(log2(nonzeros)), largest first (a
-// counting sort in LDS; order inside a class is arbitrary), so heavy chunks
-// start first, and counts are written, not added.  With several workgroups
-// (more than kClassifyOrderCap chunks) the lists are unordered and counts
-// must be zero on entry.  The table does not depend on list order.
+// List of a chunk of tier t: 0 for tier 2, 1 for the global path, 2 for
+// tier 1 (-1: none).
+__device__ __forceinline__ int tier_list(int tier) {
+  return tier == 1 ? 2 : (tier >= 2 ? tier - 2 : -1);
+}
+
+// Lists the chunks by tier: tier-2 chunks in lists[0 .. counts[0]),
+// global-path chunks in lists[chunks .. chunks + counts[1]), tier-1 chunks in
+// lists[2 chunks .. 2 chunks + counts[2]); counts[3] = 0 (the counter tier 2
+// claims its chunks from).  With one workgroup the tier-2 and global lists
+// are ordered by floor(log2(nonzeros)), largest first (a counting sort in
+// LDS; order inside a class is arbitrary), so heavy chunks start first; the
+// tier-1 list is unordered (one LDS atomic per wave: on inputs of many
+// similar chunks a counting sort put them all on one class counter); and
+// counts are written, not added.  With several workgroups (more than kClassifyOrderCap
+// chunks) the lists are unordered and counts must be zero on entry.  The
+// table does not depend on list order.
 __global__ void __launch_bounds__(kClassifyThreads)
     classify_chunks_kernel(int32_t n, int32_t chunk_size, int t1, int32_t t2_keys,
                            const int32_t *__restrict__ row_ptr, int32_t *__restrict__ lists,
                            int32_t *__restrict__ counts) {
   __shared__ int32_t s_cls[2][kClasses + 1];
+  __shared__ int32_t s_t1;
   const int64_t chunks = ceil_div64(n, chunk_size);
   const int tid = threadIdx.x, lane = lane_id();
   auto chunk_of = [&](int64_t q, int32_t *E) {
@@ -511,14 +539,14 @@ __global__ void __launch_bounds__(kClassifyThreads)
          q0 += static_cast<int64_t>(gridDim.x) * kClassifyThreads) {
       const int64_t q = q0 + tid;
       int32_t E = 0;
-      const int tier = q < chunks ? chunk_of(q, &E) : 1;
+      const int li = q < chunks ? tier_list(chunk_of(q, &E)) : -1;
 #pragma unroll
-      for (int l = 0; l < 2; ++l) {
-        const uint64_t m = ballot(tier == l + 2);
+      for (int l = 0; l < 3; ++l) {
+        const uint64_t m = ballot(li == l);
         int32_t base = 0;
         if (m != 0 && lane == 0) base = atomicAdd(&counts[l], __popcll(m));
         base = readlane(base, 0);
-        if (tier == l + 2) {
+        if (li == l) {
           lists[l * chunks + base + __popcll(m & ((1ull << lane) - 1ull))] =
               static_cast<int32_t>(q);
         }
@@ -527,23 +555,35 @@ __global__ void __launch_bounds__(kClassifyThreads)
     return;
   }
   for (int i = tid; i < 2 * (kClasses + 1); i += kClassifyThreads) (&s_cls[0][0])[i] = 0;
-  // Chunk tid + u * kClassifyThreads: its tier and its class 31 -
-  // floor(log2(E)) (ascending class = descending size; E = 0 always fits
-  // tier 1 or 2).
-  int tier[kClassifyPer], cls[kClassifyPer];
+  if (tid == 0) {
+    s_t1 = 0;
+    counts[3] = 0;
+  }
+  // Chunk tid + u * kClassifyThreads: its list and its class 31 -
+  // floor(log2(E)) (ascending class = descending size).
+  int li[kClassifyPer], cls[kClassifyPer];
 #pragma unroll
   for (int u = 0; u < kClassifyPer; ++u) {
     const int64_t q = tid + static_cast<int64_t>(u) * kClassifyThreads;
     int32_t E = 0;
-    tier[u] = q < chunks ? chunk_of(q, &E) : 1;
+    li[u] = q < chunks ? tier_list(chunk_of(q, &E)) : -1;
     cls[u] = __clz(E > 0 ? E : 1);
   }
   __syncthreads();
 #pragma unroll
   for (int u = 0; u < kClassifyPer; ++u) {
-    if (tier[u] > 1) atomicAdd(&s_cls[tier[u] - 2][cls[u]], 1);
+    if (li[u] == 0 || li[u] == 1) atomicAdd(&s_cls[li[u]][cls[u]], 1);
+    const uint64_t m = ballot(li[u] == 2);
+    int32_t base = 0;
+    if (m != 0 && lane == 0) base = atomicAdd(&s_t1, __popcll(m));
+    base = readlane(base, 0);
+    if (li[u] == 2) {
+      lists[2 * chunks + base + __popcll(m & ((1ull << lane) - 1ull))] =
+          tid + u * kClassifyThreads;
+    }
   }
   __syncthreads();
+  if (tid == 2) counts[2] = s_t1;
   if (tid < 2) {
     int32_t run = 0;
     for (int c = 0; c <= kClasses; ++c) {
@@ -556,45 +596,52 @@ __global__ void __launch_bounds__(kClassifyThreads)
   __syncthreads();
 #pragma unroll
   for (int u = 0; u < kClassifyPer; ++u) {
-    if (tier[u] > 1) {
-      const int l = tier[u] - 2;
+    if (li[u] == 0 || li[u] == 1) {
+      const int l = li[u];
       lists[l * chunks + atomicAdd(&s_cls[l][cls[u]], 1)] =
           tid + u * kClassifyThreads;
     }
   }
 }
 
-template <int CELLS, int KEYCAP, int ROWCAP, int NB_LOG2>
+template <int CELLS, int KEYCAP, int ROWCAP, int NB_LOG2, bool CLAIM>
 void launch_tier(Context &ctx, int32_t n, int32_t k, int32_t chunk_size, int32_t lb,
                  const int32_t *d_ptr, const int32_t *d_ind, uint64_t *d_table,
-                 const int32_t *list, const int32_t *list_count, int32_t *ovf,
-                 int32_t *ovf_count, int per_cu, int32_t *d_row_valid,
-                 unsigned long long *mirror) {
+                 const int32_t *list, const int32_t *list_count, int64_t host_len,
+                 int32_t *ovf, int32_t *ovf_count, int per_cu, int32_t *d_row_valid,
+                 unsigned long long *mirror, uint32_t *claim) {
   const int64_t chunks = ceil_div64(n, chunk_size);
-  // A fixed grid striding over the work: no launch per chunk of an empty list.
-  int64_t grid = list ? std::min<int64_t>(chunks, static_cast<int64_t>(ctx.num_cus) * per_cu)
-                      : chunks;
-  chunk_local_sketch_kernel<CELLS, KEYCAP, ROWCAP, NB_LOG2>
+  // A fixed grid striding over (or claiming from) the work: no launch per
+  // chunk of an empty list, and with the list's length known on the host, no
+  // more workgroups than entries.
+  const int64_t len = host_len >= 0 ? std::min<int64_t>(host_len, chunks) : chunks;
+  const int64_t grid =
+      list ? std::min<int64_t>(len, static_cast<int64_t>(ctx.num_cus) * per_cu) : chunks;
+  if (grid <= 0) return;
+  chunk_local_sketch_kernel<CELLS, KEYCAP, ROWCAP, NB_LOG2, CLAIM>
       <<<dim3(static_cast<unsigned>(grid)), kLocalThreads, 0, ctx.stream>>>(
           n, k, chunk_size, lb, d_ptr, d_ind, d_table, list, list_count, ovf, ovf_count,
-          d_row_valid, mirror);
+          d_row_valid, mirror, claim);
   SP_LAUNCH_CHECK();
 }
 
 template <int CELLS>
 void launch_local(Context &ctx, int32_t n, int32_t k, int32_t chunk_size, int32_t lb,
                   const int32_t *d_ptr, const int32_t *d_ind, uint64_t *d_table,
-                  const int32_t *lists, const int32_t *counts, int tiers,
+                  const int32_t *lists, int32_t *counts, int tiers, int64_t t1_list_len,
                   int32_t *d_row_valid, unsigned long long *mirror) {
+  const int64_t chunks = ceil_div64(n, chunk_size);
   if (tiers & 2) {
-    launch_tier<CELLS, kT2Keys, kT2Rows, kT2Nb>(ctx, n, k, chunk_size, lb, d_ptr, d_ind,
-                                                d_table, lists, counts, nullptr, nullptr, 1,
-                                                d_row_valid, mirror);
+    launch_tier<CELLS, kT2Keys, kT2Rows, kT2Nb, true>(
+        ctx, n, k, chunk_size, lb, d_ptr, d_ind, d_table, lists, counts, -1, nullptr, nullptr,
+        1, d_row_valid, mirror, reinterpret_cast<uint32_t *>(counts + 3));
   }
   if ((tiers & 1) && chunk_size <= kT1Rows) {
-    launch_tier<CELLS, kT1Keys, kT1Rows, kT1Nb>(ctx, n, k, chunk_size, lb, d_ptr, d_ind,
-                                                d_table, nullptr, nullptr, nullptr, nullptr, 2,
-                                                d_row_valid, mirror);
+    const bool listed = t1_list_len >= 0;
+    launch_tier<CELLS, kT1Keys, kT1Rows, kT1Nb, false>(
+        ctx, n, k, chunk_size, lb, d_ptr, d_ind, d_table, listed ? lists + 2 * chunks : nullptr,
+        listed ? counts + 2 : nullptr, t1_list_len, nullptr, nullptr, 2, d_row_valid, mirror,
+        nullptr);
   }
 }
 
@@ -612,7 +659,7 @@ void chunk_local_classify(Context &ctx, int32_t n, int32_t chunk_size, const int
   int grid = 1;
   if (chunks > kClassifyOrderCap) {
     grid = ctx.grid_for(ceil_div64(chunks, kClassifyThreads), kClassifyThreads, 1);
-    fill_u32(ctx, d_counts, 2, 0u);
+    fill_u32(ctx, d_counts, 4, 0u);
   }
   const int32_t t2_keys = is_symmetric ? kT2SharedKeys : kT2Keys;
   classify_chunks_kernel<<<grid, kClassifyThreads, 0, ctx.stream>>>(n, chunk_size, t1, t2_keys,
@@ -623,8 +670,8 @@ void chunk_local_classify(Context &ctx, int32_t n, int32_t chunk_size, const int
 void chunk_local_sketch_top_k(Context &ctx, int32_t n, int32_t k, int32_t chunk_size,
                               int32_t m_capacity, const int32_t *d_ptr, const int32_t *d_ind,
                               uint64_t *d_table, const int32_t *d_lists,
-                              const int32_t *d_counts, int tiers, int32_t *d_row_valid,
-                              unsigned long long *mirror) {
+                              int32_t *d_counts, int tiers, int32_t *d_row_valid,
+                              unsigned long long *mirror, int64_t t1_list_len) {
   SP_EXPECT(k <= 512, "k must be <= 512");
   SP_EXPECT(chunk_local_supported(n, chunk_size), "chunk-local sketch not applicable");
   const int32_t lb = bits_for(chunk_size - 1);
@@ -632,7 +679,7 @@ void chunk_local_sketch_top_k(Context &ctx, int32_t n, int32_t k, int32_t chunk_
 #define SP_CASE(C)                                                                       \
   case C:                                                                                \
     launch_local<C>(ctx, n, k, chunk_size, lb, d_ptr, d_ind, d_table, d_lists, d_counts, \
-                    tiers, d_row_valid, mirror);                                         \
+                    tiers, t1_list_len, d_row_valid, mirror);                            \
     break;
     SP_CASE(1) SP_CASE(2) SP_CASE(3) SP_CASE(4) SP_CASE(5) SP_CASE(6)
     SP_CASE(7) SP_CASE(8) SP_CASE(9) SP_CASE(10) SP_CASE(11) SP_CASE(12)

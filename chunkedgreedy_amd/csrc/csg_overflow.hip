@@ -42,6 +42,7 @@ constexpr int kRunsBlock = 256;
 constexpr int kOvfBlock = 256;
 constexpr int kOvfWaves = kOvfBlock / kWave;
 constexpr int kMirrorBlock = 256;
+constexpr int kMirrorRowCap = 64; // longer rows: the whole wave (ovf_mirror_kernel)
 constexpr int kSample = 16;      // run-search sample stride (one 64-byte line)
 
 __device__ __forceinline__ int64_t list_len(const int32_t *list, const int32_t *list_count,
@@ -310,11 +311,11 @@ __global__ void __launch_bounds__(kOvfBlock)
 }
 
 // The is_symmetric mirror check of the listed chunks' rows: mirror_term
-// (common.hpp) of every nonzero, summed into *mirror.  A wave per row, its
-// lanes over the row's columns with four loads in flight per lane.  Kept out
-// of the sketch kernel, where each row waited out its column loads before its
-// sketch could start (on C5 about a fifth of the global path's wave time, and
-// on the hub row's serial chain).
+// (common.hpp) of every nonzero, summed into *mirror.  A wave takes 64
+// consecutive rows, a lane per row of at most kMirrorRowCap nonzeros (four
+// column loads in flight per lane), then its longer rows one by one with all
+// lanes.  Kept out of the sketch kernel, where each row waited out its column
+// loads before its sketch could start.
 __global__ void __launch_bounds__(kMirrorBlock)
     ovf_mirror_kernel(int32_t n, int32_t chunk_size, const int32_t *__restrict__ row_ptr,
                       const int32_t *__restrict__ col_ind, const int32_t *__restrict__ list,
@@ -325,25 +326,47 @@ __global__ void __launch_bounds__(kMirrorBlock)
   __syncthreads();
   const int lane = lane_id();
   constexpr int kWaves = kMirrorBlock / kWave;
+  // Row slots of the listed chunks, taken 64 at a time (chunk_size need not
+  // be a multiple of 64: a group may span two chunks).
   const int64_t work = list_len(list, list_count, ceil_div64(n, chunk_size)) * chunk_size;
   unsigned long long msum = 0;
-  for (int64_t w = static_cast<int64_t>(blockIdx.x) * kWaves + threadIdx.x / kWave; w < work;
-       w += static_cast<int64_t>(gridDim.x) * kWaves) {
-    const int64_t row64 =
-        list ? static_cast<int64_t>(list[w / chunk_size]) * chunk_size + w % chunk_size : w;
-    if (row64 >= n) continue;
-    const int32_t row = static_cast<int32_t>(row64);
-    const int32_t rs = row_ptr[row], re = row_ptr[row + 1];
-    for (int32_t q0 = rs; q0 < re; q0 += 4 * kWave) {
+  for (int64_t g = (static_cast<int64_t>(blockIdx.x) * kWaves + threadIdx.x / kWave) * kWave;
+       g < work; g += static_cast<int64_t>(gridDim.x) * kWaves * kWave) {
+    const int64_t w = g + lane;
+    int32_t row = -1, rs = 0, re = 0;
+    if (w < work) {
+      const int64_t row64 =
+          list ? static_cast<int64_t>(list[w / chunk_size]) * chunk_size + w % chunk_size : w;
+      if (row64 < n) {
+        row = static_cast<int32_t>(row64);
+        rs = row_ptr[row];
+        re = row_ptr[row + 1];
+      }
+    }
+    const bool wide = re - rs > kMirrorRowCap;
+    for (int32_t q0 = rs; !wide && q0 < re; q0 += 4) {
       int32_t c[4];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int32_t q = q0 + u * kWave + lane;
-        c[u] = q < re ? col_ind[q] : 0;
-      }
+      for (int u = 0; u < 4; ++u) c[u] = q0 + u < re ? col_ind[q0 + u] : 0;
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        if (q0 + u * kWave + lane < re) msum += mirror_term(row, c[u]);
+        if (q0 + u < re) msum += mirror_term(row, c[u]);
+      }
+    }
+    for (uint64_t wm = ballot(wide); wm != 0; wm = clear_bit(wm, __builtin_ctzll(wm))) {
+      const int i = __builtin_ctzll(wm);
+      const int32_t wr = readlane(row, i), wb = readlane(rs, i), we = readlane(re, i);
+      for (int32_t q0 = wb; q0 < we; q0 += 4 * kWave) {
+        int32_t c[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int32_t q = q0 + u * kWave + lane;
+          c[u] = q < we ? col_ind[q] : 0;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          if (q0 + u * kWave + lane < we) msum += mirror_term(wr, c[u]);
+        }
       }
     }
   }
@@ -358,8 +381,13 @@ template <int CELLS>
 void launch_ovf_sketch(Context &ctx, int32_t n, int32_t k, int32_t chunk_size,
                        const int32_t *d_ptr, const int2 *runs, const int2 *pairs,
                        uint64_t *d_table, const int32_t *list, const int32_t *list_count,
-                       uint32_t *claim, int32_t *d_row_valid, int64_t l0, int64_t l1) {
-  const int g = ctx.grid_for(ceil_div64(n, kOvfWaves), kOvfBlock, 4);
+                       uint32_t *claim, int32_t *d_row_valid, int64_t l0, int64_t l1,
+                       int64_t rows) {
+  // A wave per row at most: rows = the launch's row slots when the host knows
+  // them (a grid sized for every row of the matrix made a one-chunk launch
+  // dispatch thousands of workgroups that found no row, holding back the
+  // kernels queued beside it).
+  const int g = ctx.grid_for(ceil_div64(rows >= 0 ? rows : n, kOvfWaves), kOvfBlock, 4);
   fill_u32(ctx, claim, 1, 0u);
   ovf_sketch_kernel<CELLS><<<g, kOvfBlock, 0, ctx.stream>>>(n, k, chunk_size, d_ptr, runs,
                                                             pairs, d_table, list, list_count,
@@ -368,6 +396,19 @@ void launch_ovf_sketch(Context &ctx, int32_t n, int32_t k, int32_t chunk_size,
 }
 
 } // namespace
+
+void chunk_mirror_check(Context &ctx, int32_t n, int32_t chunk_size, const int32_t *d_ptr,
+                        const int32_t *d_ind, const int32_t *d_chunks,
+                        const int32_t *d_chunk_count, int64_t host_list_len,
+                        unsigned long long *mirror) {
+  const int64_t rows_bound =
+      d_chunks == nullptr ? n : (host_list_len >= 0 ? host_list_len * chunk_size : n);
+  if (rows_bound <= 0) return;
+  const int gm = ctx.grid_for(ceil_div64(rows_bound, kMirrorBlock), kMirrorBlock, 2);
+  ovf_mirror_kernel<<<gm, kMirrorBlock, 0, ctx.stream>>>(n, chunk_size, d_ptr, d_ind, d_chunks,
+                                                          d_chunk_count, mirror);
+  SP_LAUNCH_CHECK();
+}
 
 size_t chunk_sketch_ws_bytes(int32_t n, int32_t nnz, int32_t chunk_size) {
   return 2 * ws_bytes<int2>(static_cast<size_t>(nnz)) +
@@ -380,8 +421,7 @@ void chunk_sketch_top_k(Context &ctx, int32_t n, int32_t nnz, int32_t k, int32_t
                         const int32_t *d_col_ptr, const int32_t *d_row_ind,
                         uint64_t *d_table, const int32_t *d_chunks,
                         const int32_t *d_chunk_count, hipEvent_t prepared,
-                        int32_t *d_row_valid, unsigned long long *mirror,
-                        int64_t host_list_len) {
+                        int32_t *d_row_valid, int64_t host_list_len) {
   SP_EXPECT(k <= 512, "k must be <= 512");
   SP_EXPECT(m_capacity % 32 == 0 && m_capacity >= 32 && m_capacity <= 512,
             "sketch capacity must be a multiple of 32 in [32, 512]");
@@ -408,11 +448,19 @@ void chunk_sketch_top_k(Context &ctx, int32_t n, int32_t nnz, int32_t k, int32_t
     SP_LAUNCH_CHECK();
   };
   auto sketch_launch = [&](uint32_t *cl, int64_t l0, int64_t l1) {
+    // Row slots of list entries [l0, l1) when the list's length is known.
+    int64_t rows = -1;
+    if (d_chunks == nullptr) {
+      rows = n;
+    } else if (host_list_len >= 0) {
+      const int64_t e = l1 < 0 || l1 > host_list_len ? host_list_len : l1;
+      rows = (e > l0 ? e - l0 : 0) * chunk_size;
+    }
     switch (m_capacity / 32) {
 #define SP_CASE(C)                                                                         \
   case C:                                                                                  \
     launch_ovf_sketch<C>(ctx, n, k, chunk_size, d_ptr, runs, pairs, d_table, d_chunks,     \
-                         d_chunk_count, cl, d_row_valid, l0, l1);                          \
+                         d_chunk_count, cl, d_row_valid, l0, l1, rows);                    \
     break;
       SP_CASE(1) SP_CASE(2) SP_CASE(3) SP_CASE(4) SP_CASE(5) SP_CASE(6)
       SP_CASE(7) SP_CASE(8) SP_CASE(9) SP_CASE(10) SP_CASE(11) SP_CASE(12)
@@ -422,20 +470,7 @@ void chunk_sketch_top_k(Context &ctx, int32_t n, int32_t nnz, int32_t k, int32_t
       break;
     }
   };
-  // The mirror check of the listed rows, when asked: independent of the
-  // sketch, so it runs beside it (on side stream 2 with the head-first
-  // split below, else ahead of it).
-  auto mirror_launch = [&]() {
-    if (mirror == nullptr) return;
-    const int64_t rows_bound =
-        d_chunks == nullptr ? n : (host_list_len >= 0 ? host_list_len * chunk_size : n);
-    const int gm = ctx.grid_for(ceil_div64(rows_bound, kMirrorBlock / kWave), kMirrorBlock, 2);
-    ovf_mirror_kernel<<<gm, kMirrorBlock, 0, ctx.stream>>>(n, chunk_size, d_ptr, d_ind,
-                                                            d_chunks, d_chunk_count, mirror);
-    SP_LAUNCH_CHECK();
-  };
   if (d_chunks == nullptr || host_list_len < 2) {
-    mirror_launch();
     runs_launch(0, -1);
     if (prepared != nullptr) SP_HIP(hipEventRecord(prepared, ctx.stream));
     sketch_launch(claim, 0, -1);
@@ -453,7 +488,6 @@ void chunk_sketch_top_k(Context &ctx, int32_t n, int32_t nnz, int32_t k, int32_t
   sketch_launch(claim, 0, 1);
   {
     OnStream on(ctx, ctx.side[2]);
-    mirror_launch();
     runs_launch(1, -1);
     if (prepared != nullptr) SP_HIP(hipEventRecord(prepared, ctx.stream));
     sketch_launch(claim + 1, 1, -1);
