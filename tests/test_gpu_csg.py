@@ -321,6 +321,46 @@ def test_overflow_chunks_take_global_path(sporder, symmetric, chunk):
     assert np.array_equal(g.cpu().numpy(), o)
 
 
+def hub_rows_matrix(n, base_deg, hubs, seed, symmetric):
+    """Random rows of base_deg columns plus hub rows {row: degree} whose
+    columns are mostly distinct (empty runs within the chunk) with a few
+    shared with their chunk's rows; hub rows start at unaligned offsets."""
+    rng = np.random.default_rng(seed)
+    rows = [np.repeat(np.arange(n), base_deg)]
+    cols = [rng.integers(0, n, size=n * base_deg)]
+    for r, d in hubs.items():
+        rows.append(np.full(d, r))
+        cols.append(rng.choice(n, size=d, replace=False))
+    rows, cols = np.concatenate(rows), np.concatenate(cols)
+    if symmetric:
+        rows, cols = np.concatenate([rows, cols]), np.concatenate([cols, rows])
+    keys = np.unique(rows.astype(np.int64) * n + cols)
+    r, c = keys // n, keys % n
+    ptr = np.zeros(n + 1, np.int64)
+    np.cumsum(np.bincount(r, minlength=n), out=ptr[1:])
+    return ptr.astype(np.int32), c.astype(np.int32)
+
+
+@pytest.mark.parametrize("symmetric", [False, True])
+@pytest.mark.parametrize("chunk", [1024, 1500])
+def test_global_path_high_degree_rows(sporder, symmetric, chunk):
+    """Global-path rows of at least 2048 nonzeros visit only the 64-nonzero
+    blocks the run search marked as holding a non-empty run; chunks past the
+    LDS capacity holding rows of 2047, 2048 and 2049 up to 15,000 nonzeros
+    (many empty runs, unaligned block offsets) and ordinary chunks beside them
+    give the oracle's table and permutation bit for bit."""
+    hubs = {5: 2047, 6: 2048, 700: 2049, 701: 9000, 702: 9000, 703: 9000, 1031: 5000,
+            1032: 15000, 1033: 15000, 3003: 12000, 3004: 12000, 3005: 12000, 9001: 3333,
+            9002: 2500}
+    ptr, ind = hub_rows_matrix(20000, 3, hubs, 41, symmetric)
+    assert synth.is_pattern_symmetric(ptr, ind) == symmetric
+    check_table(sporder, ptr, ind, 16, 4.0, chunk, symmetric)
+    dptr, dind = dev_csr(ptr, ind)
+    g = sporder.chunk_similarity_greedy(dptr, dind, is_symmetric=symmetric, chunk_size=chunk)
+    o, _ = oracle.chunk_similarity_greedy(ptr, ind, is_symmetric=symmetric, chunk_size=chunk)
+    assert np.array_equal(g.cpu().numpy(), o)
+
+
 def test_tier2_split_symmetric(sporder):
     """On a symmetric pattern tier 2 keeps chunks of at most 28,672 nonzeros
     and the larger ones, up to its 32,768 capacity, go to the global path,
