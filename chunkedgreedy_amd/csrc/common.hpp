@@ -62,8 +62,12 @@ struct Context {
   Workspace aux; // second grow-only buffer, for temporaries sized mid-call
   // Three more streams (default priority) for independent kernels of one
   // call, forked from and joined back into `stream` with the events below, so
-  // a synchronize of `stream` also waits for their work.
+  // a synchronize of `stream` also waits for their work.  The four are the
+  // last of kMadeStreams streams made at init (make_streams: the earlier ones
+  // ran the side streams' kernels one after another in some processes).
   hipStream_t side[3] = {};
+  static constexpr int kMadeStreams = 8;
+  hipStream_t unused_streams[kMadeStreams - 4] = {};
   hipEvent_t fork_ev = nullptr;
   hipEvent_t join_ev[3] = {};
   hipEvent_t prep_ev = nullptr; // a stage's preparation done (csg's global path)
@@ -73,6 +77,7 @@ struct Context {
 
   void init();
   void destroy();
+  void make_streams();
   void sync() { SP_HIP(hipStreamSynchronize(stream)); }
 
   // Grow the workspace to hold `bytes` (rounded), then reset the cursor.

@@ -8,6 +8,37 @@
 
 namespace sporder_hip {
 
+namespace {
+__global__ void noop_kernel() {}
+} // namespace
+
+// The context's four streams (stream, side[0..2]) are the last four of eight
+// made here, each given one empty kernel when made.  csg's sketch runs three
+// long kernels at once on the side streams, and which streams run beside each
+// other depends on how the runtime maps streams onto its few hardware queues
+// per process (GPU_MAX_HW_QUEUES, 4 by default), which no call reports.
+// Measured on C5 (csg, median of 4 calls): in a process where torch had made
+// its stream first, the first four streams made afterwards took 37.5 ms (the
+// other global chunks' run search on side stream 2 started only when tier
+// 2's kernel on side stream 1 ended) and the next four 23.6 ms; in a process
+// whose first streams were these, both sets took 23.6-23.7 ms.  Bounded probe
+// kernels (a held stream against an empty kernel and an event on another, with
+// and without a cross-stream wait) found every pair of the eight running
+// beside each other, so the choice follows the measurement, not a probe.  The
+// first four stay unused until the context is destroyed.
+void Context::make_streams() {
+  hipStream_t made[kMadeStreams];
+  for (auto &s : made) {
+    SP_HIP(hipStreamCreate(&s));
+    noop_kernel<<<1, kWave, 0, s>>>();
+    SP_LAUNCH_CHECK();
+    SP_HIP(hipStreamSynchronize(s));
+  }
+  for (int i = 0; i < kMadeStreams - 4; ++i) unused_streams[i] = made[i];
+  stream = made[kMadeStreams - 4];
+  for (int i = 0; i < 3; ++i) side[i] = made[kMadeStreams - 3 + i];
+}
+
 void fail_hip(hipError_t err, const char *expr, const char *file, int line) {
   std::fprintf(stderr, "%s:%d: HIP error in %s: %s\n", file, line, expr,
                hipGetErrorString(err));
@@ -23,8 +54,7 @@ void fail_expect(const char *msg, const char *file, int line) {
 
 void Context::init() {
   SP_HIP(hipGetDevice(&device));
-  SP_HIP(hipStreamCreate(&stream));
-  for (auto &s : side) SP_HIP(hipStreamCreate(&s));
+  make_streams();
   SP_HIP(hipEventCreateWithFlags(&fork_ev, hipEventDisableTiming));
   for (auto &e : join_ev) SP_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
   SP_HIP(hipEventCreateWithFlags(&prep_ev, hipEventDisableTiming));
@@ -62,6 +92,7 @@ void Context::destroy() {
   SP_HIP(hipEventDestroy(fork_ev));
   for (auto &s : side) SP_HIP(hipStreamDestroy(s));
   SP_HIP(hipStreamDestroy(stream));
+  for (auto &s : unused_streams) SP_HIP(hipStreamDestroy(s));
   SP_HIP(hipSetDevice(cur));
 }
 
