@@ -1,9 +1,9 @@
-"""The three forms of the space-saving update at capacity 128 (add() item by
-item, the compiled feed_generic(), the GCN-assembly feed4()) leave the same
-slots, bit for bit, on streams dominated by evictions and by hits, for one
-wave and for many (tests/c/sketch_probe, built by build()).  The probe also
-prints each form's cost (kernel time, whole-GPU items/s, cycles per item of
-a wave)."""
+"""The forms of the space-saving update at capacity 128 (add() item by item,
+the compiled feed_generic(), the GCN-assembly feed4(), and the probe's own
+rank-per-slot alternative) leave the same slots, bit for bit, on streams
+dominated by evictions and by hits, for one wave and for many
+(tests/c/sketch_probe, built by build()).  The probe also prints each form's
+cost (kernel time, whole-GPU items/s, cycles per item of a wave)."""
 
 import subprocess
 from pathlib import Path
@@ -28,7 +28,8 @@ def test_sketch_forms_agree(args):
     print(out.stdout, flush=True)
     assert out.returncode == 0, out.stdout + out.stderr
     agree = [line for line in out.stdout.splitlines() if "equals_form0" in line]
-    assert agree == ["form=1 equals_form0=yes", "form=2 equals_form0=yes"]
+    assert agree == ["form=1 equals_form0=yes", "form=2 equals_form0=yes",
+                     "form=3 equals_form0=yes"]
 
 
 ISSUE = Path(__file__).resolve().parent / "c" / "issue_probe"
