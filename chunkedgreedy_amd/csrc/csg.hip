@@ -209,6 +209,147 @@ static_assert(32 * kGreedyBlock <= kOffMask && kPackedCap <= kOffMask &&
                   kGreedyCompactRows <= 4096 && kOffBits + 12 <= 31,
               "row header fields");
 
+// Byte offset of a pointer into this workgroup's LDS (for LDS instructions
+// written in assembly).
+__device__ __forceinline__ uint32_t lds_offset(const void *p) {
+  return static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void *)(p)));
+}
+
+// Why ahead_steps returned.
+constexpr int32_t kStepsEnd = 0;     // pos reached end
+constexpr int32_t kStepsRestart = 1; // cur placed; its row has no free in-chunk entry
+constexpr int32_t kStepsLong = 2;    // cur placed; its row has more than 64 entries
+constexpr int32_t kStepsRing = 3;    // 64 positions in the ring; cur not yet placed
+
+// Steps of the read-ahead walk (compacted rows in LDS, at most 64 bitmap
+// words), written as one block of GCN assembly; the compiled step issues about
+// a hundred instructions, most of them on the branch structure around its
+// three LDS reads.  One step: mark cur in the visited bitmap (lane w holds
+// word w), record start + cur in slot rp of the position ring, then take the
+// row's entries [d0, d1) (one per lane, lanes past the row repeat its last
+// one), read each entry's row headers s_off[c], s_off[c + 1] and its visited
+// bit (a ds_bpermute of the bitmap word), and move to the first entry that
+// is free -- the row's preference order -- with its headers as the next
+// row's.  Runs while pos < end and the ring has room; returns at the first
+// row that has no free entry or more than 64 entries (the caller finishes
+// that step), with nd0, nd1 the headers of the row last placed.  The ring's
+// rp slots (positions pos - rp ..) are the caller's to store.  With 64-bit
+// entries the chosen entry's weight is added to link_w and links counted as
+// the compiled step does.
+//
+// Wait states: a VALU write of an SGPR is read by a VALU instruction at least
+// two instructions later (v_readlane of the weight, then s_nop 1); lane selects
+// of v_readlane are written by s_ff1 three scalar instructions before.  LDS
+// instructions need no M0 here.  Every lane of the wave must be active.
+template <bool kPacked>
+__device__ __forceinline__ int32_t ahead_steps(uint32_t &bm0, uint32_t &ring, int32_t &rp,
+                                               int32_t &cur, int32_t &nd0, int32_t &nd1,
+                                               int32_t &pos, int32_t &links, float &link_w,
+                                               int32_t end, int32_t start, int32_t lane,
+                                               uint32_t ent_lds, uint32_t off_lds) {
+  int32_t st, w, d0, d1, len, lm1, l, wl;
+  uint64_t m, lm;
+  uint32_t vt, vval, vj, va, vcl, vwt, vo, vo0, vo1, vw, vword;
+  // All wave-uniform; readfirstlane states it, so that the compiler hands
+  // them over in scalar registers.
+  cur = __builtin_amdgcn_readfirstlane(cur);
+  nd0 = __builtin_amdgcn_readfirstlane(nd0);
+  nd1 = __builtin_amdgcn_readfirstlane(nd1);
+  pos = __builtin_amdgcn_readfirstlane(pos);
+  links = __builtin_amdgcn_readfirstlane(links);
+  rp = __builtin_amdgcn_readfirstlane(rp);
+  end = __builtin_amdgcn_readfirstlane(end);
+  ent_lds = __builtin_amdgcn_readfirstlane(ent_lds);
+  off_lds = __builtin_amdgcn_readfirstlane(off_lds);
+  asm volatile(
+      "0:\n\t"
+      "s_cmp_ge_i32 %[pos], %[end]\n\t"
+      "s_cbranch_scc1 8f\n\t"
+      "s_cmp_eq_u32 %[rp], 64\n\t"
+      "s_cbranch_scc1 5f\n\t"
+      // mark cur: word cur >> 5 (lane), bit cur & 31
+      "s_lshr_b32 %[w], %[cur], 5\n\t"
+      "v_cmp_eq_u32_e32 vcc, %[w], %[lane]\n\t"
+      "v_lshlrev_b32_e64 %[vt], %[cur], 1\n\t"
+      "v_cndmask_b32_e32 %[vt], 0, %[vt], vcc\n\t"
+      "v_or_b32_e32 %[bm0], %[bm0], %[vt]\n\t"
+      // ring slot rp <- start + cur
+      "v_cmp_eq_u32_e32 vcc, %[rp], %[lane]\n\t"
+      "v_add_u32_e32 %[vval], %[cur], %[startv]\n\t"
+      "v_cndmask_b32_e32 %[ring], %[ring], %[vval], vcc\n\t"
+      "s_add_u32 %[rp], %[rp], 1\n\t"
+      "s_add_u32 %[pos], %[pos], 1\n\t"
+      // cur's entries [d0, d1)
+      "s_and_b32 %[d0], %[nd0], 0x7fff\n\t"
+      "s_and_b32 %[d1], %[nd1], 0x7fff\n\t"
+      "s_sub_i32 %[len], %[d1], %[d0]\n\t"
+      "s_cmp_lt_i32 %[len], 1\n\t"
+      "s_cbranch_scc1 7f\n\t"
+      "s_cmp_gt_i32 %[len], 64\n\t"
+      "s_cbranch_scc1 6f\n\t"
+      "s_sub_u32 %[lm1], %[len], 1\n\t"
+      "v_min_u32_e32 %[vj], %[lm1], %[lane]\n\t"
+      "v_add_u32_e32 %[vj], %[d0], %[vj]\n\t"
+      ".if %[packed]\n\t"
+      "v_lshl_add_u32 %[va], %[vj], 1, %[entl]\n\t"
+      "ds_read_u16 %[vcl], %[va]\n\t"
+      ".else\n\t"
+      "v_lshl_add_u32 %[va], %[vj], 3, %[entl]\n\t"
+      "ds_read_b32 %[vcl], %[va]\n\t"
+      "ds_read_b32 %[vwt], %[va] offset:4\n\t"
+      ".endif\n\t"
+      "v_cmp_gt_u32_e64 %[lm], %[len], %[lane]\n\t"
+      "s_waitcnt lgkmcnt(0)\n\t"
+      // each entry's row headers and visited bit
+      "v_lshl_add_u32 %[vo], %[vcl], 2, %[offl]\n\t"
+      "ds_read_b32 %[vo0], %[vo]\n\t"
+      "ds_read_b32 %[vo1], %[vo] offset:4\n\t"
+      "v_lshrrev_b32_e32 %[vw], 3, %[vcl]\n\t"
+      "ds_bpermute_b32 %[vword], %[vw], %[bm0]\n\t"
+      "s_waitcnt lgkmcnt(0)\n\t"
+      "v_lshrrev_b32_e32 %[vword], %[vcl], %[vword]\n\t"
+      "v_and_b32_e32 %[vword], 1, %[vword]\n\t"
+      "v_cndmask_b32_e64 %[vword], 1, %[vword], %[lm]\n\t"
+      "v_cmp_eq_u32_e64 %[m], 0, %[vword]\n\t"
+      "s_ff1_i32_b64 %[l], %[m]\n\t"
+      "s_cmp_lt_i32 %[l], 0\n\t"
+      "s_cbranch_scc1 7f\n\t"
+      "s_add_u32 %[links], %[links], 1\n\t"
+      "v_readlane_b32 %[cur], %[vcl], %[l]\n\t"
+      "v_readlane_b32 %[nd0], %[vo0], %[l]\n\t"
+      "v_readlane_b32 %[nd1], %[vo1], %[l]\n\t"
+      ".if %[packed] == 0\n\t"
+      "v_readlane_b32 %[wl], %[vwt], %[l]\n\t"
+      "s_nop 1\n\t"
+      "v_add_f32_e32 %[linkw], %[wl], %[linkw]\n\t"
+      ".endif\n\t"
+      "s_branch 0b\n"
+      "5:\n\t"
+      "s_mov_b32 %[st], 3\n\t"
+      "s_branch 9f\n"
+      "6:\n\t"
+      "s_mov_b32 %[st], 2\n\t"
+      "s_branch 9f\n"
+      "7:\n\t"
+      "s_mov_b32 %[st], 1\n\t"
+      "s_branch 9f\n"
+      "8:\n\t"
+      "s_mov_b32 %[st], 0\n"
+      "9:"
+      : [bm0] "+v"(bm0), [ring] "+v"(ring), [linkw] "+v"(link_w), [rp] "+s"(rp),
+        [cur] "+s"(cur), [nd0] "+s"(nd0), [nd1] "+s"(nd1), [pos] "+s"(pos),
+        [links] "+s"(links), [st] "=&s"(st), [w] "=&s"(w), [d0] "=&s"(d0), [d1] "=&s"(d1),
+        [len] "=&s"(len), [lm1] "=&s"(lm1), [l] "=&s"(l), [wl] "=&s"(wl), [m] "=&s"(m),
+        [lm] "=&s"(lm), [vt] "=&v"(vt), [vval] "=&v"(vval), [vj] "=&v"(vj), [va] "=&v"(va),
+        [vcl] "=&v"(vcl), [vwt] "=&v"(vwt), [vo] "=&v"(vo), [vo0] "=&v"(vo0),
+        [vo1] "=&v"(vo1), [vw] "=&v"(vw), [vword] "=&v"(vword)
+      : [end] "s"(end), [startv] "v"(start), [lane] "v"(lane), [entl] "s"(ent_lds),
+        [offl] "s"(off_lds), [packed] "i"(kPacked ? 1 : 0)
+      : "vcc", "scc", "memory");
+  return st;
+}
+
 // Rows of at most kPackedSortK table entries are packed by a sorting network
 // in registers (pack_row_sorted).
 constexpr int32_t kPackedSortK = 16;
@@ -590,10 +731,31 @@ __global__ void __launch_bounds__(kGreedyBlock)
     // Offsets of the next row, read ahead by the step that chose it.
     bool have_next = false;
     int32_t nd0 = 0, nd1 = 0;
+    // Read-ahead walks over at most 64 bitmap words run their steps in
+    // ahead_steps; a step it hands back (a row without a free entry, or of
+    // more than 64 entries) is finished below.
+    const bool steps_asm = kAhead && words <= kWave;
+    const uint32_t ent_lds = lds_offset(smem_u64), off_lds = lds_offset(s_off);
     while (pos < end) {
-      mark_bits(cur >> 5, 1u << (cur & 31));
-      if (lane == 0) order[pos] = start + cur;
-      pos += 1;
+      int32_t steps_st = -1;
+      if (kAhead && steps_asm) {
+        if (!have_next) {
+          nd0 = s_off[cur];
+          nd1 = s_off[cur + 1];
+        }
+        uint32_t ring = 0u;
+        int32_t rp = 0;
+        steps_st = ahead_steps<kPacked>(bm0, ring, rp, cur, nd0, nd1, pos, links, link_w, end,
+                                        start, lane, ent_lds, off_lds);
+        if (lane < rp) order[pos - rp + lane] = ring;
+        have_next = true; // nd0, nd1: the headers of cur
+        if (steps_st == kStepsEnd) break;
+        if (steps_st == kStepsRing) continue;
+      } else {
+        mark_bits(cur >> 5, 1u << (cur & 31));
+        if (lane == 0) order[pos] = start + cur;
+        pos += 1;
+      }
       int32_t h0, h1; // row headers of cur and cur + 1 (offsets for table reads)
       if constexpr (kAhead) {
         h0 = have_next ? nd0 : s_off[cur];
@@ -607,7 +769,7 @@ __global__ void __launch_bounds__(kGreedyBlock)
       const int32_t d1 = kSorted ? (h1 & kOffMask) : h1;
       float best_w = -1.0f;
       int32_t best_c = -1;
-      if (d1 > d0) {
+      if (d1 > d0 && steps_st != kStepsRestart) {
         // kWalkSingle: the row's first (preferred) entry comes with its header;
         // its visited bit is a lane read of the bitmap word.  Weights are read
         // only for the statistics.  (With read-ahead, taking the first entry
