@@ -312,6 +312,35 @@ def band(n: int, half_width: int = 2) -> Csr:
     return _coo_to_csr(n, r, c, np.ones(r.shape[0], np.float32))
 
 
+def dense_groups(n: int = 8192, chunk: int = 1024, seed: int = 5) -> Csr:
+    """Two dense row groups per chunk of `chunk` rows, every other row alone:
+    rows 0..71 of a chunk hold each of the chunk's columns 0..23 with
+    probability 0.7 (about 70 in-chunk similar rows each, past one wave's 64
+    lanes), rows 100..139 each of columns 30..45 with probability 0.6 and
+    now and then one of the first group's columns (about 40); the rest hold
+    only their diagonal.  With k >= 72 the chain walks rows of both lengths in
+    one chunk.  Values 1."""
+    rng = _rng(seed)
+    rows, cols = [], []
+    for r in range(n):
+        base = (r // chunk) * chunk
+        o = r - base
+        if o < 72:
+            c = base + np.nonzero(rng.random(24) < 0.7)[0]
+        elif 100 <= o < 140:
+            c = base + 30 + np.nonzero(rng.random(16) < 0.6)[0]
+            if rng.random() < 0.1:
+                c = np.append(c, base + int(rng.integers(0, 24)))
+        else:
+            c = np.array([r])
+        c = np.unique(c[c < n]) if c.size else np.array([r])
+        rows.append(np.full(c.size, r, np.int64))
+        cols.append(c.astype(np.int64))
+    r = np.concatenate(rows)
+    c = np.concatenate(cols)
+    return _coo_to_csr(n, r, c, np.ones(r.shape[0], np.float32))
+
+
 def is_pattern_symmetric(ptr, ind) -> bool:
     """Pattern equals its transpose (the harness test of
     bench/reorder/reorder_bench/loader.py:86-88 on the pattern)."""

@@ -29,7 +29,9 @@
 //   variant 0: the kernel's walk, its mode chosen as the kernel chooses it
 //              (table reads when the slice is neither staged nor packed, else
 //              the one-entry mode when at least half the rows with entries
-//              have exactly one, else the sorted scan with read-ahead);
+//              have exactly one, else the sorted scan with read-ahead, whose
+//              steps over rows of at most 64 entries are the assembly block's
+//              when the chunk has at most 64 bitmap words);
 //   variants 1, 2, 3: the kernel's table, one-entry and sorted modes forced
 //              (1 only applies to a slice past entry_cap, 2 and 3 to a
 //              compacted one);
@@ -58,6 +60,7 @@ struct Diag {
   int64_t misread = 0;  // shuffles from an inactive lane whose value was not 0
   int64_t runaway = 0;  // walks stopped by the model's step cap
   int64_t steps = 0;
+  int64_t asm_exits[4] = {0, 0, 0, 0}; // assembly block returns: end, restart, long row, ring
 };
 
 inline int32_t wi_index(uint64_t v) { return static_cast<int32_t>(static_cast<uint32_t>(v)) - 1; }
@@ -256,15 +259,86 @@ void walk_kernel(const Chunk &c, int mode, bool packed, int32_t k, int32_t rows_
   int32_t nd0 = 0, nd1 = 0;
   const int64_t cap = 4 * static_cast<int64_t>(c.size) + 64;
   int64_t steps = 0;
+  // Read-ahead walks over at most 64 bitmap words run their steps in the
+  // kernel's assembly block (ahead_steps): every lane active, lanes past the
+  // row repeating its last entry, positions held in a ring and stored when
+  // the block returns (at a row with no free entry or more than 64 entries,
+  // a full ring, or pos = end).
+  const bool asm_steps = ahead && c.words <= W;
   while (pos < c.end) {
-    if (++steps > cap) {
-      d.runaway += 1;
-      break;
+    int st = -1; // 0 end, 1 restart, 2 long row, 3 full ring
+    if (asm_steps) {
+      if (!have_next) {
+        nd0 = off.get(cur);
+        nd1 = off.get(cur + 1);
+      }
+      int32_t ring[W];
+      int rp = 0;
+      while (true) {
+        if (pos >= c.end) {
+          st = 0;
+          break;
+        }
+        if (rp == W) {
+          st = 3;
+          break;
+        }
+        if (++steps > cap) {
+          d.runaway += 1;
+          st = 0;
+          break;
+        }
+        d.steps += 1;
+        mark(cur >> 5, 1u << (cur & 31));
+        ring[rp++] = cur;
+        pos += 1;
+        const int32_t a0 = nd0 & kOffMask, len = (nd1 & kOffMask) - a0;
+        if (len < 1) {
+          st = 1;
+          break;
+        }
+        if (len > W) {
+          st = 2;
+          break;
+        }
+        int32_t cl[W], o0[W], o1[W], wi[W];
+        for (int l = 0; l < W; ++l) {
+          const int32_t j = std::min(l, len - 1);
+          cl[l] = packed ? static_cast<int32_t>(ent16.get(a0 + j))
+                         : static_cast<int32_t>(static_cast<uint32_t>(ent.get(a0 + j)));
+          o0[l] = off.get(cl[l]);
+          o1[l] = off.get(cl[l] + 1);
+          wi[l] = (cl[l] >> 5) & (W - 1); // ds_bpermute lane: address (cl >> 3), bits 7:2
+        }
+        uint32_t word[W];
+        wv.shfl(bm0, wi, all, word);
+        bool p[W];
+        for (int l = 0; l < W; ++l) p[l] = l < len && !((word[l] >> (cl[l] & 31)) & 1u);
+        const uint64_t m = Wave::ballot(p, all);
+        if (m == 0) {
+          st = 1;
+          break;
+        }
+        const int l = ctz64(m);
+        cur = cl[l];
+        nd0 = o0[l];
+        nd1 = o1[l];
+      }
+      for (int i = 0; i < rp; ++i) out.put(pos - rp + i, ring[i]);
+      d.asm_exits[st] += 1;
+      have_next = true;
+      if (st == 0) break;
+      if (st == 3) continue;
+    } else {
+      if (++steps > cap) {
+        d.runaway += 1;
+        break;
+      }
+      d.steps += 1;
+      mark(cur >> 5, 1u << (cur & 31));
+      out.put(pos, cur);
+      pos += 1;
     }
-    d.steps += 1;
-    mark(cur >> 5, 1u << (cur & 31));
-    out.put(pos, cur);
-    pos += 1;
     int32_t h0, h1;
     if (ahead) {
       h0 = have_next ? nd0 : off.get(cur);
@@ -277,7 +351,7 @@ void walk_kernel(const Chunk &c, int mode, bool packed, int32_t k, int32_t rows_
     const int32_t d0 = sorted ? (h0 & kOffMask) : h0;
     const int32_t d1 = sorted ? (h1 & kOffMask) : h1;
     int32_t best_c = -1;
-    if (d1 > d0) {
+    if (d1 > d0 && st != 1) {
       const int32_t c0 = (h0 >> kOffBits) & 0xFFF;
       bool first_free = false;
       if (single) {
@@ -642,8 +716,9 @@ extern "C" {
 
 // Runs the modelled walk over every chunk of `table` (n rows of k packed
 // entries).  `order` receives the permutation (positions a walk did not
-// write keep their previous value); diag[0..5] = overrun, revisit, oob,
-// misread, runaway, steps; mode_counts[0..5] = chunks walked in table,
+// write keep their previous value); diag[0..9] = overrun, revisit, oob,
+// misread, runaway, steps, and the assembly step block's returns at pos = end,
+// for a restart, at a row of more than 64 entries and at a full ring; mode_counts[0..5] = chunks walked in table,
 // one-entry and sorted mode (variant 0), of those in a 16-bit packed form
 // (one-entry, sorted), and chunks taken by the second launch.  packed_cap 0:
 // no packed form and one launch (the wide launch, or statistics asked for).
@@ -699,6 +774,7 @@ int32_t chain_model(int32_t n, int32_t k, int32_t chunk_size, const uint64_t *ta
   diag[3] = d.misread;
   diag[4] = d.runaway;
   diag[5] = d.steps;
+  for (int i = 0; i < 4; ++i) diag[6 + i] = d.asm_exits[i];
   return 0;
 }
 

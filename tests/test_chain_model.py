@@ -47,12 +47,13 @@ def model(tmp_path_factory):
         table = np.ascontiguousarray(table, np.uint64)
         n, k = table.shape
         order = np.full(n, -1, np.int32)
-        diag = np.zeros(6, np.int64)
+        diag = np.zeros(10, np.int64)
         modes = np.zeros(6, np.int64)
         rc = lib.chain_model(n, k, chunk, table.ctypes.data, entry_cap, packed_cap, variant,
                              inactive_zero, order.ctypes.data, diag.ctypes.data,
                              modes.ctypes.data)
-        keys = ("overrun", "revisit", "oob", "misread", "runaway", "steps")
+        keys = ("overrun", "revisit", "oob", "misread", "runaway", "steps",
+                "asm_end", "asm_restart", "asm_long", "asm_ring")
         m = modes.tolist()
         return rc, order, dict(zip(keys, diag.tolist())), (m if all_modes else m[:3])
 
@@ -185,3 +186,25 @@ def test_packed_modes_and_second_launch_are_exercised(model):
     assert np.array_equal(order, want)
     chunks = -(-table.shape[0] // 1024)
     assert modes[3] + modes[4] == chunks and modes[5] >= chunks - 1, modes
+
+
+def test_assembly_step_exits(model):
+    """The read-ahead steps the kernel runs in assembly (chunks of at most 64
+    bitmap words) hand a step back at a row of more than 64 in-chunk entries,
+    at a row with no free entry and when the position ring is full; the model
+    takes each of those returns and still gives the oracle's order.  Rows of
+    about 70 and 40 in-chunk entries in one chunk (synth.dense_groups, k = 96,
+    the 8192-entry staging of at most two chunks per CU); C1 at the same
+    staging fills the ring."""
+    ptr, ind, _ = synth.dense_groups()
+    table, want = table_and_order(ptr, ind, 96, 1024)
+    rc, order, diag, modes = model(table, 1024, 8192, 0)
+    assert rc == 0 and {key: diag[key] for key in CLEAN} == CLEAN
+    assert np.array_equal(order, want)
+    assert modes[2] == 8, modes
+    assert diag["asm_long"] > 0 and diag["asm_restart"] > 0, diag
+    table, want = table_and_order(*MATS["C1"], 16, 1024)
+    rc, order, diag, _ = model(table, 1024, 8192, 0)
+    assert rc == 0 and {key: diag[key] for key in CLEAN} == CLEAN
+    assert np.array_equal(order, want)
+    assert diag["asm_ring"] > 0, diag

@@ -273,6 +273,31 @@ def test_full_config_bit_exact(sporder, name):
         del B, C, ref
 
 
+@pytest.mark.parametrize("k,chunk", [(96, 1024), (72, 1024), (128, 2048), (96, 512)])
+def test_csg_rows_past_one_wave(sporder, k, chunk):
+    """Chunks whose rows hold about 70 and about 40 in-chunk entries
+    (synth.dense_groups): the chain's read-ahead steps run in assembly for the
+    shorter rows and hand the longer ones (more than 64 entries, past one
+    wave's lanes) to the compiled scan; 2048-row chunks (64 bitmap words)
+    are the largest the assembly steps take.  Permutation, restarts and
+    followed weight bit-exact against the oracle."""
+    ptr, ind, _ = synth.dense_groups()
+    sym = synth.is_pattern_symmetric(ptr, ind)
+    print(f"[dense-groups] k={k} chunk={chunk}", flush=True)
+    dptr, dind = dev_csr(ptr, ind)
+    for with_stats in (True, False):
+        got = sporder.chunk_similarity_greedy(dptr, dind, is_symmetric=sym, k=k,
+                                              chunk_size=chunk, with_stats=with_stats)
+        order, stats = got if with_stats else (got, None)
+        o_order, o_stats = oracle.chunk_similarity_greedy(ptr, ind, is_symmetric=sym, k=k,
+                                                          chunk_size=chunk)
+        assert np.array_equal(order.cpu().numpy(), o_order), with_stats
+        if stats is not None:
+            assert stats["chain_restarts"] == o_stats["chain_restarts"]
+            assert stats["avg_followed_weight"] == pytest.approx(
+                o_stats["avg_followed_weight"], rel=1e-9, abs=1e-12)
+
+
 @pytest.mark.parametrize("name", ["C2r", "C4n", "RGG20"])
 def test_locality_inputs_bit_exact(sporder, name):
     """The inputs with in-chunk locality at full size (C2 in planted row order,
