@@ -350,6 +350,118 @@ __device__ __forceinline__ int32_t ahead_steps(uint32_t &bm0, uint32_t &ring, in
   return st;
 }
 
+// The walk's restart for chunks of at most 64 bitmap words, as one block of
+// GCN assembly (the compiled search issues about 65 instructions per bitmap
+// word).  Per word, lowest first from low_word: the word's free rows (lane w
+// of ~bm0, masked by full_lane: the chunk's rows of that word, 0 past the
+// chunk's words); the rows among them that have entries (headers s_off[r],
+// s_off[r + 1], read by every lane for row min(w * 32 + (lane & 31), size - 1));
+// the free rows below the first row with entries are emitted in index order at
+// positions pos .. (stored while below end_rel, relative to the chunk's
+// order_chunk), marked visited and counted into pos and restarts.  Returns the
+// first free row with entries (the walk continues there), or -1 when no row
+// is free.  kSorted: headers carry the first entry above kOffBits.  The block
+// stores the emitted rows itself, under an exec mask of those lanes (the entry
+// mask is restored after the store); every lane of the wave must be active.
+template <bool kSorted>
+__device__ __forceinline__ int32_t restart_search(uint32_t &bm0, int32_t &low_word,
+                                                  int32_t &pos, int32_t &restarts,
+                                                  int32_t lane, uint32_t full_lane,
+                                                  uint32_t off_lds, int32_t size_m1,
+                                                  int32_t *order_chunk, int32_t start,
+                                                  int32_t end_rel) {
+  int32_t nxt, w, rb, fb, we, fe, em, emx, prel, sr, c;
+  uint64_t m, sx;
+  uint32_t vf, vr, va, vo0, vo1, vi, vval, vt, vl31;
+  low_word = __builtin_amdgcn_readfirstlane(low_word);
+  pos = __builtin_amdgcn_readfirstlane(pos);
+  restarts = __builtin_amdgcn_readfirstlane(restarts);
+  off_lds = __builtin_amdgcn_readfirstlane(off_lds);
+  size_m1 = __builtin_amdgcn_readfirstlane(size_m1);
+  start = __builtin_amdgcn_readfirstlane(start);
+  end_rel = __builtin_amdgcn_readfirstlane(end_rel);
+  const uint64_t obase = static_cast<uint64_t>(reinterpret_cast<uintptr_t>(order_chunk));
+  const uint64_t ob = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(
+                          static_cast<int32_t>(obase))) |
+                      (static_cast<uint64_t>(static_cast<uint32_t>(
+                           __builtin_amdgcn_readfirstlane(static_cast<int32_t>(obase >> 32))))
+                       << 32);
+  asm volatile(
+      "s_mov_b32 %[nxt], -1\n\t"
+      "v_and_b32_e32 %[vl31], 31, %[lane]\n"
+      "1:\n\t"
+      // lowest word at or after low_word with a free row
+      "v_not_b32_e32 %[vf], %[bm0]\n\t"
+      "v_and_b32_e32 %[vf], %[vf], %[full]\n\t"
+      "v_cmp_le_u32_e32 vcc, %[low], %[lane]\n\t"
+      "v_cndmask_b32_e32 %[vf], 0, %[vf], vcc\n\t"
+      "v_cmp_ne_u32_e64 %[m], 0, %[vf]\n\t"
+      "s_ff1_i32_b64 %[w], %[m]\n\t"
+      "s_cmp_lt_i32 %[w], 0\n\t"
+      "s_cbranch_scc1 9f\n\t"
+      "s_mov_b32 %[low], %[w]\n\t"
+      "s_lshl_b32 %[rb], %[w], 5\n\t"
+      "v_readlane_b32 %[fb], %[vf], %[w]\n\t"
+      // which of the word's rows have entries
+      "v_add_u32_e32 %[vr], %[rb], %[vl31]\n\t"
+      "v_min_u32_e32 %[vr], %[szm1], %[vr]\n\t"
+      "v_lshl_add_u32 %[va], %[vr], 2, %[offl]\n\t"
+      "ds_read_b32 %[vo0], %[va]\n\t"
+      "ds_read_b32 %[vo1], %[va] offset:4\n\t"
+      "s_waitcnt lgkmcnt(0)\n\t"
+      ".if %[sorted]\n\t"
+      "v_and_b32_e32 %[vo0], 0x7fff, %[vo0]\n\t"
+      "v_and_b32_e32 %[vo1], 0x7fff, %[vo1]\n\t"
+      ".endif\n\t"
+      "v_cmp_gt_u32_e32 vcc, %[vo1], %[vo0]\n\t"
+      "s_and_b32 %[we], vcc_lo, %[fb]\n\t"
+      // emit = we ? fb & ((1 << ctz(we)) - 1) : fb
+      "s_ff1_i32_b32 %[fe], %[we]\n\t"
+      "s_bfm_b32 %[em], %[fe], 0\n\t"
+      "s_and_b32 %[em], %[em], %[fb]\n\t"
+      "s_cmp_eq_u32 %[we], 0\n\t"
+      "s_cselect_b32 %[em], %[fb], %[em]\n\t"
+      "s_cmp_eq_u32 %[em], 0\n\t"
+      "s_cbranch_scc1 3f\n\t"
+      // store the emitted rows at pos + their rank, below end
+      "s_sub_u32 %[prel], %[pos], %[start]\n\t"
+      "v_mbcnt_lo_u32_b32 %[vi], %[em], 0\n\t"
+      "v_add_u32_e32 %[vi], %[prel], %[vi]\n\t"
+      "v_cmp_gt_u32_e32 vcc, %[endrel], %[vi]\n\t"
+      "s_and_b32 %[emx], vcc_lo, %[em]\n\t"
+      "s_add_u32 %[sr], %[rb], %[start]\n\t"
+      "v_add_u32_e32 %[vval], %[sr], %[vl31]\n\t"
+      "v_lshlrev_b32_e32 %[vi], 2, %[vi]\n\t"
+      "s_mov_b64 %[sx], exec\n\t"
+      "s_mov_b32 exec_hi, 0\n\t"
+      "s_mov_b32 exec_lo, %[emx]\n\t"
+      "global_store_dword %[vi], %[vval], %[ob]\n\t"
+      "s_mov_b64 exec, %[sx]\n\t"
+      // mark them visited
+      "v_cmp_eq_u32_e32 vcc, %[w], %[lane]\n\t"
+      "v_mov_b32_e32 %[vt], %[em]\n\t"
+      "v_cndmask_b32_e32 %[vt], 0, %[vt], vcc\n\t"
+      "v_or_b32_e32 %[bm0], %[bm0], %[vt]\n\t"
+      "s_bcnt1_i32_b32 %[c], %[em]\n\t"
+      "s_add_u32 %[pos], %[pos], %[c]\n\t"
+      "s_add_u32 %[rst], %[rst], %[c]\n"
+      "3:\n\t"
+      "s_cmp_eq_u32 %[we], 0\n\t"
+      "s_cbranch_scc1 1b\n\t"
+      "s_add_u32 %[nxt], %[rb], %[fe]\n"
+      "9:"
+      : [bm0] "+v"(bm0), [low] "+s"(low_word), [pos] "+s"(pos), [rst] "+s"(restarts),
+        [nxt] "=&s"(nxt), [w] "=&s"(w), [rb] "=&s"(rb), [fb] "=&s"(fb), [we] "=&s"(we),
+        [fe] "=&s"(fe), [em] "=&s"(em), [emx] "=&s"(emx), [prel] "=&s"(prel), [sr] "=&s"(sr),
+        [c] "=&s"(c), [m] "=&s"(m), [sx] "=&s"(sx), [vf] "=&v"(vf), [vr] "=&v"(vr), [va] "=&v"(va),
+        [vo0] "=&v"(vo0), [vo1] "=&v"(vo1), [vi] "=&v"(vi), [vval] "=&v"(vval), [vt] "=&v"(vt),
+        [vl31] "=&v"(vl31)
+      : [lane] "v"(lane), [full] "v"(full_lane), [offl] "s"(off_lds), [szm1] "s"(size_m1),
+        [ob] "s"(ob), [start] "s"(start), [endrel] "s"(end_rel), [sorted] "i"(kSorted ? 1 : 0)
+      : "vcc", "scc", "memory");
+  return nxt;
+}
+
 // Rows of at most kPackedSortK table entries are packed by a sorting network
 // in registers (pack_row_sorted).
 constexpr int32_t kPackedSortK = 16;
@@ -736,6 +848,8 @@ __global__ void __launch_bounds__(kGreedyBlock)
     // more than 64 entries) is finished below.
     const bool steps_asm = kAhead && words <= kWave;
     const uint32_t ent_lds = lds_offset(smem_u64), off_lds = lds_offset(s_off);
+    // The restart search's rows of each bitmap word (assembly form).
+    const uint32_t full_lane = lane < words ? full_bits(lane) : 0u;
     while (pos < end) {
       int32_t steps_st = -1;
       if (kAhead && steps_asm) {
@@ -887,7 +1001,11 @@ __global__ void __launch_bounds__(kGreedyBlock)
       // bitmap word below the first row that has entries are exactly the next
       // restarts, in index order: emit them in one step.
       int32_t nxt = -1;
-      while (true) {
+      if (words <= kWave) {
+        nxt = restart_search<kSorted>(bm0, low_word, pos, restarts, lane, full_lane, off_lds,
+                                      size - 1, order + start, start, end - start);
+      }
+      while (words > kWave) {
         // Lowest word at or after low_word with a free bit.
         const uint32_t f0 =
             (lane < words && lane >= low_word) ? (~bm0 & full_bits(lane)) : 0u;
