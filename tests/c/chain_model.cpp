@@ -484,8 +484,16 @@ void walk_kernel(const Chunk &c, int mode, bool packed, int32_t k, int32_t rows_
       for (int l = 0; l < W; ++l) {
         const int32_t r = w * 32 + (l & 31);
         const bool free_here = l < 32 && ((free_bits >> (l & 31)) & 1u);
-        has[l] = free_here && (sorted ? (off.get(r + 1) & kOffMask) > (off.get(r) & kOffMask)
-                                      : off.get(r + 1) > off.get(r));
+        if (c.words <= W) {
+          // The assembly search (restart_search): every lane reads the
+          // headers of its row, clamped to the chunk's last row.
+          const int32_t rc = std::min(r, c.size - 1);
+          const int32_t a0 = off.get(rc), a1 = off.get(rc + 1);
+          has[l] = free_here && (sorted ? (a1 & kOffMask) > (a0 & kOffMask) : a1 > a0);
+        } else {
+          has[l] = free_here && (sorted ? (off.get(r + 1) & kOffMask) > (off.get(r) & kOffMask)
+                                        : off.get(r + 1) > off.get(r));
+        }
       }
       const uint32_t with_entries = static_cast<uint32_t>(Wave::ballot(has, all));
       const uint32_t emit =
