@@ -17,7 +17,10 @@
 //   1  feed_generic() (the compiled two-loop update),
 //   2  feed4() (the GCN-assembly update used at capacity 128),
 //   3  RankSketch below (compiled): a rank per slot, the victim found by
-//      ballot(rank == 0) instead of the DPP minimum; measured, not used.
+//      ballot(rank == 0) instead of the DPP minimum; measured, not used,
+//   4  QueueSketch below: feed4() with the eviction order kept between
+//      evictions (a sort serves about 60 evictions on C3's hub stream, the
+//      front taken by scalar tests); measured, not used.
 // Per form: kernel time (third of three launches), whole-GPU items/s, and
 // the mean s_memtime cycles per item of a wave.  Then whether each form's
 // final slots (keys and weight bits) equal form 0's.  Exit status 0 when they
@@ -147,6 +150,230 @@ struct RankSketch {
 
 } // namespace
 
+// The eviction order of a full capacity-128 sketch (WaveSketch<4>), kept
+// between evictions by QueueSketch::feed().  One bitonic sort of the 128 (weight, 64j + p)
+// keys puts the 64 smallest slots, in eviction order, one per lane; later
+// evictions take them from the front while the front's weight is below
+// `bound`, a lower bound of every slot outside the unevicted queue: the
+// 65th smallest weight at the sort, lowered to each evicted slot's new
+// weight.  A hit on a queued slot takes it out of the queue and lowers the
+// bound to its new weight.  Queued slots are untouched and stay in key order,
+// and every other slot weighs at least the bound, so a front below the bound
+// is the minimum key that the full reduction would find; otherwise the
+// eviction sorts again.
+struct MinQueue {
+  uint32_t qw;    // lane r: weight bits of the r-th smallest slot at the sort
+  uint32_t qs;    // lane r: that slot as 64j + p (local cell j, physical lane p)
+  int32_t head;   // wave-uniform: next lane to evict; 64 = nothing queued
+  uint32_t bound; // wave-uniform: see above; 0 = sort at the next eviction
+  uint64_t qm[2]; // wave-uniform, per cell: lanes whose slot is queued, not evicted
+
+  __device__ __forceinline__ void reset() {
+    qw = 0;
+    qs = 0;
+    head = 64;
+    bound = 0;
+    qm[0] = 0;
+    qm[1] = 0;
+  }
+};
+
+// Form 4: WaveSketch<4> with its eviction order kept in a MinQueue.
+struct QueueSketch {
+  WaveSketch<4> s;
+  MinQueue q;
+
+  __device__ __forceinline__ void clear() {
+    s.clear();
+    q.reset();
+  }
+
+  // feed4() on a full sketch with the eviction order kept in a
+  // MinQueue: the same updates item by item, but an eviction takes the
+  // queue's front (two lane reads and scalar tests) instead of the wave
+  // minimum (six DPP steps and two vector-to-scalar round trips), and sorts
+  // the sketch again only when the front may no longer be the minimum.  On
+  // one hub row's long stream the new weight (minimum + w) lands above the
+  // queue's remaining slots nearly always, so each sort serves about 60
+  // evictions.  While slots are free it is feed4(), and the queue is empty.
+  __device__ __forceinline__ void feed(uint64_t mask, int32_t other, float alpha) {
+        if (__builtin_amdgcn_readfirstlane(s.filled) < 128) {
+      s.feed4(mask, other, alpha);
+      q.reset();
+      return;
+    }
+    const int lane = lane_id();
+    mask = uniform_mask(mask);
+    for (;;) {
+      uint32_t need, kk, ww;
+      queue_steps(mask, other, alpha, need, kk, ww);
+      if (need == 0) return;
+      // The front may not be the minimum: sort the 128 (weight, 64j + p)
+      // keys, queue the 64 smallest, and evict the smallest for (kk, ww).
+      uint32_t hi[2] = {__float_as_uint(s.wt[0]), __float_as_uint(s.wt[1])};
+      uint32_t lo[2] = {static_cast<uint32_t>(lane), static_cast<uint32_t>(64 + lane)};
+      bitonic_sort128(hi, lo);
+      const uint64_t kth =
+          (static_cast<uint64_t>(static_cast<uint32_t>(readlane(static_cast<int32_t>(hi[0]), 63)))
+           << 32) |
+          static_cast<uint32_t>(readlane(static_cast<int32_t>(lo[0]), 63));
+      const uint64_t mine0 = (static_cast<uint64_t>(__float_as_uint(s.wt[0])) << 32) |
+                             static_cast<uint32_t>(lane);
+      const uint64_t mine1 = (static_cast<uint64_t>(__float_as_uint(s.wt[1])) << 32) |
+                             static_cast<uint32_t>(64 + lane);
+      uint64_t qm0 = ballot(mine0 <= kth), qm1 = ballot(mine1 <= kth);
+      const uint32_t wq = static_cast<uint32_t>(readlane(static_cast<int32_t>(hi[0]), 0));
+      const uint32_t slot = static_cast<uint32_t>(readlane(static_cast<int32_t>(lo[0]), 0));
+      uint32_t bound = static_cast<uint32_t>(readlane(static_cast<int32_t>(hi[1]), 0));
+      q.qw = hi[0];
+      q.qs = lo[0];
+      const float wn = __uint_as_float(ww) + __uint_as_float(wq); // the slot holds wq
+      const uint64_t sel = 1ull << (slot & 63u);
+      if (slot < 64u) {
+        s.key[0] = mask_select(sel, static_cast<int32_t>(kk), s.key[0]);
+        s.wt[0] = __int_as_float(mask_select(sel, __float_as_int(wn), __float_as_int(s.wt[0])));
+        qm0 &= ~sel;
+      } else {
+        s.key[1] = mask_select(sel, static_cast<int32_t>(kk), s.key[1]);
+        s.wt[1] = __int_as_float(mask_select(sel, __float_as_int(wn), __float_as_int(s.wt[1])));
+        qm1 &= ~sel;
+      }
+      bound = min(bound, __float_as_uint(wn));
+      q.bound = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int32_t>(bound)));
+      q.qm[0] = uniform_mask(qm0);
+      q.qm[1] = uniform_mask(qm1);
+      q.head = 1;
+      if (mask == 0) return;
+    }
+  }
+
+  static __device__ __forceinline__ uint64_t uniform_mask(uint64_t m) {
+    return static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int32_t>(m))) |
+           (static_cast<uint64_t>(static_cast<uint32_t>(
+                __builtin_amdgcn_readfirstlane(static_cast<int32_t>(m >> 32))))
+            << 32);
+  }
+
+  // feed()'s item loop, one block of GCN assembly in feed4()'s style.  A
+  // hit adds w in both cells by their hit masks; when it hits a queued slot,
+  // that slot leaves the queue (its mask bit cleared) and the bound drops to
+  // its new weight (v_readlane of the hit lane).  A miss skips front entries
+  // whose slot left the queue, and evicts the front when its weight is below
+  // the bound: v_writelane of k at the slot's lane (M0), wq + w by a select
+  // on the one-hot lane mask, the slot's queue bit cleared, the bound
+  // lowered to the new weight.  Otherwise it stops with need = 1 and the
+  // item (kk, ww) for the caller to evict after a sort; need = 0 when the
+  // mask is exhausted.  Every lane of the wave must be active.
+  __device__ __forceinline__ void queue_steps(uint64_t &mask, int32_t other, float alpha, uint32_t &need,
+                                              uint32_t &kk, uint32_t &ww) {
+    uint32_t i, p, slot, wq, nw, m0_saved;
+    uint64_t h0, h1, any, sel;
+    float t;
+    int32_t head = __builtin_amdgcn_readfirstlane(q.head);
+    uint32_t bound = static_cast<uint32_t>(
+        __builtin_amdgcn_readfirstlane(static_cast<int32_t>(q.bound)));
+    uint64_t qm0 = uniform_mask(q.qm[0]), qm1 = uniform_mask(q.qm[1]);
+    asm volatile(
+        "s_mov_b32 %[m0s], m0\n\t"
+        "s_mov_b32 %[need], 0\n\t"
+        "s_cmp_eq_u64 %[mask], 0\n\t"
+        "s_cbranch_scc1 9f\n"
+        "5:\n\t"
+        "s_ff1_i32_b64 %[i], %[mask]\n\t"
+        "s_bitset0_b64 %[mask], %[i]\n\t"
+        "v_readlane_b32 %[kk], %[other], %[i]\n\t"
+        "v_readlane_b32 %[ww], %[alpha], %[i]\n\t"
+        "s_nop 0\n\t"
+        "v_cmp_eq_u32_e64 %[h0], %[kk], %[k0]\n\t"
+        "v_cmp_eq_u32_e64 %[h1], %[kk], %[k1]\n\t"
+        "s_or_b64 %[any], %[h0], %[h1]\n\t"
+        "s_cbranch_scc0 6f\n\t"
+        // hit
+        "v_add_f32_e64 %[t], %[ww], %[w0]\n\t"
+        "v_cndmask_b32_e64 %[w0], %[w0], %[t], %[h0]\n\t"
+        "v_add_f32_e64 %[t], %[ww], %[w1]\n\t"
+        "v_cndmask_b32_e64 %[w1], %[w1], %[t], %[h1]\n\t"
+        "s_and_b64 %[h0], %[h0], %[qm0]\n\t"
+        "s_and_b64 %[h1], %[h1], %[qm1]\n\t"
+        "s_or_b64 %[any], %[h0], %[h1]\n\t"
+        "s_cbranch_scc1 8f\n\t"
+        "s_cmp_lg_u64 %[mask], 0\n\t"
+        "s_cbranch_scc1 5b\n\t"
+        "s_branch 9f\n"
+        // the hit slot was queued: it leaves the queue
+        "8:\n\t"
+        "s_andn2_b64 %[qm0], %[qm0], %[h0]\n\t"
+        "s_andn2_b64 %[qm1], %[qm1], %[h1]\n\t"
+        "s_cmp_eq_u64 %[h0], 0\n\t"
+        "s_cbranch_scc1 81f\n\t"
+        "s_ff1_i32_b64 %[p], %[h0]\n\t"
+        "v_readlane_b32 %[nw], %[w0], %[p]\n\t"
+        "s_branch 82f\n"
+        "81:\n\t"
+        "s_ff1_i32_b64 %[p], %[h1]\n\t"
+        "v_readlane_b32 %[nw], %[w1], %[p]\n"
+        "82:\n\t"
+        "s_min_u32 %[bound], %[bound], %[nw]\n\t"
+        "s_cmp_lg_u64 %[mask], 0\n\t"
+        "s_cbranch_scc1 5b\n\t"
+        "s_branch 9f\n"
+        // miss: the queue's front, past the slots that left it
+        "6:\n\t"
+        "s_cmp_ge_u32 %[head], 64\n\t"
+        "s_cbranch_scc1 7f\n\t"
+        "v_readlane_b32 %[slot], %[qs], %[head]\n\t"
+        "v_readlane_b32 %[wq], %[qw], %[head]\n\t"
+        "s_and_b32 %[p], %[slot], 63\n\t"
+        "s_cmp_ge_u32 %[slot], 64\n\t"
+        "s_cselect_b64 %[sel], %[qm1], %[qm0]\n\t"
+        "s_bitcmp1_b64 %[sel], %[p]\n\t"
+        "s_cbranch_scc1 61f\n\t"
+        "s_add_u32 %[head], %[head], 1\n\t"
+        "s_branch 6b\n"
+        "61:\n\t"
+        "s_cmp_lt_u32 %[wq], %[bound]\n\t"
+        "s_cbranch_scc0 7f\n\t"
+        "s_add_u32 %[head], %[head], 1\n\t"
+        "s_lshl_b64 %[sel], 1, %[p]\n\t"
+        "s_mov_b32 m0, %[p]\n\t"
+        "s_cmp_ge_u32 %[slot], 64\n\t"
+        "s_cbranch_scc1 65f\n\t"
+        "s_andn2_b64 %[qm0], %[qm0], %[sel]\n\t"
+        "v_writelane_b32 %[k0], %[kk], m0\n\t"
+        "v_add_f32_e64 %[t], %[ww], %[w0]\n\t"
+        "v_cndmask_b32_e64 %[w0], %[w0], %[t], %[sel]\n\t"
+        "s_branch 66f\n"
+        "65:\n\t"
+        "s_andn2_b64 %[qm1], %[qm1], %[sel]\n\t"
+        "v_writelane_b32 %[k1], %[kk], m0\n\t"
+        "v_add_f32_e64 %[t], %[ww], %[w1]\n\t"
+        "v_cndmask_b32_e64 %[w1], %[w1], %[t], %[sel]\n"
+        "66:\n\t"
+        "s_nop 0\n\t"
+        "v_readlane_b32 %[nw], %[t], %[p]\n\t"
+        "s_min_u32 %[bound], %[bound], %[nw]\n\t"
+        "s_cmp_lg_u64 %[mask], 0\n\t"
+        "s_cbranch_scc1 5b\n\t"
+        "s_branch 9f\n"
+        "7:\n\t"
+        "s_mov_b32 %[need], 1\n"
+        "9:\n\t"
+        "s_mov_b32 m0, %[m0s]"
+        : [k0] "+v"(s.key[0]), [k1] "+v"(s.key[1]), [w0] "+v"(s.wt[0]), [w1] "+v"(s.wt[1]),
+          [mask] "+s"(mask), [head] "+s"(head), [bound] "+s"(bound), [qm0] "+s"(qm0),
+          [qm1] "+s"(qm1), [need] "=&s"(need), [kk] "=&s"(kk), [ww] "=&s"(ww), [t] "=&v"(t),
+          [i] "=&s"(i), [p] "=&s"(p), [slot] "=&s"(slot), [wq] "=&s"(wq), [nw] "=&s"(nw),
+          [h0] "=&s"(h0), [h1] "=&s"(h1), [any] "=&s"(any), [sel] "=&s"(sel),
+          [m0s] "=&s"(m0_saved)
+        : [other] "v"(other), [alpha] "v"(alpha), [qw] "v"(q.qw), [qs] "v"(q.qs)
+        : "scc");
+    q.head = head;
+    q.bound = bound;
+    q.qm[0] = qm0;
+    q.qm[1] = qm1;
+  }
+};
+
 template <int FORM>
 __global__ void __launch_bounds__(256)
     probe(const int32_t *__restrict__ keys, const float *__restrict__ alphas, int n_items,
@@ -160,6 +387,8 @@ __global__ void __launch_bounds__(256)
   st.clear();
   RankSketch rs;
   rs.clear();
+  QueueSketch qsk;
+  qsk.clear();
   int32_t o = K[lane];
   float a = A[lane];
   const long long t0 = clock64();
@@ -179,14 +408,17 @@ __global__ void __launch_bounds__(256)
       st.feed_generic(mask, o, a);
     } else if constexpr (FORM == 2) {
       st.feed4(mask, o, a);
-    } else {
+    } else if constexpr (FORM == 3) {
       rs.feed(mask, o, a);
+    } else {
+      qsk.feed(mask, o, a);
     }
     o = o_next;
     a = a_next;
   }
   const long long t1 = clock64();
   if constexpr (FORM == 3) st = rs.s;
+  if constexpr (FORM == 4) st = qsk.s;
   const size_t base = static_cast<size_t>(w) * 128;
   out_key[base + lane] = st.key[0];
   out_key[base + kWave + lane] = st.key[1];
@@ -256,7 +488,7 @@ int main(int argc, char **argv) {
       std::memcpy(&al[i], &fbuf[2 * j + 1], 4);
     }
   }
-  constexpr int kForms = 4;
+  constexpr int kForms = 5;
   int32_t *dk, *ok[kForms];
   float *da, *ow[kForms];
   long long *cy;
@@ -283,6 +515,7 @@ int main(int argc, char **argv) {
       if (v == 1) probe<1><<<blocks, threads>>>(dk, da, n_items, ok[v], ow[v], cy);
       if (v == 2) probe<2><<<blocks, threads>>>(dk, da, n_items, ok[v], ow[v], cy);
       if (v == 3) probe<3><<<blocks, threads>>>(dk, da, n_items, ok[v], ow[v], cy);
+      if (v == 4) probe<4><<<blocks, threads>>>(dk, da, n_items, ok[v], ow[v], cy);
       CK(hipGetLastError());
       CK(hipEventRecord(e1));
       CK(hipEventSynchronize(e1));

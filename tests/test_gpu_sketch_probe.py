@@ -29,7 +29,7 @@ def test_sketch_forms_agree(args):
     assert out.returncode == 0, out.stdout + out.stderr
     agree = [line for line in out.stdout.splitlines() if "equals_form0" in line]
     assert agree == ["form=1 equals_form0=yes", "form=2 equals_form0=yes",
-                     "form=3 equals_form0=yes"]
+                     "form=3 equals_form0=yes", "form=4 equals_form0=yes"]
 
 
 ISSUE = Path(__file__).resolve().parent / "c" / "issue_probe"
